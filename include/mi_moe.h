@@ -1,0 +1,154 @@
+/*
+ * mi_moe.h -- C ABI of the MI355X fused-MoE expert library (libmimoe.so).
+ *
+ * Plain C: opaque handle, raw device pointers, sizes, an int status and a
+ * thread-local error string.  No torch types cross this boundary.  Each entry
+ * point names the reference interface it replaces (paths relative to the
+ * reference checkout).
+ *
+ * Streams are passed as void* (a hipStream_t; NULL = the default stream).
+ * All data pointers given to mi_moe_forward* must be device memory on the
+ * device the handle was created on.  Loader entry points accept either host
+ * or device memory (flag src_on_device).
+ */
+#ifndef MI_MOE_H
+#define MI_MOE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define MI_MOE_OK 0
+#define MI_MOE_EINVAL 1      /* bad argument / shape / dtype */
+#define MI_MOE_ENOTLOADED 2  /* forward before weights were stored */
+#define MI_MOE_EUNSUPPORTED 3
+#define MI_MOE_EHIP 4        /* a HIP runtime call failed */
+#define MI_MOE_EDEVICE 5     /* a kernel reported an error (e.g. bounded wait expired) */
+
+/* quant types: 0/1 as Int8-gemm/quant_traits.h:7-10 (Python ints 0/1); 2 is
+ * the W4A16 AWQ-style format of the absent NPU grouped_gemv path. */
+#define MI_MOE_Q8_0 0
+#define MI_MOE_Q4_0 1
+#define MI_MOE_W4A16 2
+
+/* dtype codes for activations and scales */
+#define MI_MOE_F16 0
+#define MI_MOE_BF16 1
+
+typedef struct mi_moe_handle mi_moe_handle;
+
+/* Thread-local message for the last non-zero status of this thread. */
+const char* mi_moe_last_error(void);
+
+/* Library/ABI version (major*10000 + minor*100 + patch). */
+int mi_moe_version(void);
+
+/* Create a handle for E experts, hidden H, intermediate I.
+ * Replaces MoEInfer::MoEInfer (Int8-gemm/moe_infer.cpp:18-75) and the
+ * TorchBind constructor MoEInfer(E,H,I,quant_type)
+ * (Int8-gemm/nanovllm_ops.cpp:28-30,353).  Requires H%32==0, I%32==0
+ * (W4A16: H%512==0, I%128==0).  Allocates nothing on the device until weights
+ * are stored; uses the current HIP device. */
+int mi_moe_create(int64_t num_experts, int64_t hidden, int64_t intermediate,
+                  int quant_type, mi_moe_handle** out);
+
+/* Free all device memory of the handle.  Replaces MoEInfer::~MoEInfer
+ * (Int8-gemm/moe_infer.cpp:77-84). */
+int mi_moe_destroy(mi_moe_handle* h);
+
+/* Shape / type queries (Int8-gemm/nanovllm_ops.cpp:376-391). */
+int mi_moe_get_info(const mi_moe_handle* h, int64_t* num_experts,
+                    int64_t* hidden, int64_t* intermediate, int* quant_type,
+                    int* scale_dtype);
+
+/* Pre-quantized Q8_0 / Q4_0 weights in the caller wire layout -> device
+ * layout owned by the handle.  Replaces MoEInfer::store_quantized_weights_repack
+ * (Int8-gemm/moe_infer.cpp:96-282), bound as store_quantized_repack
+ * (Int8-gemm/nanovllm_ops.cpp:366-371).
+ *   Q8_0: gate_up_qs int8 [E,2I,H], down_qs int8 [E,H,I]
+ *   Q4_0: gate_up_qs u32 [E,2I,H/8], down_qs u32 [E,H,I/8]
+ *   gate_up_d [E,2I,H/32], down_d [E,H,I/32]: fp16 or bf16 (scale_dtype). */
+int mi_moe_store_quantized(mi_moe_handle* h, const void* gate_up_qs,
+                           const void* gate_up_d, const void* down_qs,
+                           const void* down_d, int scale_dtype,
+                           int src_on_device, void* stream);
+
+/* Online Q8_0 weight quantization of one projection of one expert.
+ * Replaces MoEInfer::quantize_and_store_expert (Int8-gemm/moe_infer.cpp:
+ * 284-360; rule of quantize_weight_only, Int8-gemm/q8_gemm.cpp:197-260).
+ * proj: 0 = gate_proj [I,H], 1 = up_proj [I,H], 2 = down_proj [H,I];
+ * w_dtype: 0 fp16, 1 bf16, 2 fp32.  Q8_0 handles only (the reference rejects
+ * Q4_0, Int8-gemm/nanovllm_ops.cpp:359-363).  Scales are stored as fp16. */
+int mi_moe_quantize_and_store_expert(mi_moe_handle* h, int64_t expert,
+                                     int proj, const void* w, int w_dtype,
+                                     int src_on_device, void* stream);
+
+/* W4A16 AWQ-layout weights -> device layout.  No reference counterpart in
+ * the checkout: the W4A16 grouped_gemv loader lives in the absent
+ * sgl-kernel-npu submodule (README.md:19-30,152).  Layout: see formats.py /
+ * INTEGRATION.md (w13_* [E,H,2I/8],[E,H/g,2I/8],[E,H/g,2I]; w2_* [E,I,H/8],
+ * [E,I/g,H/8],[E,I/g,H]).  group must be 128. */
+int mi_moe_store_awq(mi_moe_handle* h, const int32_t* w13_qweight,
+                     const int32_t* w13_qzeros, const void* w13_scales,
+                     const int32_t* w2_qweight, const int32_t* w2_qzeros,
+                     const void* w2_scales, int64_t group, int scale_dtype,
+                     int src_on_device, void* stream);
+
+/* The fused MoE layer: y[t] = sum_k topk_w[t,k] * Expert_{ids[t,k]}(x[t]).
+ * Replaces MoEInfer::ExecuteFn (Int8-gemm/moe_infer.h:51-61) /
+ * execute_on_cpu_routed_from_pointers (Int8-gemm/moe_infer.cpp:430-456) and
+ * the op body of moe_forward (Int8-gemm/nanovllm_ops.cpp:219-236).
+ *   x, y      [T,H] fp16 or bf16 (act_dtype), device
+ *   topk_w    [T,K] fp32, device
+ *   topk_ids  [T,K] int32, device; ids outside [0,E) are dropped
+ *             (Int8-gemm/moe_common.cpp:158,175-181); a token with no valid
+ *             id gets y = 0.
+ * Stream-ordered and asynchronous.  Calls that overlap on one handle race on
+ * its workspace (the reference is likewise not re-entrant). */
+int mi_moe_forward(mi_moe_handle* h, const void* x, void* y,
+                   const float* topk_w, const int32_t* topk_ids, int64_t T,
+                   int64_t K, int act_dtype, void* stream);
+
+/* Wall time of the last mi_moe_forward on the handle, in ms, measured with
+ * HIP events around its launches (synchronizes on the end event).
+ * Replaces MoEInfer::get_last_run_time_ms (Int8-gemm/moe_infer.h:23,
+ * Int8-gemm/moe_infer.cpp:439-455).  Returns a negative value if timing is
+ * off or no call was made. */
+double mi_moe_get_last_run_time_ms(mi_moe_handle* h);
+
+/* Enable (1) / disable (0) the per-call HIP-event timing (default 1). */
+int mi_moe_set_timing(mi_moe_handle* h, int enable);
+
+/* Stage A activation quantization alone: x [T,H] fp16/bf16 -> x_qs [T,H]
+ * int8, x_d [T,H/32] fp32, with the device block quantizer used inside the
+ * fused kernels.  Replaces Stage A of moe_forward_ptr_impl
+ * (Int8-gemm/q8_gemm.cpp:360-377; quantize_block_q8_0,
+ * Int8-gemm/gemm_kernels.cpp:25-58). */
+int mi_moe_quantize_act_q8_0(const void* x, int act_dtype, int64_t T,
+                             int64_t H, int8_t* x_qs, float* x_d, void* stream);
+
+/* Routing alone: ids [T,K] -> counts [E], starts [E+1], token_map [T*K]
+ * (token id per expert-sorted position; entries past starts[E] unspecified),
+ * scatter [T*K] (position or -1).  Replaces preprocess_moe_routing
+ * (Int8-gemm/moe_common.cpp:146-216); any top_k >= 1 is accepted. */
+int mi_moe_route(const int32_t* topk_ids, int64_t T, int64_t K, int64_t E,
+                 int32_t* counts, int32_t* starts, int32_t* token_map,
+                 int32_t* scatter, void* stream);
+
+/* Per-32-block int32 dot products of the handle's stored weights against
+ * quantized activations, computed by the device block-dot routine of the
+ * fused kernels: isum[m][n][kb] for expert e, proj 0 = gate_up [2I rows, K=H],
+ * 1 = down [H rows, K=I]; a_qs [M,K] int8 device; isum [M,N,K/32] int32
+ * device.  Q8_0 / Q4_0 handles only.  Exposes the inner product of
+ * gemm_q{8,4}_0_microkernel (Int8-gemm/gemm_kernels.cpp:102-133,262-309) for
+ * bit-exact checking. */
+int mi_moe_block_dots(mi_moe_handle* h, int64_t expert, int proj,
+                      const int8_t* a_qs, int64_t M, int32_t* isum,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,396 @@
+// capi.hip -- the C ABI of libmimoe.so (include/mi_moe.h): handle lifetime,
+// weight ingestion (wire layout -> device tile layout), the fused forward,
+// and the standalone routing / quantization entry points.
+//
+// Host-side counterpart of MoEInfer (Int8-gemm/moe_infer.{h,cpp}) and the op
+// body of moe_forward (Int8-gemm/nanovllm_ops.cpp:219-236).  No exceptions
+// cross the ABI: every entry point returns a status and records a message
+// readable with mi_moe_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "mi_moe.h"
+#include "mi_moe_device.hpp"
+#include "mi_moe_internal.hpp"
+
+#define MI_API extern "C" __attribute__((visibility("default")))
+
+namespace mimoe {
+// kernels / launchers defined in the other translation units
+hipError_t launch_route_global(const int32_t*, int, int, int, const RouteGlobal&, hipStream_t);
+hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*, hipStream_t);
+hipError_t launch_w4a16_fused(const W4Args&, int, int, int, hipStream_t);
+size_t w4a16_lds_bytes(const W4Args&);
+int w4a16_max_blocks_per_cu(int, int, size_t);
+hipError_t launch_awq_repack(const int32_t*, const int32_t*, const uint16_t*, void*, uint16_t*,
+                             uint16_t*, int, int, int, int, int, int, hipStream_t);
+}  // namespace mimoe
+
+using namespace mimoe;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIPCHK(expr)                                                                   \
+  do {                                                                                 \
+    hipError_t _e = (expr);                                                            \
+    if (_e != hipSuccess)                                                              \
+      return fail(MI_MOE_EHIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), \
+                  __FILE__, __LINE__);                                                 \
+  } while (0)
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  hipError_t alloc(size_t b) {
+    release();
+    if (b == 0) b = 256;
+    hipError_t e = hipMalloc(&p, b);
+    if (e == hipSuccess) bytes = b;
+    return e;
+  }
+};
+
+// Scoped temporary device copy of a caller buffer (host or device source).
+struct Staged {
+  const void* ptr = nullptr;
+  DevBuf own;
+  hipError_t stage(const void* src, size_t bytes, int on_device, hipStream_t st) {
+    if (on_device) { ptr = src; return hipSuccess; }
+    hipError_t e = own.alloc(bytes);
+    if (e != hipSuccess) return e;
+    e = hipMemcpyAsync(own.p, src, bytes, hipMemcpyHostToDevice, st);
+    ptr = own.p;
+    return e;
+  }
+  ~Staged() { own.release(); }
+};
+
+}  // namespace
+
+struct mi_moe_handle {
+  int64_t E = 0, H = 0, I = 0;
+  int quant = 0;
+  int scale_dtype = 0;
+  int group = 128;
+  int device = 0;
+  int num_cu = 0;
+  bool loaded = false;
+  bool timing = true;
+  bool timed_once = false;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // weights (device layout)
+  DevBuf w13, w13_s, w13_z, w2, w2_s, w2_z;
+  // workspace
+  int64_t cap_T = 0, cap_n = 0;
+  DevBuf ctl, done1, cnt2, act, eout, r_counts, r_starts, r_active, r_tok, r_scat, r_U;
+  int occ_cache[2][2] = {{0, 0}, {0, 0}};
+  size_t occ_lds[2][2] = {{0, 0}, {0, 0}};
+};
+
+namespace {
+
+int check_handle(const mi_moe_handle* h) {
+  if (!h) return fail(MI_MOE_EINVAL, "null handle");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(MI_MOE_EHIP, "hipGetDevice failed");
+  if (dev != h->device)
+    return fail(MI_MOE_EINVAL, "current HIP device %d differs from the handle's device %d", dev,
+                h->device);
+  return MI_MOE_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
+  if (h->ctl.p == nullptr) {
+    HIPCHK(h->ctl.alloc(CTL_WORDS * sizeof(uint32_t)));
+    HIPCHK(h->done1.alloc((size_t)h->E * sizeof(uint32_t)));
+    HIPCHK(h->r_counts.alloc((size_t)h->E * sizeof(int32_t)));
+    HIPCHK(h->r_starts.alloc((size_t)(h->E + 1) * sizeof(int32_t)));
+    HIPCHK(h->r_active.alloc((size_t)h->E * sizeof(int32_t)));
+    HIPCHK(h->r_U.alloc(sizeof(int32_t)));
+    HIPCHK(hipMemsetAsync(h->ctl.p, 0, h->ctl.bytes, st));
+    HIPCHK(hipMemsetAsync(h->done1.p, 0, h->done1.bytes, st));
+  }
+  if (T <= h->cap_T && n <= h->cap_n) return MI_MOE_OK;
+  int64_t capT = h->cap_T ? h->cap_T : 16;
+  while (capT < T) capT *= 2;
+  int64_t capn = h->cap_n ? h->cap_n : 128;
+  while (capn < n) capn *= 2;
+  // buffers may be in use by queued work on this stream
+  HIPCHK(hipStreamSynchronize(st));
+  const int64_t NI2 = h->H / 64;
+  HIPCHK(h->cnt2.alloc((size_t)capT * NI2 * sizeof(uint32_t)));
+  HIPCHK(hipMemsetAsync(h->cnt2.p, 0, h->cnt2.bytes, st));
+  HIPCHK(h->act.alloc((size_t)capn * h->I * 2));
+  HIPCHK(h->eout.alloc((size_t)capn * h->H * sizeof(float)));
+  HIPCHK(h->r_tok.alloc((size_t)capn * sizeof(int32_t)));
+  HIPCHK(h->r_scat.alloc((size_t)capn * sizeof(int32_t)));
+  h->cap_T = capT;
+  h->cap_n = capn;
+  return MI_MOE_OK;
+}
+
+RouteGlobal route_view(mi_moe_handle* h) {
+  RouteGlobal rg;
+  rg.counts = (int32_t*)h->r_counts.p;
+  rg.starts = (int32_t*)h->r_starts.p;
+  rg.active = (int32_t*)h->r_active.p;
+  rg.tok = (int32_t*)h->r_tok.p;
+  rg.scat = (int32_t*)h->r_scat.p;
+  rg.U = (int32_t*)h->r_U.p;
+  return rg;
+}
+
+int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, const int32_t* ids,
+                  int64_t T, int64_t K, int act, hipStream_t st) {
+  const int64_t n = T * K;
+  int rc = ensure_workspace(h, T, n, st);
+  if (rc) return rc;
+  W4Args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = (const uint16_t*)x;
+  a.y = (uint16_t*)y;
+  a.tw = tw;
+  a.ids = ids;
+  a.T = (int)T; a.K = (int)K; a.E = (int)h->E; a.H = (int)h->H; a.I = (int)h->I; a.n = (int)n;
+  a.route_global = n > kRouteLdsMax;
+  a.rg = route_view(h);
+  a.w13 = h->w13.p; a.w13_s = (const uint16_t*)h->w13_s.p; a.w13_z = (const uint16_t*)h->w13_z.p;
+  a.w2 = h->w2.p; a.w2_s = (const uint16_t*)h->w2_s.p; a.w2_z = (const uint16_t*)h->w2_z.p;
+  a.ctl = (uint32_t*)h->ctl.p;
+  a.done1 = (uint32_t*)h->done1.p;
+  a.cnt2 = (uint32_t*)h->cnt2.p;
+  a.act = (uint16_t*)h->act.p;
+  a.eout = (float*)h->eout.p;
+  if (a.route_global) {
+    if (h->E > 512) return fail(MI_MOE_EUNSUPPORTED, "more than 512 experts with T*K > %d", kRouteLdsMax);
+    HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.rg, st));
+  }
+  const int64_t NI1 = h->I / 16, NI2 = h->H / 64;
+  const int64_t max_items = (n < h->E ? n : h->E) * (NI1 + NI2);
+  const size_t lds = w4a16_lds_bytes(a);
+  const int sc = h->scale_dtype;
+  if (h->occ_lds[act][sc] != lds) {
+    h->occ_cache[act][sc] = w4a16_max_blocks_per_cu(act, sc, lds);
+    h->occ_lds[act][sc] = lds;
+  }
+  int64_t grid = (int64_t)h->num_cu * h->occ_cache[act][sc];
+  if (grid > max_items) grid = max_items;
+  if (grid < 1) grid = 1;
+  HIPCHK(launch_w4a16_fused(a, act, sc, (int)grid, st));
+  return MI_MOE_OK;
+}
+
+}  // namespace
+
+// ====================================================================== ABI
+MI_API const char* mi_moe_last_error(void) { return g_err.c_str(); }
+
+MI_API int mi_moe_version(void) { return 100; }
+
+MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe_handle** out) {
+  if (!out) return fail(MI_MOE_EINVAL, "out is null");
+  *out = nullptr;
+  if (E <= 0 || H <= 0 || I <= 0) return fail(MI_MOE_EINVAL, "E, H, I must be positive");
+  if (quant_type < 0 || quant_type > 2) return fail(MI_MOE_EINVAL, "quant_type must be 0, 1 or 2");
+  if (H % 32 != 0) return fail(MI_MOE_EINVAL, "hidden_size must be multiple of 32");
+  if (I % 32 != 0) return fail(MI_MOE_EINVAL, "intermediate_size must be multiple of 32");
+  if (quant_type == MI_MOE_W4A16 && (H % 512 != 0 || I % 128 != 0))
+    return fail(MI_MOE_EINVAL, "W4A16 needs hidden_size %% 512 == 0 and intermediate_size %% 128 == 0");
+  if (E > 512) return fail(MI_MOE_EUNSUPPORTED, "at most 512 experts");
+  mi_moe_handle* h = new (std::nothrow) mi_moe_handle();
+  if (!h) return fail(MI_MOE_EINVAL, "out of host memory");
+  h->E = E; h->H = H; h->I = I; h->quant = quant_type;
+  if (hipGetDevice(&h->device) != hipSuccess ||
+      hipDeviceGetAttribute(&h->num_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess ||
+      hipEventCreate(&h->ev0) != hipSuccess || hipEventCreate(&h->ev1) != hipSuccess) {
+    delete h;
+    return fail(MI_MOE_EHIP, "HIP device query / event creation failed");
+  }
+  *out = h;
+  return MI_MOE_OK;
+}
+
+MI_API int mi_moe_destroy(mi_moe_handle* h) {
+  if (!h) return MI_MOE_OK;
+  (void)hipDeviceSynchronize();
+  DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z, &h->ctl,
+                    &h->done1, &h->cnt2, &h->act, &h->eout, &h->r_counts, &h->r_starts,
+                    &h->r_active, &h->r_tok, &h->r_scat, &h->r_U};
+  for (DevBuf* b : bufs) b->release();
+  if (h->ev0) (void)hipEventDestroy(h->ev0);
+  if (h->ev1) (void)hipEventDestroy(h->ev1);
+  delete h;
+  return MI_MOE_OK;
+}
+
+MI_API int mi_moe_get_info(const mi_moe_handle* h, int64_t* E, int64_t* H, int64_t* I, int* quant,
+                           int* scale_dtype) {
+  if (!h) return fail(MI_MOE_EINVAL, "null handle");
+  if (E) *E = h->E;
+  if (H) *H = h->H;
+  if (I) *I = h->I;
+  if (quant) *quant = h->quant;
+  if (scale_dtype) *scale_dtype = h->scale_dtype;
+  return MI_MOE_OK;
+}
+
+MI_API int mi_moe_set_timing(mi_moe_handle* h, int enable) {
+  if (!h) return fail(MI_MOE_EINVAL, "null handle");
+  h->timing = enable != 0;
+  return MI_MOE_OK;
+}
+
+MI_API double mi_moe_get_last_run_time_ms(mi_moe_handle* h) {
+  if (!h || !h->timing || !h->timed_once) return -1.0;
+  if (hipEventSynchronize(h->ev1) != hipSuccess) return -1.0;
+  float ms = 0.0f;
+  if (hipEventElapsedTime(&ms, h->ev0, h->ev1) != hipSuccess) return -1.0;
+  return (double)ms;
+}
+
+MI_API int mi_moe_store_awq(mi_moe_handle* h, const int32_t* w13_q, const int32_t* w13_z,
+                            const void* w13_s, const int32_t* w2_q, const int32_t* w2_z,
+                            const void* w2_s, int64_t group, int scale_dtype, int src_on_device,
+                            void* stream) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  if (h->quant != MI_MOE_W4A16) return fail(MI_MOE_EINVAL, "store_awq needs a W4A16 handle (quant_type 2)");
+  if (group != 128) return fail(MI_MOE_EUNSUPPORTED, "W4A16 group size %lld unsupported (128 only)", (long long)group);
+  if (scale_dtype != MI_MOE_F16 && scale_dtype != MI_MOE_BF16) return fail(MI_MOE_EINVAL, "scale dtype must be fp16 or bf16");
+  if (!w13_q || !w13_z || !w13_s || !w2_q || !w2_z || !w2_s) return fail(MI_MOE_EINVAL, "null weight pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t E = h->E, H = h->H, I = h->I, N13 = 2 * I;
+  const size_t q13 = (size_t)E * H * (N13 / 8) * 4, z13 = (size_t)E * (H / 128) * (N13 / 8) * 4,
+               s13 = (size_t)E * (H / 128) * N13 * 2;
+  const size_t q2 = (size_t)E * I * (H / 8) * 4, z2 = (size_t)E * (I / 128) * (H / 8) * 4,
+               s2 = (size_t)E * (I / 128) * H * 2;
+  Staged a, b, c, d, e, f;
+  HIPCHK(a.stage(w13_q, q13, src_on_device, st));
+  HIPCHK(b.stage(w13_z, z13, src_on_device, st));
+  HIPCHK(c.stage(w13_s, s13, src_on_device, st));
+  HIPCHK(d.stage(w2_q, q2, src_on_device, st));
+  HIPCHK(e.stage(w2_z, z2, src_on_device, st));
+  HIPCHK(f.stage(w2_s, s2, src_on_device, st));
+  const int64_t NT13 = 2 * (I / 16), G1 = H / 128, NT2 = H / 16, G2 = I / 128;
+  HIPCHK(h->w13.alloc((size_t)E * NT13 * G1 * 1024));
+  HIPCHK(h->w13_s.alloc((size_t)E * NT13 * G1 * 16 * 2));
+  HIPCHK(h->w13_z.alloc((size_t)E * NT13 * G1 * 4 * 2));
+  HIPCHK(h->w2.alloc((size_t)E * NT2 * G2 * 1024));
+  HIPCHK(h->w2_s.alloc((size_t)E * NT2 * G2 * 16 * 2));
+  HIPCHK(h->w2_z.alloc((size_t)E * NT2 * G2 * 4 * 2));
+  HIPCHK(launch_awq_repack((const int32_t*)a.ptr, (const int32_t*)b.ptr, (const uint16_t*)c.ptr,
+                           h->w13.p, (uint16_t*)h->w13_s.p, (uint16_t*)h->w13_z.p, (int)E, (int)H,
+                           (int)N13, (int)NT13, 1, (int)I, st));
+  HIPCHK(launch_awq_repack((const int32_t*)d.ptr, (const int32_t*)e.ptr, (const uint16_t*)f.ptr,
+                           h->w2.p, (uint16_t*)h->w2_s.p, (uint16_t*)h->w2_z.p, (int)E, (int)I,
+                           (int)H, (int)NT2, 0, (int)I, st));
+  HIPCHK(hipStreamSynchronize(st));
+  h->scale_dtype = scale_dtype;
+  h->group = (int)group;
+  h->loaded = true;
+  return MI_MOE_OK;
+}
+
+MI_API int mi_moe_store_quantized(mi_moe_handle* h, const void* gate_up_qs, const void* gate_up_d,
+                                  const void* down_qs, const void* down_d, int scale_dtype,
+                                  int src_on_device, void* stream) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  (void)gate_up_qs; (void)gate_up_d; (void)down_qs; (void)down_d; (void)scale_dtype;
+  (void)src_on_device; (void)stream;
+  return fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 device path not built yet");
+}
+
+MI_API int mi_moe_quantize_and_store_expert(mi_moe_handle* h, int64_t expert, int proj,
+                                            const void* w, int w_dtype, int src_on_device,
+                                            void* stream) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  (void)expert; (void)proj; (void)w; (void)w_dtype; (void)src_on_device; (void)stream;
+  return fail(MI_MOE_EUNSUPPORTED, "Q8_0 online quantization not built yet");
+}
+
+MI_API int mi_moe_block_dots(mi_moe_handle* h, int64_t expert, int proj, const int8_t* a_qs,
+                             int64_t M, int32_t* isum, void* stream) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  (void)expert; (void)proj; (void)a_qs; (void)M; (void)isum; (void)stream;
+  return fail(MI_MOE_EUNSUPPORTED, "block dots need a Q8_0/Q4_0 handle (not built yet)");
+}
+
+MI_API int mi_moe_forward(mi_moe_handle* h, const void* x, void* y, const float* topk_w,
+                          const int32_t* topk_ids, int64_t T, int64_t K, int act_dtype,
+                          void* stream) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  if (!h->loaded) return fail(MI_MOE_ENOTLOADED, "weights not stored");
+  if (act_dtype != MI_MOE_F16 && act_dtype != MI_MOE_BF16)
+    return fail(MI_MOE_EINVAL, "hidden dtype must be fp16 or bf16");
+  if (T < 0 || K < 1 || K > 64) return fail(MI_MOE_EINVAL, "bad T=%lld / top_k=%lld", (long long)T, (long long)K);
+  if (T == 0) return MI_MOE_OK;
+  if ((int64_t)T * K > (int64_t)1 << 24) return fail(MI_MOE_EINVAL, "T*top_k too large");
+  if (!x || !y || !topk_w || !topk_ids) return fail(MI_MOE_EINVAL, "null data pointer");
+  if (!aligned16(x) || !aligned16(y)) return fail(MI_MOE_EINVAL, "hidden/out must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (h->timing) HIPCHK(hipEventRecord(h->ev0, st));
+  if (h->quant == MI_MOE_W4A16) rc = forward_w4a16(h, x, y, topk_w, topk_ids, T, K, act_dtype, st);
+  else rc = fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 device path not built yet");
+  if (rc) return rc;
+  if (h->timing) {
+    HIPCHK(hipEventRecord(h->ev1, st));
+    h->timed_once = true;
+  }
+  return MI_MOE_OK;
+}
+
+MI_API int mi_moe_quantize_act_q8_0(const void* x, int act_dtype, int64_t T, int64_t H,
+                                    int8_t* x_qs, float* x_d, void* stream) {
+  if (act_dtype != MI_MOE_F16 && act_dtype != MI_MOE_BF16) return fail(MI_MOE_EINVAL, "dtype must be fp16 or bf16");
+  if (T < 0 || H <= 0 || H % 32) return fail(MI_MOE_EINVAL, "H must be a positive multiple of 32");
+  if (T == 0) return MI_MOE_OK;
+  if (!x || !x_qs || !x_d) return fail(MI_MOE_EINVAL, "null pointer");
+  if (!aligned16(x) || !aligned16(x_qs)) return fail(MI_MOE_EINVAL, "x and x_qs must be 16-byte aligned");
+  HIPCHK(launch_quant_act(x, act_dtype, T, H, x_qs, x_d, (hipStream_t)stream));
+  return MI_MOE_OK;
+}
+
+MI_API int mi_moe_route(const int32_t* ids, int64_t T, int64_t K, int64_t E, int32_t* counts,
+                        int32_t* starts, int32_t* token_map, int32_t* scatter, void* stream) {
+  if (T < 0 || K < 1 || E < 1) return fail(MI_MOE_EINVAL, "bad T/K/E");
+  if (E > 512) return fail(MI_MOE_EUNSUPPORTED, "at most 512 experts");
+  if (T * K > ((int64_t)1 << 24)) return fail(MI_MOE_EINVAL, "T*K too large");
+  if (!ids || !counts || !starts || !token_map || !scatter) return fail(MI_MOE_EINVAL, "null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  DevBuf active, U;
+  HIPCHK(active.alloc((size_t)E * sizeof(int32_t)));
+  HIPCHK(U.alloc(sizeof(int32_t)));
+  RouteGlobal rg{counts, starts, (int32_t*)active.p, token_map, scatter, (int32_t*)U.p};
+  HIPCHK(launch_route_global(ids, (int)(T * K), (int)K, (int)E, rg, st));
+  HIPCHK(hipStreamSynchronize(st));
+  active.release();
+  U.release();
+  return MI_MOE_OK;
+}

@@ -1,0 +1,185 @@
+// common_kernels.hip -- routing and Q8_0 activation quantization kernels used
+// by every weight format (and exposed alone through the C ABI for checking).
+#pragma clang fp contract(off)
+#include "mi_moe_device.hpp"
+#include "mi_moe_internal.hpp"
+
+namespace mimoe {
+
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / kWave;
+
+// Global routing (one workgroup of 1024 threads): the stable counting sort of
+// preprocess_moe_routing (Int8-gemm/moe_common.cpp:146-216) for any number of
+// (t,k) pairs.  Each wave owns a contiguous segment of ids; per-wave
+// per-expert counts are prefix-summed across waves so the ranks stay in
+// (t,k) order.  LDS: (kRouteWaves + 1) * E ints (E <= 512).
+__global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
+    const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
+    int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out) {
+  extern __shared__ int lds[];
+  int* counts = lds;            // [E]
+  int* cw = lds + E;            // [kRouteWaves][E]
+  __shared__ int s_U;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int e = tid; e < E; e += kRouteThreads) counts[e] = 0;
+  for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) cw[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += kRouteThreads) {
+    const int e = ids[i];
+    if ((unsigned)e < (unsigned)E) atomicAdd(&counts[e], 1);
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    const int per = (E + kWave - 1) / kWave;
+    const int base = lane * per;
+    int s = 0, a = 0;
+    for (int i = 0; i < per; ++i) {
+      const int e = base + i;
+      if (e < E) { const int c = counts[e]; s += c; a += (c > 0); }
+    }
+    int sinc = s, ainc = a;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int v = __shfl_up(sinc, off);
+      const int w = __shfl_up(ainc, off);
+      if (lane >= off) { sinc += v; ainc += w; }
+    }
+    int sx = sinc - s, ax = ainc - a;
+    for (int i = 0; i < per; ++i) {
+      const int e = base + i;
+      if (e < E) {
+        const int c = counts[e];
+        counts_out[e] = c;
+        starts_out[e] = sx;
+        counts[e] = sx;  // counts[] now holds starts
+        if (c > 0) active_out[ax++] = e;
+        sx += c;
+      }
+    }
+    if (lane == kWave - 1) { starts_out[E] = sinc; *U_out = ainc; s_U = ainc; }
+  }
+  __syncthreads();
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  const int seg = ((n + kRouteWaves - 1) / kRouteWaves + kWave - 1) / kWave * kWave;
+  const int lo = wave * seg, hi = min(n, lo + seg);
+  int* mine = cw + wave * E;
+  // pass A: per-wave counts
+  for (int b0 = lo; b0 < hi; b0 += kWave) {
+    const int i = b0 + lane;
+    const int e = (i < hi) ? ids[i] : -1;
+    const bool valid = (i < hi) && ((unsigned)e < (unsigned)E);
+    uint64_t m = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const uint64_t bb = __ballot(valid && ((e >> bit) & 1));
+      m &= ((e >> bit) & 1) ? bb : ~bb;
+    }
+    if (valid && __ffsll((long long)m) - 1 == lane) mine[e] += __popcll(m);
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // prefix over waves, seeded with starts
+  for (int e = tid; e < E; e += kRouteThreads) {
+    int run = counts[e];
+    for (int w = 0; w < kRouteWaves; ++w) {
+      const int c = cw[w * E + e];
+      cw[w * E + e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  // pass B: ranks
+  for (int b0 = lo; b0 < hi; b0 += kWave) {
+    const int i = b0 + lane;
+    const int e = (i < hi) ? ids[i] : -1;
+    const bool valid = (i < hi) && ((unsigned)e < (unsigned)E);
+    uint64_t m = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const uint64_t bb = __ballot(valid && ((e >> bit) & 1));
+      m &= ((e >> bit) & 1) ? bb : ~bb;
+    }
+    int add = 0;
+    if (valid) {
+      const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+      const int pos = mine[e] + __popcll(m & lt);
+      scat[i] = pos;
+      tok[pos] = i / K;
+      if (__ffsll((long long)m) - 1 == lane) add = __popcll(m);
+    } else if (i < hi) {
+      scat[i] = -1;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (add) mine[e] += add;
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const RouteGlobal& rg,
+                               hipStream_t st) {
+  const size_t lds = (size_t)(kRouteWaves + 1) * E * sizeof(int);
+  hipLaunchKernelGGL(route_global_kernel, dim3(1), dim3(kRouteThreads), lds, st, ids, n, K, E,
+                     rg.counts, rg.starts, rg.active, rg.tok, rg.scat, rg.U);
+  return hipGetLastError();
+}
+
+// Stage A: one thread per 32-element block.  quantize_block_q8_0 rule
+// (Int8-gemm/gemm_kernels.cpp:37-57): amax, d = amax/127, id = 1/d (0 if d==0),
+// q = sat8(RNE(x*id)); d stays fp32 (Int8-gemm/q8_gemm.cpp:371-375).
+template <int ACT>
+__global__ void quant_act_q8_0_kernel(const uint16_t* __restrict__ x, int64_t nblk,
+                                      int8_t* __restrict__ qs, float* __restrict__ d) {
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
+       b += (int64_t)gridDim.x * blockDim.x) {
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(x + b * 32);
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4_t w = src[c];
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        v[8 * c + 2 * h] = to_f32<ACT>(ws[h] & 0xffffu);
+        v[8 * c + 2 * h + 1] = to_f32<ACT>(ws[h] >> 16);
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const float av = __builtin_fabsf(v[j]);
+      amax = av > amax ? av : amax;
+    }
+    const float dd = amax / 127.0f;
+    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+    uint32_t packed[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        word |= ((uint32_t)(uint8_t)q8_round(v[4 * w + h] * id)) << (8 * h);
+      packed[w] = word;
+    }
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(qs + b * 32);
+    dst[0] = u32x4_t{packed[0], packed[1], packed[2], packed[3]};
+    dst[1] = u32x4_t{packed[4], packed[5], packed[6], packed[7]};
+    d[b] = dd;
+  }
+}
+
+hipError_t launch_quant_act(const void* x, int act, int64_t T, int64_t H, int8_t* qs, float* d,
+                            hipStream_t st) {
+  const int64_t nblk = T * (H / 32);
+  if (nblk == 0) return hipSuccess;
+  int64_t grid = (nblk + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  if (act == 1)
+    hipLaunchKernelGGL(quant_act_q8_0_kernel<1>, dim3((unsigned)grid), dim3(256), 0, st,
+                       (const uint16_t*)x, nblk, qs, d);
+  else
+    hipLaunchKernelGGL(quant_act_q8_0_kernel<0>, dim3((unsigned)grid), dim3(256), 0, st,
+                       (const uint16_t*)x, nblk, qs, d);
+  return hipGetLastError();
+}
+
+}  // namespace mimoe

@@ -1,0 +1,87 @@
+"""Build recipes for the native parts of the package (run on the CPU host).
+
+* ``libmimoe.so`` -- the HIP kernels + C ABI (include/mi_moe.h), built with
+  hipcc for gfx950 only.  No torch dependency.
+* ``libnanovllm_shim.so`` -- the TorchBind / dispatcher registration
+  (``torch.classes.nanovllm.MoEInfer``, ``torch.ops.nanovllm.moe_forward``),
+  linked against libmimoe.so.
+
+Both land next to this file so they travel with the source tree.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG_DIR)                    # moe-ascend-opt_amd/
+CSRC = os.path.join(ROOT, "csrc")
+INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
+LIB = os.path.join(PKG_DIR, "libmimoe.so")
+SHIM = os.path.join(PKG_DIR, "libnanovllm_shim.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+HIP_SOURCES = ["capi.hip", "common_kernels.hip", "w4a16.hip", "qint.hip"]
+# Packed-FP32 instructions are disabled for all device code (only scalar /
+# float2 source is written; the compiler must not form v_pk_* fp32 ops).
+NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        sys.stderr.write(out + "\n")
+        raise RuntimeError("build step failed: " + " ".join(cmd[:3]) + " ...")
+    return out
+
+
+def build_lib(verbose: bool = False) -> str:
+    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+           "-fvisibility=hidden", f"-I{INCLUDE}", f"-I{CSRC}", *NO_PK_FP32, *srcs, "-o", tmp]
+    out = _run(cmd)
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def _torch_paths():
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    inc = [os.path.join(tdir, "include"), os.path.join(tdir, "include", "torch", "csrc", "api", "include")]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return inc, os.path.join(tdir, "lib"), abi
+
+
+def build_shim(verbose: bool = False) -> str:
+    inc, libdir, abi = _torch_paths()
+    tmp = SHIM + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-DTORCH_EXTENSION_NAME=nanovllm_shim",
+           *[f"-I{p}" for p in inc], "-I/opt/rocm/include", f"-I{INCLUDE}",
+           os.path.join(CSRC, "nanovllm_shim.cpp"), "-o", tmp,
+           f"-L{libdir}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+           f"-L{PKG_DIR}", "-lmimoe",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}", "-Wl,--no-as-needed"]
+    out = _run(cmd)
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, SHIM)
+    return SHIM
+
+
+def build_all(verbose: bool = False):
+    build_lib(verbose)
+    build_shim(verbose)
+    return LIB, SHIM
+
+
+if __name__ == "__main__":
+    build_all(verbose=True)
+    print("built", LIB, SHIM)
