@@ -23,9 +23,7 @@ namespace mimoe {
 // kernels / launchers defined in the other translation units
 hipError_t launch_route_global(const int32_t*, int, int, int, const RouteGlobal&, hipStream_t);
 hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*, hipStream_t);
-hipError_t launch_w4a16_fused(const W4Args&, int, int, int, hipStream_t);
-size_t w4a16_lds_bytes(const W4Args&);
-int w4a16_max_blocks_per_cu(int, int, size_t);
+hipError_t launch_w4a16(const W4Args&, int, int, int, int, hipStream_t);
 hipError_t launch_awq_repack(const int32_t*, const int32_t*, const uint16_t*, void*, uint16_t*,
                              uint16_t*, int, int, int, int, int, int, hipStream_t);
 }  // namespace mimoe
@@ -103,9 +101,7 @@ struct mi_moe_handle {
   DevBuf w13, w13_s, w13_z, w2, w2_s, w2_z;
   // workspace
   int64_t cap_T = 0, cap_n = 0;
-  DevBuf ctl, done1, cnt2, act, eout, r_counts, r_starts, r_active, r_tok, r_scat, r_U;
-  int occ_cache[2][2] = {{0, 0}, {0, 0}};
-  size_t occ_lds[2][2] = {{0, 0}, {0, 0}};
+  DevBuf cnt2, act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U;
 };
 
 namespace {
@@ -123,15 +119,11 @@ int check_handle(const mi_moe_handle* h) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
-  if (h->ctl.p == nullptr) {
-    HIPCHK(h->ctl.alloc(CTL_WORDS * sizeof(uint32_t)));
-    HIPCHK(h->done1.alloc((size_t)h->E * sizeof(uint32_t)));
+  if (h->r_U.p == nullptr) {
     HIPCHK(h->r_counts.alloc((size_t)h->E * sizeof(int32_t)));
     HIPCHK(h->r_starts.alloc((size_t)(h->E + 1) * sizeof(int32_t)));
     HIPCHK(h->r_active.alloc((size_t)h->E * sizeof(int32_t)));
     HIPCHK(h->r_U.alloc(sizeof(int32_t)));
-    HIPCHK(hipMemsetAsync(h->ctl.p, 0, h->ctl.bytes, st));
-    HIPCHK(hipMemsetAsync(h->done1.p, 0, h->done1.bytes, st));
   }
   if (T <= h->cap_T && n <= h->cap_n) return MI_MOE_OK;
   int64_t capT = h->cap_T ? h->cap_T : 16;
@@ -144,12 +136,29 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
   HIPCHK(h->cnt2.alloc((size_t)capT * NI2 * sizeof(uint32_t)));
   HIPCHK(hipMemsetAsync(h->cnt2.p, 0, h->cnt2.bytes, st));
   HIPCHK(h->act.alloc((size_t)capn * h->I * 2));
+  HIPCHK(h->act_d.alloc((size_t)capn * (h->I / 32) * sizeof(float)));
   HIPCHK(h->eout.alloc((size_t)capn * h->H * sizeof(float)));
   HIPCHK(h->r_tok.alloc((size_t)capn * sizeof(int32_t)));
   HIPCHK(h->r_scat.alloc((size_t)capn * sizeof(int32_t)));
   h->cap_T = capT;
   h->cap_n = capn;
   return MI_MOE_OK;
+}
+
+RouteGlobal route_view(mi_moe_handle* h);
+
+void fill_sched(mi_moe_handle* h, SchedArgs& c, const void* x, void* y, const float* tw,
+                const int32_t* ids, int64_t T, int64_t K) {
+  c.x = (const uint16_t*)x;
+  c.y = (uint16_t*)y;
+  c.tw = tw;
+  c.ids = ids;
+  c.T = (int)T; c.K = (int)K; c.E = (int)h->E; c.H = (int)h->H; c.I = (int)h->I;
+  c.n = (int)(T * K);
+  c.route_global = c.n > kRouteLdsMax;
+  c.rg = route_view(h);
+  c.cnt2 = (uint32_t*)h->cnt2.p;
+  c.eout = (float*)h->eout.p;
 }
 
 RouteGlobal route_view(mi_moe_handle* h) {
@@ -170,36 +179,14 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
   if (rc) return rc;
   W4Args a;
   std::memset(&a, 0, sizeof(a));
-  a.x = (const uint16_t*)x;
-  a.y = (uint16_t*)y;
-  a.tw = tw;
-  a.ids = ids;
-  a.T = (int)T; a.K = (int)K; a.E = (int)h->E; a.H = (int)h->H; a.I = (int)h->I; a.n = (int)n;
-  a.route_global = n > kRouteLdsMax;
-  a.rg = route_view(h);
+  fill_sched(h, a.c, x, y, tw, ids, T, K);
   a.w13 = h->w13.p; a.w13_s = (const uint16_t*)h->w13_s.p; a.w13_z = (const uint16_t*)h->w13_z.p;
   a.w2 = h->w2.p; a.w2_s = (const uint16_t*)h->w2_s.p; a.w2_z = (const uint16_t*)h->w2_z.p;
-  a.ctl = (uint32_t*)h->ctl.p;
-  a.done1 = (uint32_t*)h->done1.p;
-  a.cnt2 = (uint32_t*)h->cnt2.p;
   a.act = (uint16_t*)h->act.p;
-  a.eout = (float*)h->eout.p;
-  if (a.route_global) {
-    if (h->E > 512) return fail(MI_MOE_EUNSUPPORTED, "more than 512 experts with T*K > %d", kRouteLdsMax);
-    HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.rg, st));
-  }
-  const int64_t NI1 = h->I / 16, NI2 = h->H / 64;
-  const int64_t max_items = (n < h->E ? n : h->E) * (NI1 + NI2);
-  const size_t lds = w4a16_lds_bytes(a);
-  const int sc = h->scale_dtype;
-  if (h->occ_lds[act][sc] != lds) {
-    h->occ_cache[act][sc] = w4a16_max_blocks_per_cu(act, sc, lds);
-    h->occ_lds[act][sc] = lds;
-  }
-  int64_t grid = (int64_t)h->num_cu * h->occ_cache[act][sc];
-  if (grid > max_items) grid = max_items;
-  if (grid < 1) grid = 1;
-  HIPCHK(launch_w4a16_fused(a, act, sc, (int)grid, st));
+  if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st));
+  const int64_t umax = n < h->E ? n : h->E;
+  const int64_t grid1 = umax * (h->I / 16), grid2 = umax * (h->H / 64);
+  HIPCHK(launch_w4a16(a, act, h->scale_dtype, (int)grid1, (int)grid2, st));
   return MI_MOE_OK;
 }
 
@@ -236,8 +223,8 @@ MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe
 MI_API int mi_moe_destroy(mi_moe_handle* h) {
   if (!h) return MI_MOE_OK;
   (void)hipDeviceSynchronize();
-  DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z, &h->ctl,
-                    &h->done1, &h->cnt2, &h->act, &h->eout, &h->r_counts, &h->r_starts,
+  DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z,
+                    &h->cnt2, &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
                     &h->r_active, &h->r_tok, &h->r_scat, &h->r_U};
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
@@ -382,8 +369,15 @@ MI_API int mi_moe_route(const int32_t* ids, int64_t T, int64_t K, int64_t E, int
   if (T < 0 || K < 1 || E < 1) return fail(MI_MOE_EINVAL, "bad T/K/E");
   if (E > 512) return fail(MI_MOE_EUNSUPPORTED, "at most 512 experts");
   if (T * K > ((int64_t)1 << 24)) return fail(MI_MOE_EINVAL, "T*K too large");
-  if (!ids || !counts || !starts || !token_map || !scatter) return fail(MI_MOE_EINVAL, "null pointer");
+  if (!counts || !starts) return fail(MI_MOE_EINVAL, "null pointer");
   hipStream_t st = (hipStream_t)stream;
+  if (T == 0) {  // nothing routed: empty histogram
+    HIPCHK(hipMemsetAsync(counts, 0, (size_t)E * sizeof(int32_t), st));
+    HIPCHK(hipMemsetAsync(starts, 0, (size_t)(E + 1) * sizeof(int32_t), st));
+    HIPCHK(hipStreamSynchronize(st));
+    return MI_MOE_OK;
+  }
+  if (!ids || !token_map || !scatter) return fail(MI_MOE_EINVAL, "null pointer");
   DevBuf active, U;
   HIPCHK(active.alloc((size_t)E * sizeof(int32_t)));
   HIPCHK(U.alloc(sizeof(int32_t)));

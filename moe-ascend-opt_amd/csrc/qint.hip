@@ -1,0 +1,491 @@
+// qint.hip -- Q8_0 / Q4_0 weights with Q8_0-quantized activations: the
+// reference CPU algorithm (moe_forward_ptr_impl, Int8-gemm/q8_gemm.cpp:
+// 276-646) on gfx950.
+//
+// Arithmetic per output (m, n), as the reference micro-kernels
+// (Int8-gemm/gemm_kernels.cpp:102-179, 254-358):
+//     isum_kb = sum_{i<32} a_q * w_q            (exact int32, v_dot4_i32_i8)
+//     c      += ((float)isum_kb * dw[n,kb]) * da[m,kb]
+// with w_q = int8 (Q8_0) or nibble-8 (Q4_0: dot with the unsigned nibble,
+// then subtract 8 * sum(a_q) of the block).  Each lane owns one weight row;
+// the four waves of a workgroup split the k blocks and their fp32 partial
+// sums are added in wave order.
+//
+// Device weight layout (lane-per-row tiles of 64 rows, one 32-element block
+// per step):
+//   gate_up: [E][I/32 slices][H/32 blocks][chunk][64 lanes][16 B]; lane r<32
+//            is gate row 32s+r, lane r>=32 is up row I+32s+r-32, so SiLU*mul
+//            pairs lanes r and r+32 and one slice yields one Q8_0 block of
+//            the intermediate.
+//   down:    [E][H/64][I/32 blocks][chunk][64 lanes][16 B]; lane r = row 64hb+r
+//   Q8_0: 2 chunks (bytes 0-15, 16-31 of the row's block); Q4_0: 1 chunk of
+//   4 words, word d holding elements 8d+m (low nibble of byte m) and 8d+4+m
+//   (high nibble), so (w & 0x0F0F0F0F) and (w >> 4 & 0x0F0F0F0F) line up with
+//   activation dwords 2d and 2d+1.
+//   scales: [tile][block][64 lanes] (fp16 or bf16 bits).
+#pragma clang fp contract(off)
+#include "mi_moe_device.hpp"
+#include "mi_moe_internal.hpp"
+#include "mi_moe_sched.hpp"
+
+namespace mimoe {
+
+template <int QT>
+struct QFmt {
+  static constexpr int chunks = QT == 0 ? 2 : 1;
+  static constexpr int block_bytes = chunks * 64 * 16;  // one (tile, block)
+};
+
+template <int QT>
+__device__ __forceinline__ void unpack_w(const u32x4_t w0, const u32x4_t w1, int (&wd)[8]) {
+  if constexpr (QT == 0) {
+    wd[0] = (int)w0.x; wd[1] = (int)w0.y; wd[2] = (int)w0.z; wd[3] = (int)w0.w;
+    wd[4] = (int)w1.x; wd[5] = (int)w1.y; wd[6] = (int)w1.z; wd[7] = (int)w1.w;
+  } else {
+    const uint32_t w[4] = {w0.x, w0.y, w0.z, w0.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      wd[2 * d] = (int)(w[d] & 0x0f0f0f0fu);
+      wd[2 * d + 1] = (int)((w[d] >> 4) & 0x0f0f0f0fu);
+    }
+  }
+}
+
+// Exact int32 dot of one 32-element block (Int8-gemm/gemm_kernels.cpp:
+// 109-133 for Q8_0, 262-309 for Q4_0).
+template <int QT>
+__device__ __forceinline__ int block_isum(const int (&wd)[8], const int* xv, int xsum) {
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_sdot4(wd[j], xv[j], s, false);
+  if constexpr (QT == 1) s -= 8 * xsum;
+  return s;
+}
+
+// Q8_0 quantization of 32 fp32 values (quantize_block_q8_0,
+// Int8-gemm/gemm_kernels.cpp:25-58): returns d, writes 32 bytes, sum of q.
+__device__ __forceinline__ float quant_block_q8_0(const float (&v)[32], int8_t* dst, int* qsum) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const float av = __builtin_fabsf(v[j]);
+    amax = av > amax ? av : amax;
+  }
+  const float d = amax / 127.0f;
+  const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  int s = 0;
+  uint32_t packed[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int8_t q = q8_round(v[4 * w + h] * id);
+      s += q;
+      word |= ((uint32_t)(uint8_t)q) << (8 * h);
+    }
+    packed[w] = word;
+  }
+  u32x4_t* o = reinterpret_cast<u32x4_t*>(dst);
+  o[0] = u32x4_t{packed[0], packed[1], packed[2], packed[3]};
+  o[1] = u32x4_t{packed[4], packed[5], packed[6], packed[7]};
+  *qsum = s;
+  return d;
+}
+
+// Dot of this lane's weight row against the staged activations for k blocks
+// [kb0, kb1), accumulating into acc[c] for the cntp staged tokens.
+template <int QT, int SC>
+__device__ __forceinline__ void rows_dot(const char* wtile, const uint16_t* stile, int lane, int kb0,
+                                         int kb1, const int8_t* xq, const float* xd, const int* xs,
+                                         int K, int KB, int cntp, float (&acc)[kQTokPerPass]) {
+  constexpr int BB = QFmt<QT>::block_bytes;
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const char* wp = wtile + (size_t)kb * BB + lane * 16;
+    const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(wp);
+    u32x4_t w1 = {0, 0, 0, 0};
+    if constexpr (QT == 0) w1 = *reinterpret_cast<const u32x4_t*>(wp + 1024);
+    const float dw = to_f32<SC>(stile[kb * 64 + lane]);
+    int wd[8];
+    unpack_w<QT>(w0, w1, wd);
+#pragma unroll
+    for (int cc = 0; cc < kQTokPerPass; ++cc) {
+      if (cc >= cntp) break;
+      const int* xv = reinterpret_cast<const int*>(xq + cc * K + kb * 32);
+      const int s = block_isum<QT>(wd, xv, QT == 1 ? xs[cc * KB + kb] : 0);
+      const float t1 = (float)s * dw;
+      const float t2 = t1 * xd[cc * KB + kb];
+      acc[cc] = acc[cc] + t2;
+    }
+  }
+}
+
+struct QLds {
+  int8_t* xq;   // [kQTokPerPass][Kmax]
+  float* xd;    // [kQTokPerPass][KBmax]
+  int* xs;      // [kQTokPerPass][KBmax]
+  float* red;   // [4][kQTokPerPass][64]
+  int* route;
+};
+
+__device__ __forceinline__ QLds carve(unsigned char* smem, int Kmax) {
+  QLds L;
+  const int KBmax = Kmax / 32;
+  L.xq = reinterpret_cast<int8_t*>(smem);
+  L.xd = reinterpret_cast<float*>(smem + kQTokPerPass * Kmax);
+  L.xs = reinterpret_cast<int*>(L.xd + kQTokPerPass * KBmax);
+  L.red = reinterpret_cast<float*>(L.xs + kQTokPerPass * KBmax);
+  L.route = reinterpret_cast<int*>(L.red + 4 * kQTokPerPass * 64);
+  return L;
+}
+
+// ---------------------------------------------------------------- phase 1
+template <int QT, int ACT, int SC>
+__device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, const QLds& L) {
+  const SchedArgs& c = a.c;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int e = rv.active[ui];
+  const int p0 = rv.starts[e], cnt = rv.starts[e + 1] - p0;
+  const int KB = c.H / 32, S = c.I / 32;
+  const int kb0 = KB * wave / 4, kb1 = KB * (wave + 1) / 4;
+  const size_t tile = (size_t)e * S + sl;
+  const char* wtile = (const char*)a.w13 + tile * KB * QFmt<QT>::block_bytes;
+  const uint16_t* stile = a.w13_d + tile * KB * 64;
+
+  for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
+    const int cntp = min(kQTokPerPass, cnt - cb0);
+    // Stage A for the staged tokens (Int8-gemm/q8_gemm.cpp:360-377)
+    for (int idx = tid; idx < cntp * KB; idx += kBlock) {
+      const int cc = idx / KB, kb = idx - cc * KB;
+      const int t = rv.tok[p0 + cb0 + cc];
+      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(c.x + (size_t)t * c.H + kb * 32);
+      float v[32];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const u32x4_t w = src[q4];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          v[8 * q4 + 2 * h] = to_f32<ACT>(ws[h] & 0xffffu);
+          v[8 * q4 + 2 * h + 1] = to_f32<ACT>(ws[h] >> 16);
+        }
+      }
+      int qs;
+      L.xd[cc * KB + kb] = quant_block_q8_0(v, L.xq + cc * c.H + kb * 32, &qs);
+      L.xs[cc * KB + kb] = qs;
+    }
+    __syncthreads();
+    float acc[kQTokPerPass];
+#pragma unroll
+    for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
+    rows_dot<QT, SC>(wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.H, KB, cntp, acc);
+#pragma unroll
+    for (int cc = 0; cc < kQTokPerPass; ++cc)
+      if (cc < cntp) L.red[(wave * kQTokPerPass + cc) * 64 + lane] = acc[cc];
+    __syncthreads();
+    {
+      // thread t -> token cc = t/32, intermediate column r = t%32 of the slice
+      const int cc = tid >> 5, r = tid & 31;
+      const int ccl = cc < cntp ? cc : 0;
+      float g = L.red[(0 * kQTokPerPass + ccl) * 64 + r];
+      float u = L.red[(0 * kQTokPerPass + ccl) * 64 + r + 32];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        g = g + L.red[(w * kQTokPerPass + ccl) * 64 + r];
+        u = u + L.red[(w * kQTokPerPass + ccl) * 64 + r + 32];
+      }
+      const float act = silu_mul(g, u);
+      // Q8_0 re-quantization of the 32-value intermediate block
+      // (pack_A_q8_0, Int8-gemm/gemm_kernels.cpp:394-425)
+      float amax = __builtin_fabsf(act);
+#pragma unroll
+      for (int m = 16; m >= 1; m >>= 1) {
+        const float o = __shfl_xor(amax, m, 32);
+        amax = o > amax ? o : amax;
+      }
+      const float d = amax / 127.0f;
+      const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+      const int8_t q = q8_round(act * id);
+      if (cc < cntp) {
+        const size_t row = (size_t)(p0 + cb0 + cc);
+        a.act_q[row * c.I + 32 * sl + r] = q;
+        if (r == 0) a.act_d[row * S + sl] = d;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- phase 2
+template <int QT, int ACT, int SC>
+__device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, const QLds& L,
+                         int* s_list, int* s_nlist) {
+  const SchedArgs& c = a.c;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int e = rv.active[ui];
+  const int p0 = rv.starts[e], cnt = rv.starts[e + 1] - p0;
+  const int KB2 = c.I / 32, HB = c.H / 64;
+  const int kb0 = KB2 * wave / 4, kb1 = KB2 * (wave + 1) / 4;
+  const size_t tile = (size_t)e * HB + hb;
+  const char* wtile = (const char*)a.w2 + tile * KB2 * QFmt<QT>::block_bytes;
+  const uint16_t* stile = a.w2_d + tile * KB2 * 64;
+
+  for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
+    const int cntp = min(kQTokPerPass, cnt - cb0);
+    for (int idx = tid; idx < cntp * KB2; idx += kBlock) {
+      const int cc = idx / KB2, kb = idx - cc * KB2;
+      const size_t row = (size_t)(p0 + cb0 + cc);
+      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.act_q + row * c.I + kb * 32);
+      const u32x4_t q0 = src[0], q1 = src[1];
+      u32x4_t* dst = reinterpret_cast<u32x4_t*>(L.xq + cc * c.I + kb * 32);
+      dst[0] = q0;
+      dst[1] = q1;
+      if constexpr (QT == 1) {
+        const uint32_t ws[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        int s = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_sdot4((int)ws[j], 0x01010101, s, false);
+        L.xs[cc * KB2 + kb] = s;
+      }
+      L.xd[cc * KB2 + kb] = a.act_d[row * KB2 + kb];
+    }
+    __syncthreads();
+    float acc[kQTokPerPass];
+#pragma unroll
+    for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
+    rows_dot<QT, SC>(wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.I, KB2, cntp, acc);
+#pragma unroll
+    for (int cc = 0; cc < kQTokPerPass; ++cc)
+      if (cc < cntp) L.red[(wave * kQTokPerPass + cc) * 64 + lane] = acc[cc];
+    __syncthreads();
+    for (int cc = wave; cc < cntp; cc += 4) {
+      float v = L.red[(0 * kQTokPerPass + cc) * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) v = v + L.red[(w * kQTokPerPass + cc) * 64 + lane];
+      c.eout[(size_t)(p0 + cb0 + cc) * c.H + 64 * hb + lane] = v;
+    }
+    __syncthreads();
+  }
+  combine_hb<ACT>(c, rv, p0, cnt, hb, s_list, s_nlist);
+}
+
+// ---------------------------------------------------------------- kernels
+__host__ __device__ inline size_t q_stage_bytes(int Kmax) {
+  return (size_t)kQTokPerPass * Kmax + (size_t)kQTokPerPass * (Kmax / 32) * 8 +
+         (size_t)4 * kQTokPerPass * 64 * 4;
+}
+
+template <int QT, int ACT, int SC>
+__global__ __launch_bounds__(kBlock) void q_phase1_kernel(QArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_U;
+  const QLds L = carve(smem, a.c.H);
+  const RouteView rv = sched_route(a.c, L.route, &s_U);
+  if (blockIdx.x == 0) zero_unrouted<ACT>(a.c, rv);
+  const int S = a.c.I / 32;
+  const int ui = blockIdx.x / S;
+  if (ui >= rv.U) return;
+  q_phase1<QT, ACT, SC>(a, rv, ui, blockIdx.x % S, L);
+}
+
+template <int QT, int ACT, int SC>
+__global__ __launch_bounds__(kBlock) void q_phase2_kernel(QArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_U, s_nlist;
+  __shared__ int s_list[kBlock];
+  const QLds L = carve(smem, a.c.I);
+  const RouteView rv = sched_route(a.c, L.route, &s_U);
+  const int HB = a.c.H / 64;
+  const int ui = blockIdx.x / HB;
+  if (ui >= rv.U) return;
+  q_phase2<QT, ACT, SC>(a, rv, ui, blockIdx.x % HB, L, s_list, &s_nlist);
+}
+
+template <int QT, int ACT, int SC>
+static hipError_t launch_q_t(const QArgs& a, int grid1, int grid2, hipStream_t st) {
+  const size_t route = a.c.route_global ? 0 : route_lds_ints(a.c.E, a.c.n) * sizeof(int);
+  hipLaunchKernelGGL((q_phase1_kernel<QT, ACT, SC>), dim3(grid1), dim3(kBlock),
+                     q_stage_bytes(a.c.H) + route, st, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((q_phase2_kernel<QT, ACT, SC>), dim3(grid2), dim3(kBlock),
+                     q_stage_bytes(a.c.I) + route, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_qint(const QArgs& a, int qt, int act, int sc, int grid1, int grid2, hipStream_t st) {
+  if (qt == 0) {
+    if (act == 1) return sc == 1 ? launch_q_t<0, 1, 1>(a, grid1, grid2, st) : launch_q_t<0, 1, 0>(a, grid1, grid2, st);
+    return sc == 1 ? launch_q_t<0, 0, 1>(a, grid1, grid2, st) : launch_q_t<0, 0, 0>(a, grid1, grid2, st);
+  }
+  if (act == 1) return sc == 1 ? launch_q_t<1, 1, 1>(a, grid1, grid2, st) : launch_q_t<1, 1, 0>(a, grid1, grid2, st);
+  return sc == 1 ? launch_q_t<1, 0, 1>(a, grid1, grid2, st) : launch_q_t<1, 0, 0>(a, grid1, grid2, st);
+}
+
+// ---------------------------------------------------------------- weights
+// Tile coordinates of wire row `row` of projection proj (0 gate_up [2I rows],
+// 1 down [H rows]).
+__device__ __forceinline__ void row_to_tile(int proj, int row, int I, int& tile_in_e, int& lane) {
+  if (proj == 0) {
+    const int up = row >= I;
+    const int rr = up ? row - I : row;
+    tile_in_e = rr >> 5;
+    lane = (rr & 31) + 32 * up;
+  } else {
+    tile_in_e = row >> 6;
+    lane = row & 63;
+  }
+}
+
+// Q4_0 wire word (elements k..k+7 at nibbles 0..7) -> device word (byte m =
+// element m | element m+4 << 4).
+__device__ __forceinline__ uint32_t q4_to_dev(uint32_t w) {
+  uint32_t o = 0;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t lo = (w >> (4 * m)) & 0xfu, hi = (w >> (4 * (m + 4))) & 0xfu;
+    o |= (lo | (hi << 4)) << (8 * m);
+  }
+  return o;
+}
+
+// One thread per (e, row, block): wire -> device tile, plus its scale.
+template <int QT>
+__global__ void q_repack_kernel(const void* __restrict__ qs, const uint16_t* __restrict__ d,
+                                void* __restrict__ wdst, uint16_t* __restrict__ ddst, int E,
+                                int rows, int K, int proj, int I) {
+  const int KB = K / 32;
+  const size_t total = (size_t)E * rows * KB;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const int kb = idx % KB;
+    const size_t er = idx / KB;
+    const int row = er % rows;
+    const int e = (int)(er / rows);
+    int ti, lane;
+    row_to_tile(proj, row, I, ti, lane);
+    const int tiles_per_e = proj == 0 ? I / 32 : rows / 64;
+    const size_t tile = (size_t)e * tiles_per_e + ti;
+    char* dst = (char*)wdst + (tile * KB + kb) * QFmt<QT>::block_bytes + lane * 16;
+    if constexpr (QT == 0) {
+      const u32x4_t* src = reinterpret_cast<const u32x4_t*>((const int8_t*)qs + er * K + kb * 32);
+      *reinterpret_cast<u32x4_t*>(dst) = src[0];
+      *reinterpret_cast<u32x4_t*>(dst + 1024) = src[1];
+    } else {
+      const u32x4_t src = *reinterpret_cast<const u32x4_t*>((const uint32_t*)qs + er * (K / 8) + kb * 4);
+      *reinterpret_cast<u32x4_t*>(dst) =
+          u32x4_t{q4_to_dev(src.x), q4_to_dev(src.y), q4_to_dev(src.z), q4_to_dev(src.w)};
+    }
+    ddst[(tile * KB + kb) * 64 + lane] = d[er * KB + kb];
+  }
+}
+
+hipError_t launch_q_repack(int qt, const void* qs, const uint16_t* d, void* wdst, uint16_t* ddst,
+                           int E, int rows, int K, int proj, int I, hipStream_t st) {
+  const size_t total = (size_t)E * rows * (K / 32);
+  int grid = (int)((total + 255) / 256);
+  if (grid > 65536) grid = 65536;
+  if (qt == 0)
+    hipLaunchKernelGGL(q_repack_kernel<0>, dim3(grid), dim3(256), 0, st, qs, d, wdst, ddst, E, rows, K, proj, I);
+  else
+    hipLaunchKernelGGL(q_repack_kernel<1>, dim3(grid), dim3(256), 0, st, qs, d, wdst, ddst, E, rows, K, proj, I);
+  return hipGetLastError();
+}
+
+// Online Q8_0 weight quantization of one projection of one expert
+// (quantize_weight_only, Int8-gemm/q8_gemm.cpp:197-260): fp16 scale, q from
+// the fp32 reciprocal of the unrounded scale.  One thread per (row, block).
+template <int WDT>  // 0 fp16, 1 bf16, 2 fp32
+__global__ void q8_online_quant_kernel(const void* __restrict__ w, int N, int K, int e, int proj,
+                                       int I, int row_offset, void* __restrict__ wdst,
+                                       uint16_t* __restrict__ ddst) {
+  const int KB = K / 32;
+  const size_t total = (size_t)N * KB;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const int kb = idx % KB;
+    const int n = (int)(idx / KB);
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const size_t off = (size_t)n * K + kb * 32 + j;
+      if constexpr (WDT == 2) v[j] = ((const float*)w)[off];
+      else v[j] = to_f32<WDT>(((const uint16_t*)w)[off]);
+    }
+    int ti, lane;
+    const int row = n + row_offset;
+    row_to_tile(proj == 2 ? 1 : 0, row, I, ti, lane);
+    const int tiles_per_e = proj == 2 ? N / 64 : I / 32;
+    const size_t tile = (size_t)e * tiles_per_e + ti;
+    int8_t q[32];
+    int qs;
+    const float d = quant_block_q8_0(v, q, &qs);
+    char* dst = (char*)wdst + (tile * KB + kb) * QFmt<0>::block_bytes + lane * 16;
+    *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(q);
+    *reinterpret_cast<u32x4_t*>(dst + 1024) = *reinterpret_cast<const u32x4_t*>(q + 16);
+    ddst[(tile * KB + kb) * 64 + lane] = f32_to_f16(d);
+  }
+}
+
+hipError_t launch_q8_online_quant(const void* w, int wdt, int N, int K, int e, int proj, int I,
+                                  void* wdst, uint16_t* ddst, hipStream_t st) {
+  const size_t total = (size_t)N * (K / 32);
+  int grid = (int)((total + 255) / 256);
+  if (grid > 65536) grid = 65536;
+  const int row_offset = proj == 1 ? I : 0;
+  if (wdt == 2)
+    hipLaunchKernelGGL(q8_online_quant_kernel<2>, dim3(grid), dim3(256), 0, st, w, N, K, e, proj, I, row_offset, wdst, ddst);
+  else if (wdt == 1)
+    hipLaunchKernelGGL(q8_online_quant_kernel<1>, dim3(grid), dim3(256), 0, st, w, N, K, e, proj, I, row_offset, wdst, ddst);
+  else
+    hipLaunchKernelGGL(q8_online_quant_kernel<0>, dim3(grid), dim3(256), 0, st, w, N, K, e, proj, I, row_offset, wdst, ddst);
+  return hipGetLastError();
+}
+
+// Per-block int32 dots of stored weights (same unpack + block_isum as the
+// fused kernels): isum[m][n][kb].  One thread per (m, n, kb).
+template <int QT>
+__global__ void q_block_dots_kernel(const void* __restrict__ wbase, const int8_t* __restrict__ a_qs,
+                                    int32_t* __restrict__ isum, int M, int N, int K, int e, int proj,
+                                    int I, int tiles_per_e) {
+  const int KB = K / 32;
+  const size_t total = (size_t)M * N * KB;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const int kb = idx % KB;
+    const size_t mn = idx / KB;
+    const int n = mn % N;
+    const int m = (int)(mn / N);
+    int ti, lane;
+    row_to_tile(proj, n, I, ti, lane);
+    const size_t tile = (size_t)e * tiles_per_e + ti;
+    const char* wp = (const char*)wbase + (tile * KB + kb) * QFmt<QT>::block_bytes + lane * 16;
+    const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(wp);
+    u32x4_t w1 = {0, 0, 0, 0};
+    if constexpr (QT == 0) w1 = *reinterpret_cast<const u32x4_t*>(wp + 1024);
+    int wd[8];
+    unpack_w<QT>(w0, w1, wd);
+    const int* xv = reinterpret_cast<const int*>(a_qs + (size_t)m * K + kb * 32);
+    int xsum = 0;
+    if constexpr (QT == 1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xsum = __builtin_amdgcn_sdot4(xv[j], 0x01010101, xsum, false);
+    }
+    isum[idx] = block_isum<QT>(wd, xv, xsum);
+  }
+}
+
+hipError_t launch_q_block_dots(int qt, const void* wbase, const int8_t* a_qs, int32_t* isum, int M,
+                               int N, int K, int e, int proj, int I, int tiles_per_e, hipStream_t st) {
+  const size_t total = (size_t)M * N * (K / 32);
+  if (total == 0) return hipSuccess;
+  int grid = (int)((total + 255) / 256);
+  if (grid > 65536) grid = 65536;
+  if (qt == 0)
+    hipLaunchKernelGGL(q_block_dots_kernel<0>, dim3(grid), dim3(256), 0, st, wbase, a_qs, isum, M, N, K, e, proj, I, tiles_per_e);
+  else
+    hipLaunchKernelGGL(q_block_dots_kernel<1>, dim3(grid), dim3(256), 0, st, wbase, a_qs, isum, M, N, K, e, proj, I, tiles_per_e);
+  return hipGetLastError();
+}
+
+}  // namespace mimoe

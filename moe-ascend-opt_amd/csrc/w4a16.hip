@@ -19,19 +19,16 @@
 // down tiles [expert][16-row tile][group].  Per-(tile, group) metadata:
 // 16 scales (2 B each) and 16 zero nibbles packed as four u16 (rows 4q..4q+3).
 //
-// Work decomposition (one persistent launch, tickets from an atomic counter):
-//   phase 1 item (expert, j): rows j*16.. of gate and up, all H; 4 waves split
-//     the groups; LDS reduction; SiLU*mul; write act[pos][16j..16j+15].
-//   phase 2 item (expert, hb): 64 rows of down (one 16-row tile per wave),
-//     all I; waits for the expert's phase-1 items (bounded spin), writes
-//     eout[pos][64hb..]; the last arriving expert of a token does the combine
-//     y[t] = cast(sum_k w[t,k] * eout[scatter[t,k]]) in k order
-//     (Int8-gemm/q8_gemm.cpp:593-641).
-// Tickets are taken in order, so every phase-1 item a phase-2 item waits on is
-// already held by a running workgroup that never waits: no deadlock.
+// Work decomposition: see mi_moe_sched.hpp (phase-1 launch: one workgroup
+// per (expert, 16-row slice j of I) computing rows j*16.. of gate and up over
+// all of H, the 4 waves splitting the groups, then an LDS reduction, SiLU*mul
+// and act[pos][16j..16j+15]; phase-2 launch: one workgroup per (expert, hb)
+// computing 64 rows of down (one 16-row tile per wave) over all of I, then
+// the counted combine).
 #pragma clang fp contract(off)
 #include "mi_moe_device.hpp"
 #include "mi_moe_internal.hpp"
+#include "mi_moe_sched.hpp"
 
 namespace mimoe {
 
@@ -91,27 +88,14 @@ __device__ __forceinline__ void fold(f32x4_t& acc, const f32x4_t G, const f32x4_
   acc.w = __builtin_fmaf(s[3], __builtin_fmaf(-c[3], X.w, G.w), acc.w);
 }
 
-struct RouteView {
-  const int* starts;
-  const int* active;
-  const int* tok;
-  const int* scat;
-  int U;
-};
-
-__device__ __forceinline__ int nvalid_of(const RouteView& rv, int t, int K) {
-  int c = 0;
-  for (int k = 0; k < K; ++k) c += rv.scat[t * K + k] >= 0;
-  return c;
-}
-
 // ---------------------------------------------------------------- phase 1
 template <int ACT, int SC>
 __device__ void w4_phase1(const W4Args& a, const RouteView& rv, int ui, int j, float* red) {
+  const SchedArgs& c = a.c;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   const int e = rv.active[ui];
   const int p0 = rv.starts[e], cnt = rv.starts[e + 1] - p0;
-  const int G1 = a.H >> 7, NI1 = a.I >> 4;
+  const int G1 = c.H >> 7, NI1 = c.I >> 4;
   const int gpw = G1 >> 2, g0 = wave * gpw;
   const size_t tile_g = ((size_t)e * NI1 + j) * 2, tile_u = tile_g + 1;
   const char* wg_base = (const char*)a.w13 + (tile_g * G1) * 1024 + lane * 16;
@@ -125,7 +109,7 @@ __device__ void w4_phase1(const W4Args& a, const RouteView& rv, int ui, int j, f
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int col = cb0 + 16 * b + r;
-      xoff[b] = (b < nb && col < cnt) ? rv.tok[p0 + col] * a.H : -1;
+      xoff[b] = (b < nb && col < cnt) ? rv.tok[p0 + col] * c.H : -1;
     }
     f32x4_t accg[4], accu[4];
 #pragma unroll
@@ -157,7 +141,7 @@ __device__ void w4_phase1(const W4Args& a, const RouteView& rv, int ui, int j, f
           if (b >= nb) break;
           u32x4_t B[4];
           if (xoff[b] >= 0) {
-            const uint16_t* xp = a.x + xoff[b] + 128 * g + 32 * q;
+            const uint16_t* xp = c.x + xoff[b] + 128 * g + 32 * q;
 #pragma unroll
             for (int i = 0; i < 4; ++i) B[i] = ldg16(xp + 8 * i);
           } else {
@@ -202,51 +186,28 @@ __device__ void w4_phase1(const W4Args& a, const RouteView& rv, int ui, int j, f
           const uint32_t h2 = from_f32<ACT>(silu_mul(g.z, u.z));
           const uint32_t h3 = from_f32<ACT>(silu_mul(g.w, u.w));
           u32x2_t pk = {h0 | (h1 << 16), h2 | (h3 << 16)};
-          *reinterpret_cast<u32x2_t*>(a.act + (size_t)(p0 + col) * a.I + 16 * j + 4 * q) = pk;
+          *reinterpret_cast<u32x2_t*>(a.act + (size_t)(p0 + col) * c.I + 16 * j + 4 * q) = pk;
         }
       }
     }
     __syncthreads();
   }
-  // every wave publishes its act stores (L2 write-back), then one arrival
-  fence_release();
-  __syncthreads();
-  if (tid == 0)
-    __hip_atomic_fetch_add(a.done1 + e, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- phase 2
 template <int ACT, int SC>
 __device__ void w4_phase2(const W4Args& a, const RouteView& rv, int ui, int hb, int* s_list,
                           int* s_nlist) {
+  const SchedArgs& c = a.c;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   const int e = rv.active[ui];
   const int p0 = rv.starts[e], cnt = rv.starts[e + 1] - p0;
-  const int G2 = a.I >> 7, NI1 = a.I >> 4, NI2 = a.H >> 6, NT = a.H >> 4;
+  const int G2 = c.I >> 7, NT = c.H >> 4;
   const int nt = 4 * hb + wave;
   const size_t tile = (size_t)e * NT + nt;
   const char* w_base = (const char*)a.w2 + (tile * G2) * 1024 + lane * 16;
   const u32x4_t ones = {W4Consts<ACT>::ones, W4Consts<ACT>::ones, W4Consts<ACT>::ones,
                         W4Consts<ACT>::ones};
-
-  // Issue the first weight loads before waiting on the expert's activations.
-  u32x4_t wpre[4];
-#pragma unroll
-  for (int gi = 0; gi < 4; ++gi)
-    if (gi < G2) wpre[gi] = ldg16(w_base + (size_t)gi * 1024);
-
-  if (tid == 0) {
-    uint32_t spins = 0;
-    while (ld_acquire_relaxed(a.done1 + e) < (uint32_t)NI1) {
-      __builtin_amdgcn_s_sleep(1);
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(a.ctl + CTL_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-  fence_acquire();
 
   for (int cb0 = 0; cb0 < cnt; cb0 += kColsPerPass) {
     const int nb = min(4, (cnt - cb0 + 15) >> 4);
@@ -254,7 +215,7 @@ __device__ void w4_phase2(const W4Args& a, const RouteView& rv, int ui, int hb, 
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int col = cb0 + 16 * b + r;
-      aoff[b] = (b < nb && col < cnt) ? (p0 + col) * a.I : -1;
+      aoff[b] = (b < nb && col < cnt) ? (p0 + col) * c.I : -1;
     }
     f32x4_t acc[4];
 #pragma unroll
@@ -263,15 +224,14 @@ __device__ void w4_phase2(const W4Args& a, const RouteView& rv, int ui, int hb, 
     for (int gc = 0; gc < G2; gc += 4) {
       u32x4_t wv[4];
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        if (gc + gi < G2) wv[gi] = (gc == 0 && cb0 == 0) ? wpre[gi] : ldg16(w_base + (size_t)(gc + gi) * 1024);
-      }
+      for (int gi = 0; gi < 4; ++gi)
+        if (gc + gi < G2) wv[gi] = ldg16(w_base + (size_t)(gc + gi) * 1024);
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi) {
         if (gc + gi >= G2) break;
         const int g = gc + gi;
-        float s[4], c[4];
-        load_meta<ACT, SC>(a.w2_s, a.w2_z, tile * G2 + g, q, s, c);
+        float s[4], cz[4];
+        load_meta<ACT, SC>(a.w2_s, a.w2_z, tile * G2 + g, q, s, cz);
         u32x4_t A[4];
         A[0] = deq4<ACT>(wv[gi].x); A[1] = deq4<ACT>(wv[gi].y);
         A[2] = deq4<ACT>(wv[gi].z); A[3] = deq4<ACT>(wv[gi].w);
@@ -293,7 +253,7 @@ __device__ void w4_phase2(const W4Args& a, const RouteView& rv, int ui, int hb, 
             X = mfma16<ACT>(ones, B[i], X);
             G = mfma16<ACT>(A[i], B[i], G);
           }
-          fold(acc[b], G, X, s, c);
+          fold(acc[b], G, X, s, cz);
         }
       }
     }
@@ -301,104 +261,38 @@ __device__ void w4_phase2(const W4Args& a, const RouteView& rv, int ui, int hb, 
     for (int b = 0; b < 4; ++b) {
       const int col = cb0 + 16 * b + r;
       if (b < nb && col < cnt)
-        *reinterpret_cast<f32x4_t*>(a.eout + (size_t)(p0 + col) * a.H + 16 * nt + 4 * q) = acc[b];
+        *reinterpret_cast<f32x4_t*>(c.eout + (size_t)(p0 + col) * c.H + 16 * nt + 4 * q) = acc[b];
     }
   }
-  fence_release();
-  __syncthreads();
-
-  // Combine: count arrivals per (token, hb); the last expert of a token sums
-  // eout over k in order and casts.
-  for (int c0 = 0; c0 < cnt; c0 += kBlock) {
-    if (tid == 0) *s_nlist = 0;
-    __syncthreads();
-    const int c = c0 + tid;
-    if (c < cnt) {
-      const int t = rv.tok[p0 + c];
-      const uint32_t old = __hip_atomic_fetch_add(a.cnt2 + (size_t)t * NI2 + hb, 1u,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((int)old + 1 == nvalid_of(rv, t, a.K)) s_list[atomicAdd(s_nlist, 1)] = t;
-    }
-    __syncthreads();
-    const int nl = *s_nlist;
-    if (nl > 0) {
-      fence_acquire();
-      for (int li = wave; li < nl; li += 4) {
-        const int t = s_list[li];
-        const int h = 64 * hb + lane;
-        float acc = 0.0f;
-        for (int k = 0; k < a.K; ++k) {
-          const int pos = rv.scat[t * a.K + k];
-          if (pos < 0) continue;
-          const float prod = a.tw[t * a.K + k] * a.eout[(size_t)pos * a.H + h];
-          acc = acc + prod;
-        }
-        a.y[(size_t)t * a.H + h] = from_f32<ACT>(acc);
-        if (lane == 0) a.cnt2[(size_t)t * NI2 + hb] = 0u;
-      }
-    }
-    __syncthreads();
-  }
+  combine_hb<ACT>(c, rv, p0, cnt, hb, s_list, s_nlist);
 }
 
-// ---------------------------------------------------------------- kernel
+// ---------------------------------------------------------------- kernels
+constexpr size_t kW4RedBytes = (size_t)4 * 2 * 4 * 64 * 4 * sizeof(float);  // 32 KiB
+
 template <int ACT, int SC>
-__global__ __launch_bounds__(kBlock) void w4a16_fused_kernel(W4Args a) {
+__global__ __launch_bounds__(kBlock) void w4a16_phase1_kernel(W4Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_ticket, s_U, s_nlist;
+  __shared__ int s_U;
+  float* red = reinterpret_cast<float*>(smem);
+  const RouteView rv = sched_route(a.c, reinterpret_cast<int*>(smem + kW4RedBytes), &s_U);
+  if (blockIdx.x == 0) zero_unrouted<ACT>(a.c, rv);
+  const int NI1 = a.c.I >> 4;
+  const int ui = blockIdx.x / NI1;
+  if (ui >= rv.U) return;  // uniform across the workgroup
+  w4_phase1<ACT, SC>(a, rv, ui, blockIdx.x % NI1, red);
+}
+
+template <int ACT, int SC>
+__global__ __launch_bounds__(kBlock) void w4a16_phase2_kernel(W4Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_U, s_nlist;
   __shared__ int s_list[kBlock];
-  float* red = reinterpret_cast<float*>(smem);                  // 32 KiB
-  int* rl = reinterpret_cast<int*>(smem + 4 * 2 * 4 * 64 * 4 * 4);
-  const int tid = threadIdx.x;
-
-  RouteView rv;
-  if (!a.route_global) {
-    int* counts = rl;
-    int* starts = counts + a.E;
-    int* active = starts + a.E + 1;
-    int* tok = active + a.E;
-    int* scat = tok + a.n;
-    route_lds(a.ids, a.n, a.K, a.E, counts, starts, active, tok, scat, &s_U);
-    rv.starts = starts; rv.active = active; rv.tok = tok; rv.scat = scat; rv.U = s_U;
-  } else {
-    rv.starts = a.rg.starts; rv.active = a.rg.active; rv.tok = a.rg.tok; rv.scat = a.rg.scat;
-    rv.U = *a.rg.U;
-  }
-  const int NI1 = a.I >> 4, NI2 = a.H >> 6;
-  const int total1 = rv.U * NI1, total = rv.U * (NI1 + NI2);
-
-  for (;;) {
-    if (tid == 0) s_ticket = (int)atomicAdd(a.ctl + CTL_TICKET, 1u);
-    __syncthreads();
-    const int tk = s_ticket;
-    __syncthreads();
-    if (tk == 0) {
-      // tokens without any valid expert id get y = 0 (Int8-gemm/q8_gemm.cpp:329-332, 599-611)
-      for (int t = tid >> 6; t < a.T; t += 4) {
-        if (nvalid_of(rv, t, a.K) == 0)
-          for (int h = tid & 63; h < a.H; h += 64) a.y[(size_t)t * a.H + h] = 0;
-      }
-    }
-    if (tk >= total) break;
-    if (tk < total1) {
-      w4_phase1<ACT, SC>(a, rv, tk / NI1, tk % NI1, red);
-    } else {
-      const int t2 = tk - total1;
-      w4_phase2<ACT, SC>(a, rv, t2 / NI2, t2 % NI2, s_list, &s_nlist);
-    }
-  }
-  // The last workgroup out resets the per-call counters for the next launch.
-  if (tid == 0) {
-    fence_release();
-    const uint32_t old = atomicAdd(a.ctl + CTL_EXIT, 1u);
-    if (old == gridDim.x - 1) {
-      fence_acquire();
-      for (int e = 0; e < a.E; ++e) a.done1[e] = 0u;
-      a.ctl[CTL_TICKET] = 0u;
-      a.ctl[CTL_EXIT] = 0u;
-      fence_release();
-    }
-  }
+  const RouteView rv = sched_route(a.c, reinterpret_cast<int*>(smem), &s_U);
+  const int NI2 = a.c.H >> 6;
+  const int ui = blockIdx.x / NI2;
+  if (ui >= rv.U) return;
+  w4_phase2<ACT, SC>(a, rv, ui, blockIdx.x % NI2, s_list, &s_nlist);
 }
 
 // ---------------------------------------------------------------- repack
@@ -473,36 +367,29 @@ __global__ void awq_repack_meta(const uint16_t* __restrict__ scales, const int32
 }
 
 // ---------------------------------------------------------------- launchers
-#define W4_INST(ACT, SC) template __global__ void w4a16_fused_kernel<ACT, SC>(W4Args);
+#define W4_INST(ACT, SC)                                                   \
+  template __global__ void w4a16_phase1_kernel<ACT, SC>(W4Args);          \
+  template __global__ void w4a16_phase2_kernel<ACT, SC>(W4Args);
 W4_INST(0, 0)
 W4_INST(0, 1)
 W4_INST(1, 0)
 W4_INST(1, 1)
 
-size_t w4a16_lds_bytes(const W4Args& a) {
-  size_t red = (size_t)4 * 2 * 4 * 64 * 4 * sizeof(float);
-  size_t route = a.route_global ? 0 : (size_t)(3 * a.E + 1 + 2 * a.n) * sizeof(int);
-  return red + route;
-}
-
-hipError_t launch_w4a16_fused(const W4Args& a, int act, int sc, int grid, hipStream_t st) {
-  const size_t lds = w4a16_lds_bytes(a);
-  if (act == 1 && sc == 1) hipLaunchKernelGGL((w4a16_fused_kernel<1, 1>), dim3(grid), dim3(kBlock), lds, st, a);
-  else if (act == 1) hipLaunchKernelGGL((w4a16_fused_kernel<1, 0>), dim3(grid), dim3(kBlock), lds, st, a);
-  else if (sc == 1) hipLaunchKernelGGL((w4a16_fused_kernel<0, 1>), dim3(grid), dim3(kBlock), lds, st, a);
-  else hipLaunchKernelGGL((w4a16_fused_kernel<0, 0>), dim3(grid), dim3(kBlock), lds, st, a);
+template <int ACT, int SC>
+static hipError_t launch_w4_t(const W4Args& a, int grid1, int grid2, hipStream_t st) {
+  const size_t route = a.c.route_global ? 0 : route_lds_ints(a.c.E, a.c.n) * sizeof(int);
+  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, SC>), dim3(grid1), dim3(kBlock), kW4RedBytes + route, st, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((w4a16_phase2_kernel<ACT, SC>), dim3(grid2), dim3(kBlock), route, st, a);
   return hipGetLastError();
 }
 
-int w4a16_max_blocks_per_cu(int act, int sc, size_t lds) {
-  int nb = 0;
-  hipError_t err;
-  if (act == 1 && sc == 1) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, w4a16_fused_kernel<1, 1>, kBlock, lds);
-  else if (act == 1) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, w4a16_fused_kernel<1, 0>, kBlock, lds);
-  else if (sc == 1) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, w4a16_fused_kernel<0, 1>, kBlock, lds);
-  else err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, w4a16_fused_kernel<0, 0>, kBlock, lds);
-  if (err != hipSuccess || nb < 1) nb = 1;
-  return nb;
+hipError_t launch_w4a16(const W4Args& a, int act, int sc, int grid1, int grid2, hipStream_t st) {
+  if (act == 1 && sc == 1) return launch_w4_t<1, 1>(a, grid1, grid2, st);
+  if (act == 1) return launch_w4_t<1, 0>(a, grid1, grid2, st);
+  if (sc == 1) return launch_w4_t<0, 1>(a, grid1, grid2, st);
+  return launch_w4_t<0, 0>(a, grid1, grid2, st);
 }
 
 hipError_t launch_awq_repack(const int32_t* qw, const int32_t* qz, const uint16_t* sc, void* w_dst,
