@@ -16,16 +16,29 @@
 #include "mi_moe.h"
 #include "mi_moe_device.hpp"
 #include "mi_moe_internal.hpp"
+#include "mi_moe_sched.hpp"
 
 #define MI_API extern "C" __attribute__((visibility("default")))
 
 namespace mimoe {
+constexpr size_t kMaxLds = 65536;   // dynamic LDS a fused-kernel launch may ask for
+
 // kernels / launchers defined in the other translation units
-hipError_t launch_route_global(const int32_t*, int, int, int, const RouteGlobal&, hipStream_t);
+hipError_t launch_route_global(const int32_t*, int, int, int, const RouteGlobal&, hipStream_t, int);
+hipError_t launch_combine(const float*, const float*, const int32_t*, void*, int, int, int, int, int,
+                          hipStream_t);
+hipError_t launch_awq_repack_all(const int32_t*, const int32_t*, const uint16_t*, const int32_t*,
+                                 const int32_t*, const uint16_t*, void*, unsigned char*, void*,
+                                 unsigned char*, int, int, int, hipStream_t);
 hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*, hipStream_t);
 hipError_t launch_w4a16(const W4Args&, int, int, int, int, hipStream_t);
-hipError_t launch_awq_repack(const int32_t*, const int32_t*, const uint16_t*, void*, uint16_t*,
-                             uint16_t*, int, int, int, int, int, int, hipStream_t);
+hipError_t launch_qint(const QArgs&, int, int, int, int, int, hipStream_t);
+hipError_t launch_q_repack(int, const void*, const uint16_t*, void*, uint16_t*, int, int, int, int,
+                           int, hipStream_t);
+hipError_t launch_q8_online_quant(const void*, int, int, int, int, int, int, void*, uint16_t*,
+                                  hipStream_t);
+hipError_t launch_q_block_dots(int, const void*, const int8_t*, int32_t*, int, int, int, int, int,
+                               int, int, hipStream_t);
 }  // namespace mimoe
 
 using namespace mimoe;
@@ -101,7 +114,7 @@ struct mi_moe_handle {
   DevBuf w13, w13_s, w13_z, w2, w2_s, w2_z;
   // workspace
   int64_t cap_T = 0, cap_n = 0;
-  DevBuf cnt2, act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U;
+  DevBuf arrive, act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U;
 };
 
 namespace {
@@ -132,9 +145,9 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
   while (capn < n) capn *= 2;
   // buffers may be in use by queued work on this stream
   HIPCHK(hipStreamSynchronize(st));
-  const int64_t NI2 = h->H / 64;
-  HIPCHK(h->cnt2.alloc((size_t)capT * NI2 * sizeof(uint32_t)));
-  HIPCHK(hipMemsetAsync(h->cnt2.p, 0, h->cnt2.bytes, st));
+  // arrival counters start at zero and every call leaves them at zero
+  HIPCHK(h->arrive.alloc((size_t)capT * (h->H / 64) * sizeof(uint32_t)));
+  HIPCHK(hipMemsetAsync(h->arrive.p, 0, h->arrive.bytes, st));
   HIPCHK(h->act.alloc((size_t)capn * h->I * 2));
   HIPCHK(h->act_d.alloc((size_t)capn * (h->I / 32) * sizeof(float)));
   HIPCHK(h->eout.alloc((size_t)capn * h->H * sizeof(float)));
@@ -157,8 +170,8 @@ void fill_sched(mi_moe_handle* h, SchedArgs& c, const void* x, void* y, const fl
   c.n = (int)(T * K);
   c.route_global = c.n > kRouteLdsMax;
   c.rg = route_view(h);
-  c.cnt2 = (uint32_t*)h->cnt2.p;
   c.eout = (float*)h->eout.p;
+  c.arrive = (uint32_t*)h->arrive.p;
 }
 
 RouteGlobal route_view(mi_moe_handle* h) {
@@ -180,13 +193,60 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
   W4Args a;
   std::memset(&a, 0, sizeof(a));
   fill_sched(h, a.c, x, y, tw, ids, T, K);
-  a.w13 = h->w13.p; a.w13_s = (const uint16_t*)h->w13_s.p; a.w13_z = (const uint16_t*)h->w13_z.p;
-  a.w2 = h->w2.p; a.w2_s = (const uint16_t*)h->w2_s.p; a.w2_z = (const uint16_t*)h->w2_z.p;
+  a.w13 = h->w13.p; a.w13_m = (const unsigned char*)h->w13_s.p;
+  a.w2 = h->w2.p; a.w2_m = (const unsigned char*)h->w2_s.p;
   a.act = (uint16_t*)h->act.p;
-  if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st));
+  a.sdt = h->scale_dtype;
+  // token columns per pass: up to 16, as many as fit 64 KB of LDS with the
+  // routing arrays (cnt <= T unless a token repeats an expert; more passes then)
+  const size_t route = (n <= 64 || a.c.route_global) ? 0 : route_lds_ints((int)h->E, (int)n) * sizeof(int);
+  a.p1_cols = a.p2_cols = (int)(T < 16 ? T : 16);
+  while (a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols) + route > kMaxLds) --a.p1_cols;
+  while (a.p2_cols > 1 && w4_p2_lds_bytes((int)h->I, a.p2_cols) + route > kMaxLds) --a.p2_cols;
+  if (n <= 64) {
+    // decode: work item per pair, phase 2 combines (no routing kernel)
+    HIPCHK(launch_w4a16(a, act, 1, (int)(n * (h->I / 16)), (int)(n * (h->H / 64)), st));
+    return MI_MOE_OK;
+  }
+  if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
   const int64_t umax = n < h->E ? n : h->E;
   const int64_t grid1 = umax * (h->I / 16), grid2 = umax * (h->H / 64);
-  HIPCHK(launch_w4a16(a, act, h->scale_dtype, (int)grid1, (int)grid2, st));
+  HIPCHK(launch_w4a16(a, act, 0, (int)grid1, (int)grid2, st));
+  HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
+  return MI_MOE_OK;
+}
+
+int q_alloc_weights(mi_moe_handle* h) {
+  const int64_t E = h->E, H = h->H, I = h->I;
+  const int64_t bb = h->quant == MI_MOE_Q8_0 ? 2048 : 1024;  // bytes per (tile, block)
+  HIPCHK(h->w13.alloc((size_t)E * (I / 32) * (H / 32) * bb));
+  HIPCHK(h->w13_s.alloc((size_t)E * (I / 32) * (H / 32) * 64 * 2));
+  HIPCHK(h->w2.alloc((size_t)E * (H / 64) * (I / 32) * bb));
+  HIPCHK(h->w2_s.alloc((size_t)E * (H / 64) * (I / 32) * 64 * 2));
+  HIPCHK(hipMemset(h->w13.p, 0, h->w13.bytes));
+  HIPCHK(hipMemset(h->w13_s.p, 0, h->w13_s.bytes));
+  HIPCHK(hipMemset(h->w2.p, 0, h->w2.bytes));
+  HIPCHK(hipMemset(h->w2_s.p, 0, h->w2_s.bytes));
+  return MI_MOE_OK;
+}
+
+int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const int32_t* ids,
+              int64_t T, int64_t K, int act, hipStream_t st) {
+  const int64_t n = T * K;
+  int rc = ensure_workspace(h, T, n, st);
+  if (rc) return rc;
+  QArgs a;
+  std::memset(&a, 0, sizeof(a));
+  fill_sched(h, a.c, x, y, tw, ids, T, K);
+  a.w13 = h->w13.p; a.w13_d = (const uint16_t*)h->w13_s.p;
+  a.w2 = h->w2.p; a.w2_d = (const uint16_t*)h->w2_s.p;
+  a.act_q = (int8_t*)h->act.p;
+  a.act_d = (float*)h->act_d.p;
+  if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
+  const int64_t umax = n < h->E ? n : h->E;
+  const int64_t grid1 = umax * (h->I / 32), grid2 = umax * (h->H / 64);
+  HIPCHK(launch_qint(a, h->quant, act, h->scale_dtype, (int)grid1, (int)grid2, st));
+  HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
   return MI_MOE_OK;
 }
 
@@ -204,6 +264,8 @@ MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe
   if (quant_type < 0 || quant_type > 2) return fail(MI_MOE_EINVAL, "quant_type must be 0, 1 or 2");
   if (H % 32 != 0) return fail(MI_MOE_EINVAL, "hidden_size must be multiple of 32");
   if (I % 32 != 0) return fail(MI_MOE_EINVAL, "intermediate_size must be multiple of 32");
+  if (quant_type != MI_MOE_W4A16 && H % 64 != 0)
+    return fail(MI_MOE_EINVAL, "hidden_size must be multiple of 64");
   if (quant_type == MI_MOE_W4A16 && (H % 512 != 0 || I % 128 != 0))
     return fail(MI_MOE_EINVAL, "W4A16 needs hidden_size %% 512 == 0 and intermediate_size %% 128 == 0");
   if (E > 512) return fail(MI_MOE_EUNSUPPORTED, "at most 512 experts");
@@ -224,7 +286,7 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
   if (!h) return MI_MOE_OK;
   (void)hipDeviceSynchronize();
   DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z,
-                    &h->cnt2, &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
+                    &h->arrive, &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
                     &h->r_active, &h->r_tok, &h->r_scat, &h->r_U};
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
@@ -281,19 +343,15 @@ MI_API int mi_moe_store_awq(mi_moe_handle* h, const int32_t* w13_q, const int32_
   HIPCHK(d.stage(w2_q, q2, src_on_device, st));
   HIPCHK(e.stage(w2_z, z2, src_on_device, st));
   HIPCHK(f.stage(w2_s, s2, src_on_device, st));
-  const int64_t NT13 = 2 * (I / 16), G1 = H / 128, NT2 = H / 16, G2 = I / 128;
+  const int64_t NT13 = 2 * (I / 16), G1 = H / 128, CH = I / 32, MQ = H / 64, G2 = I / 128;
   HIPCHK(h->w13.alloc((size_t)E * NT13 * G1 * 1024));
-  HIPCHK(h->w13_s.alloc((size_t)E * NT13 * G1 * 16 * 2));
-  HIPCHK(h->w13_z.alloc((size_t)E * NT13 * G1 * 4 * 2));
-  HIPCHK(h->w2.alloc((size_t)E * NT2 * G2 * 1024));
-  HIPCHK(h->w2_s.alloc((size_t)E * NT2 * G2 * 16 * 2));
-  HIPCHK(h->w2_z.alloc((size_t)E * NT2 * G2 * 4 * 2));
-  HIPCHK(launch_awq_repack((const int32_t*)a.ptr, (const int32_t*)b.ptr, (const uint16_t*)c.ptr,
-                           h->w13.p, (uint16_t*)h->w13_s.p, (uint16_t*)h->w13_z.p, (int)E, (int)H,
-                           (int)N13, (int)NT13, 1, (int)I, st));
-  HIPCHK(launch_awq_repack((const int32_t*)d.ptr, (const int32_t*)e.ptr, (const uint16_t*)f.ptr,
-                           h->w2.p, (uint16_t*)h->w2_s.p, (uint16_t*)h->w2_z.p, (int)E, (int)I,
-                           (int)H, (int)NT2, 0, (int)I, st));
+  HIPCHK(h->w13_s.alloc((size_t)E * (I / 16) * 80 * G1));    // metadata blocks
+  HIPCHK(h->w2.alloc((size_t)E * CH * MQ * 1024));
+  HIPCHK(h->w2_s.alloc((size_t)E * MQ * 160 * G2));          // metadata blocks
+  HIPCHK(launch_awq_repack_all((const int32_t*)a.ptr, (const int32_t*)b.ptr, (const uint16_t*)c.ptr,
+                               (const int32_t*)d.ptr, (const int32_t*)e.ptr, (const uint16_t*)f.ptr,
+                               h->w13.p, (unsigned char*)h->w13_s.p, h->w2.p, (unsigned char*)h->w2_s.p,
+                               (int)E, (int)H, (int)I, st));
   HIPCHK(hipStreamSynchronize(st));
   h->scale_dtype = scale_dtype;
   h->group = (int)group;
@@ -306,9 +364,28 @@ MI_API int mi_moe_store_quantized(mi_moe_handle* h, const void* gate_up_qs, cons
                                   int src_on_device, void* stream) {
   int rc = check_handle(h);
   if (rc) return rc;
-  (void)gate_up_qs; (void)gate_up_d; (void)down_qs; (void)down_d; (void)scale_dtype;
-  (void)src_on_device; (void)stream;
-  return fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 device path not built yet");
+  if (h->quant != MI_MOE_Q8_0 && h->quant != MI_MOE_Q4_0)
+    return fail(MI_MOE_EINVAL, "store_quantized needs a Q8_0 or Q4_0 handle");
+  if (scale_dtype != MI_MOE_F16 && scale_dtype != MI_MOE_BF16)
+    return fail(MI_MOE_EINVAL, "gate_up_d must be float16 or bfloat16");
+  if (!gate_up_qs || !gate_up_d || !down_qs || !down_d) return fail(MI_MOE_EINVAL, "null weight pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t E = h->E, H = h->H, I = h->I;
+  const size_t qdiv = h->quant == MI_MOE_Q4_0 ? 2 : 1;
+  Staged a, b, c, d;
+  HIPCHK(a.stage(gate_up_qs, (size_t)E * 2 * I * H / qdiv, src_on_device, st));
+  HIPCHK(b.stage(gate_up_d, (size_t)E * 2 * I * (H / 32) * 2, src_on_device, st));
+  HIPCHK(c.stage(down_qs, (size_t)E * H * I / qdiv, src_on_device, st));
+  HIPCHK(d.stage(down_d, (size_t)E * H * (I / 32) * 2, src_on_device, st));
+  if (!h->w13.p) { rc = q_alloc_weights(h); if (rc) return rc; }
+  HIPCHK(launch_q_repack(h->quant, a.ptr, (const uint16_t*)b.ptr, h->w13.p, (uint16_t*)h->w13_s.p,
+                         (int)E, (int)(2 * I), (int)H, 0, (int)I, st));
+  HIPCHK(launch_q_repack(h->quant, c.ptr, (const uint16_t*)d.ptr, h->w2.p, (uint16_t*)h->w2_s.p,
+                         (int)E, (int)H, (int)I, 1, (int)I, st));
+  HIPCHK(hipStreamSynchronize(st));
+  h->scale_dtype = scale_dtype;
+  h->loaded = true;
+  return MI_MOE_OK;
 }
 
 MI_API int mi_moe_quantize_and_store_expert(mi_moe_handle* h, int64_t expert, int proj,
@@ -316,16 +393,45 @@ MI_API int mi_moe_quantize_and_store_expert(mi_moe_handle* h, int64_t expert, in
                                             void* stream) {
   int rc = check_handle(h);
   if (rc) return rc;
-  (void)expert; (void)proj; (void)w; (void)w_dtype; (void)src_on_device; (void)stream;
-  return fail(MI_MOE_EUNSUPPORTED, "Q8_0 online quantization not built yet");
+  if (h->quant != MI_MOE_Q8_0)
+    return fail(MI_MOE_EINVAL, "Q4_0 does not support online quantization. "
+                               "Use store_quantized_repack() with pre-quantized weights.");
+  if (expert < 0 || expert >= h->E) return fail(MI_MOE_EINVAL, "expert index out of range");
+  if (proj < 0 || proj > 2) return fail(MI_MOE_EINVAL, "Unknown proj (0 gate_proj, 1 up_proj, 2 down_proj)");
+  if (w_dtype < 0 || w_dtype > 2) return fail(MI_MOE_EINVAL, "weight must be float32, float16 or bfloat16");
+  if (!w) return fail(MI_MOE_EINVAL, "null weight pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t N = proj == 2 ? h->H : h->I, K = proj == 2 ? h->I : h->H;
+  const size_t esz = w_dtype == 2 ? 4 : 2;
+  Staged a;
+  HIPCHK(a.stage(w, (size_t)N * K * esz, src_on_device, st));
+  if (!h->w13.p) { rc = q_alloc_weights(h); if (rc) return rc; }
+  void* wdst = proj == 2 ? h->w2.p : h->w13.p;
+  uint16_t* ddst = (uint16_t*)(proj == 2 ? h->w2_s.p : h->w13_s.p);
+  HIPCHK(launch_q8_online_quant(a.ptr, w_dtype, (int)N, (int)K, (int)expert, proj, (int)h->I, wdst,
+                                ddst, st));
+  HIPCHK(hipStreamSynchronize(st));
+  h->scale_dtype = MI_MOE_F16;  // quantize_weight_only stores fp16 scales
+  h->loaded = true;
+  return MI_MOE_OK;
 }
 
 MI_API int mi_moe_block_dots(mi_moe_handle* h, int64_t expert, int proj, const int8_t* a_qs,
                              int64_t M, int32_t* isum, void* stream) {
   int rc = check_handle(h);
   if (rc) return rc;
-  (void)expert; (void)proj; (void)a_qs; (void)M; (void)isum; (void)stream;
-  return fail(MI_MOE_EUNSUPPORTED, "block dots need a Q8_0/Q4_0 handle (not built yet)");
+  if (h->quant != MI_MOE_Q8_0 && h->quant != MI_MOE_Q4_0)
+    return fail(MI_MOE_EINVAL, "block dots need a Q8_0 or Q4_0 handle");
+  if (!h->loaded) return fail(MI_MOE_ENOTLOADED, "weights not stored");
+  if (expert < 0 || expert >= h->E || (proj != 0 && proj != 1) || M < 0)
+    return fail(MI_MOE_EINVAL, "bad expert / proj / M");
+  if (M == 0) return MI_MOE_OK;
+  if (!a_qs || !isum) return fail(MI_MOE_EINVAL, "null pointer");
+  const int64_t N = proj == 0 ? 2 * h->I : h->H, K = proj == 0 ? h->H : h->I;
+  const int tiles = proj == 0 ? (int)(h->I / 32) : (int)(h->H / 64);
+  HIPCHK(launch_q_block_dots(h->quant, proj == 0 ? h->w13.p : h->w2.p, a_qs, isum, (int)M, (int)N,
+                             (int)K, (int)expert, proj, (int)h->I, tiles, (hipStream_t)stream));
+  return MI_MOE_OK;
 }
 
 MI_API int mi_moe_forward(mi_moe_handle* h, const void* x, void* y, const float* topk_w,
@@ -344,7 +450,7 @@ MI_API int mi_moe_forward(mi_moe_handle* h, const void* x, void* y, const float*
   hipStream_t st = (hipStream_t)stream;
   if (h->timing) HIPCHK(hipEventRecord(h->ev0, st));
   if (h->quant == MI_MOE_W4A16) rc = forward_w4a16(h, x, y, topk_w, topk_ids, T, K, act_dtype, st);
-  else rc = fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 device path not built yet");
+  else rc = forward_q(h, x, y, topk_w, topk_ids, T, K, act_dtype, st);
   if (rc) return rc;
   if (h->timing) {
     HIPCHK(hipEventRecord(h->ev1, st));
@@ -382,7 +488,7 @@ MI_API int mi_moe_route(const int32_t* ids, int64_t T, int64_t K, int64_t E, int
   HIPCHK(active.alloc((size_t)E * sizeof(int32_t)));
   HIPCHK(U.alloc(sizeof(int32_t)));
   RouteGlobal rg{counts, starts, (int32_t*)active.p, token_map, scatter, (int32_t*)U.p};
-  HIPCHK(launch_route_global(ids, (int)(T * K), (int)K, (int)E, rg, st));
+  HIPCHK(launch_route_global(ids, (int)(T * K), (int)K, (int)E, rg, st, 1));
   HIPCHK(hipStreamSynchronize(st));
   active.release();
   U.release();

@@ -16,7 +16,8 @@ constexpr int kRouteWaves = kRouteThreads / kWave;
 // (t,k) order.  LDS: (kRouteWaves + 1) * E ints (E <= 512).
 __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
     const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
-    int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out) {
+    int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out,
+    int tok_div) {
   extern __shared__ int lds[];
   int* counts = lds;            // [E]
   int* cw = lds + E;            // [kRouteWaves][E]
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
       const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
       const int pos = mine[e] + __popcll(m & lt);
       scat[i] = pos;
-      tok[pos] = i / K;
+      tok[pos] = tok_div ? i / K : i;
       if (__ffsll((long long)m) - 1 == lane) add = __popcll(m);
     } else if (i < hi) {
       scat[i] = -1;
@@ -115,11 +116,59 @@ __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
   }
 }
 
+// tok_div = 0: tok[] holds pair indices t*K+k (fused kernels); 1: token ids.
 hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const RouteGlobal& rg,
-                               hipStream_t st) {
+                               hipStream_t st, int tok_div) {
   const size_t lds = (size_t)(kRouteWaves + 1) * E * sizeof(int);
   hipLaunchKernelGGL(route_global_kernel, dim3(1), dim3(kRouteThreads), lds, st, ids, n, K, E,
-                     rg.counts, rg.starts, rg.active, rg.tok, rg.scat, rg.U);
+                     rg.counts, rg.starts, rg.active, rg.tok, rg.scat, rg.U, tok_div);
+  return hipGetLastError();
+}
+
+// Stage C1 + C2 of Int8-gemm/q8_gemm.cpp:593-641 (tp = 1): y[t,h] =
+// cast(sum_k w[t,k] * eout[t*K+k, h]) over the valid ids in k order; a token
+// without a valid id gets 0.  One thread per (t, 4 consecutive h).
+template <int ACT>
+__global__ void combine_kernel(const float* __restrict__ eout, const float* __restrict__ tw,
+                               const int32_t* __restrict__ ids, uint16_t* __restrict__ y, int T,
+                               int K, int E, int H) {
+  const int H4 = H >> 2;
+  const int64_t total = (int64_t)T * H4;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int t = (int)(idx / H4), h = (int)(idx - (int64_t)t * H4) * 4;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < K; ++k) {
+      const int i = t * K + k;
+      const int e = ids[i];
+      if ((unsigned)e >= (unsigned)E) continue;
+      const float w = tw[i];
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(eout + (size_t)i * H + h);
+      const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float prod = w * vv[j];
+        acc[j] = acc[j] + prod;
+      }
+    }
+    const uint32_t lo = from_f32<ACT>(acc[0]) | ((uint32_t)from_f32<ACT>(acc[1]) << 16);
+    const uint32_t hi = from_f32<ACT>(acc[2]) | ((uint32_t)from_f32<ACT>(acc[3]) << 16);
+    *reinterpret_cast<u32x2_t*>(y + (size_t)t * H + h) = u32x2_t{lo, hi};
+  }
+}
+
+hipError_t launch_combine(const float* eout, const float* tw, const int32_t* ids, void* y, int T,
+                          int K, int E, int H, int act, hipStream_t st) {
+  const int64_t total = (int64_t)T * (H / 4);
+  if (total == 0) return hipSuccess;
+  int64_t grid = (total + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  if (act == 1)
+    hipLaunchKernelGGL(combine_kernel<1>, dim3((unsigned)grid), dim3(256), 0, st, eout, tw, ids,
+                       (uint16_t*)y, T, K, E, H);
+  else
+    hipLaunchKernelGGL(combine_kernel<0>, dim3((unsigned)grid), dim3(256), 0, st, eout, tw, ids,
+                       (uint16_t*)y, T, K, E, H);
   return hipGetLastError();
 }
 

@@ -18,7 +18,6 @@ typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 constexpr int kBlock = 256;            // 4 waves per workgroup
-constexpr uint32_t kSpinLimit = 1u << 24;
 
 // ------------------------------------------------------------ conversions
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) {
@@ -94,22 +93,12 @@ __device__ __forceinline__ int8_t q8_round(float v) {
   return (int8_t)(int)r;
 }
 
-// ------------------------------------------------------------ cross-WG sync
-__device__ __forceinline__ uint32_t ld_acquire_relaxed(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void fence_release() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-}
-__device__ __forceinline__ void fence_acquire() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-}
-
 // ------------------------------------------------------------ routing
 // Stable counting sort of the routed (t,k) pairs by expert, the semantics of
 // preprocess_moe_routing (Int8-gemm/moe_common.cpp:146-216): counts, exclusive
-// starts, token id per expert-sorted position, and scatter[(t,k)] = position
-// or -1 for an id outside [0,E).  Also emits the ascending list of active
+// starts, pair index i = t*K+k per expert-sorted position (the reference's
+// token_map entry {t,k}), and scatter[i] = position or -1 for an id outside
+// [0,E).  Also emits the ascending list of active
 // experts.  Whole-workgroup routine (blockDim.x == 256), all arrays in LDS.
 // Ranks are computed by wave 0 in 64-id chunks with a ballot match.
 __device__ inline void route_lds(const int32_t* __restrict__ ids, int n, int K,
@@ -169,7 +158,7 @@ __device__ inline void route_lds(const int32_t* __restrict__ ids, int n, int K,
         const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
         const int pos = starts[e] + counts[e] + __popcll(m & lt);
         scat[i] = pos;
-        tok[pos] = i / K;
+        tok[pos] = i;
         if (__ffsll((long long)m) - 1 == lane) add = __popcll(m);
       } else if (i < n) {
         scat[i] = -1;

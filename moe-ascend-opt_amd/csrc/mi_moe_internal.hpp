@@ -9,8 +9,6 @@ namespace mimoe {
 // Routing done inside the fused kernel (LDS) up to this many (t,k) pairs;
 // beyond it a separate routing kernel writes the arrays to the workspace.
 constexpr int kRouteLdsMax = 1024;
-// Columns (routed rows of one expert) handled per register pass (W4A16).
-constexpr int kColsPerPass = 64;
 // Tokens per pass of the integer path (activations staged in LDS).
 constexpr int kQTokPerPass = 8;
 
@@ -33,21 +31,31 @@ struct SchedArgs {
   int T, K, E, H, I, n;
   int route_global;
   RouteGlobal rg;
-  uint32_t* cnt2;          // [T * (H/64)] combine arrivals
-  float* eout;             // [n, H] per-(t,k) expert outputs
+  float* eout;             // [n, H] per-pair expert outputs (row i = t*K+k)
+  uint32_t* arrive;        // [T, H/64] arrival counters of the decode combine (kept zero)
 };
 
-// W4A16 fused kernel (w4a16.hip).
+// W4A16 fused kernels (w4a16.hip).
 struct W4Args {
   SchedArgs c;
-  const void* w13;         // uint4 tiles
-  const uint16_t* w13_s;   // [tile][g][16]
-  const uint16_t* w13_z;   // [tile][g][4]  (u16 per row quartet)
-  const void* w2;
-  const uint16_t* w2_s;
-  const uint16_t* w2_z;
-  uint16_t* act;           // [n, I] SiLU*mul activations (act dtype)
+  const void* w13;             // uint4 tiles [e][I/16][gate,up][H/128][64 lanes][16 B]
+  const unsigned char* w13_m;  // metadata blocks of 80*(H/128) bytes per (e, I/16 slice)
+  const void* w2;              // [e][H/64][I/32][64 lanes][16 B]
+  const unsigned char* w2_m;   // metadata blocks of 160*(I/128) bytes per (e, H/64 quad)
+  uint16_t* act;               // [n, I] SiLU*mul activations (act dtype), row = pair
+  int p1_cols, p2_cols;        // token columns per pass (rows staged in LDS)
+  int sdt;                     // scale dtype: 1 bf16, 0 fp16
 };
+
+// LDS bytes of the W4A16 phase kernels (routing arrays come on top).
+constexpr int kP1RedBytes = 4 * 2 * 64 * 4 * 4;
+constexpr int kP2RedBytes = 4 * 4 * 64 * 4 * 4;
+__host__ __device__ inline size_t w4_p1_lds_bytes(int H, int cols) {
+  return (size_t)kP1RedBytes + (size_t)80 * (H >> 7) + (size_t)cols * H * 2;
+}
+__host__ __device__ inline size_t w4_p2_lds_bytes(int I, int cols) {
+  return (size_t)kP2RedBytes + (size_t)160 * (I >> 7) + (size_t)cols * I * 2;
+}
 
 // Q8_0 / Q4_0 fused kernel (qint.hip).
 struct QArgs {
@@ -56,7 +64,7 @@ struct QArgs {
   const uint16_t* w13_d;   // [E][I/32][H/32][64]
   const void* w2;          // [E][H/64 tiles][I/32 blocks][chunks][64][16 B]
   const uint16_t* w2_d;    // [E][H/64][I/32][64]
-  int8_t* act_q;           // [n, I] intermediate Q8_0 bytes
+  int8_t* act_q;           // [n, I] intermediate Q8_0 bytes, row = pair
   float* act_d;            // [n, I/32] intermediate Q8_0 scales
 };
 

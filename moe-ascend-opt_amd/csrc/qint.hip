@@ -157,7 +157,7 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
     // Stage A for the staged tokens (Int8-gemm/q8_gemm.cpp:360-377)
     for (int idx = tid; idx < cntp * KB; idx += kBlock) {
       const int cc = idx / KB, kb = idx - cc * KB;
-      const int t = rv.tok[p0 + cb0 + cc];
+      const int t = rv.pair[p0 + cb0 + cc] / c.K;
       const u32x4_t* src = reinterpret_cast<const u32x4_t*>(c.x + (size_t)t * c.H + kb * 32);
       float v[32];
 #pragma unroll
@@ -207,7 +207,7 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
       const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
       const int8_t q = q8_round(act * id);
       if (cc < cntp) {
-        const size_t row = (size_t)(p0 + cb0 + cc);
+        const size_t row = (size_t)rv.pair[p0 + cb0 + cc];
         a.act_q[row * c.I + 32 * sl + r] = q;
         if (r == 0) a.act_d[row * S + sl] = d;
       }
@@ -218,8 +218,7 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
 
 // ---------------------------------------------------------------- phase 2
 template <int QT, int ACT, int SC>
-__device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, const QLds& L,
-                         int* s_list, int* s_nlist) {
+__device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, const QLds& L) {
   const SchedArgs& c = a.c;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int e = rv.active[ui];
@@ -234,7 +233,7 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
     const int cntp = min(kQTokPerPass, cnt - cb0);
     for (int idx = tid; idx < cntp * KB2; idx += kBlock) {
       const int cc = idx / KB2, kb = idx - cc * KB2;
-      const size_t row = (size_t)(p0 + cb0 + cc);
+      const size_t row = (size_t)rv.pair[p0 + cb0 + cc];
       const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.act_q + row * c.I + kb * 32);
       const u32x4_t q0 = src[0], q1 = src[1];
       u32x4_t* dst = reinterpret_cast<u32x4_t*>(L.xq + cc * c.I + kb * 32);
@@ -262,11 +261,10 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
       float v = L.red[(0 * kQTokPerPass + cc) * 64 + lane];
 #pragma unroll
       for (int w = 1; w < 4; ++w) v = v + L.red[(w * kQTokPerPass + cc) * 64 + lane];
-      c.eout[(size_t)(p0 + cb0 + cc) * c.H + 64 * hb + lane] = v;
+      c.eout[(size_t)rv.pair[p0 + cb0 + cc] * c.H + 64 * hb + lane] = v;
     }
     __syncthreads();
   }
-  combine_hb<ACT>(c, rv, p0, cnt, hb, s_list, s_nlist);
 }
 
 // ---------------------------------------------------------------- kernels
@@ -281,7 +279,6 @@ __global__ __launch_bounds__(kBlock) void q_phase1_kernel(QArgs a) {
   __shared__ int s_U;
   const QLds L = carve(smem, a.c.H);
   const RouteView rv = sched_route(a.c, L.route, &s_U);
-  if (blockIdx.x == 0) zero_unrouted<ACT>(a.c, rv);
   const int S = a.c.I / 32;
   const int ui = blockIdx.x / S;
   if (ui >= rv.U) return;
@@ -291,14 +288,13 @@ __global__ __launch_bounds__(kBlock) void q_phase1_kernel(QArgs a) {
 template <int QT, int ACT, int SC>
 __global__ __launch_bounds__(kBlock) void q_phase2_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_U, s_nlist;
-  __shared__ int s_list[kBlock];
+  __shared__ int s_U;
   const QLds L = carve(smem, a.c.I);
   const RouteView rv = sched_route(a.c, L.route, &s_U);
   const int HB = a.c.H / 64;
   const int ui = blockIdx.x / HB;
   if (ui >= rv.U) return;
-  q_phase2<QT, ACT, SC>(a, rv, ui, blockIdx.x % HB, L, s_list, &s_nlist);
+  q_phase2<QT, ACT, SC>(a, rv, ui, blockIdx.x % HB, L);
 }
 
 template <int QT, int ACT, int SC>
