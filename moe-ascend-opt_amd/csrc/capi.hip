@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -22,6 +23,8 @@
 
 namespace mimoe {
 constexpr size_t kMaxLds = 65536;   // dynamic LDS a fused-kernel launch may ask for
+constexpr size_t kXAllBytes = 16384; // hidden rows phase 1 copies whole on the decode path
+constexpr int kDecodeCols = 4;       // phase-1 pass width on the decode path
 
 // kernels / launchers defined in the other translation units
 hipError_t launch_route_global(const int32_t*, int, int, int, const RouteGlobal&, hipStream_t, int);
@@ -114,7 +117,7 @@ struct mi_moe_handle {
   DevBuf w13, w13_s, w13_z, w2, w2_s, w2_z;
   // workspace
   int64_t cap_T = 0, cap_n = 0;
-  DevBuf arrive, act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U;
+  DevBuf act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U;
 };
 
 namespace {
@@ -145,9 +148,6 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
   while (capn < n) capn *= 2;
   // buffers may be in use by queued work on this stream
   HIPCHK(hipStreamSynchronize(st));
-  // arrival counters start at zero and every call leaves them at zero
-  HIPCHK(h->arrive.alloc((size_t)capT * (h->H / 64) * sizeof(uint32_t)));
-  HIPCHK(hipMemsetAsync(h->arrive.p, 0, h->arrive.bytes, st));
   HIPCHK(h->act.alloc((size_t)capn * h->I * 2));
   HIPCHK(h->act_d.alloc((size_t)capn * (h->I / 32) * sizeof(float)));
   HIPCHK(h->eout.alloc((size_t)capn * h->H * sizeof(float)));
@@ -171,7 +171,6 @@ void fill_sched(mi_moe_handle* h, SchedArgs& c, const void* x, void* y, const fl
   c.route_global = c.n > kRouteLdsMax;
   c.rg = route_view(h);
   c.eout = (float*)h->eout.p;
-  c.arrive = (uint32_t*)h->arrive.p;
 }
 
 RouteGlobal route_view(mi_moe_handle* h) {
@@ -197,15 +196,22 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
   a.w2 = h->w2.p; a.w2_m = (const unsigned char*)h->w2_s.p;
   a.act = (uint16_t*)h->act.p;
   a.sdt = h->scale_dtype;
+  // decode path: T*K <= 64 pairs, at most 16 experts per token (a wave each
+  // in the down kernel)
+  const bool ballot = n <= 64 && K <= 16;
+  a.route_lds = (ballot || a.c.route_global) ? 0 : (int)(route_lds_ints((int)h->E, (int)n) * sizeof(int));
+  // phase 1 copies the hidden rows of every token when they are few
+  a.x_all = ballot && (size_t)T * h->H * 2 <= kXAllBytes;
   // token columns per pass: up to 16, as many as fit 64 KB of LDS with the
   // routing arrays (cnt <= T unless a token repeats an expert; more passes then)
-  const size_t route = (n <= 64 || a.c.route_global) ? 0 : route_lds_ints((int)h->E, (int)n) * sizeof(int);
   a.p1_cols = a.p2_cols = (int)(T < 16 ? T : 16);
-  while (a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols) + route > kMaxLds) --a.p1_cols;
-  while (a.p2_cols > 1 && w4_p2_lds_bytes((int)h->I, a.p2_cols) + route > kMaxLds) --a.p2_cols;
-  if (n <= 64) {
-    // decode: work item per pair, phase 2 combines (no routing kernel)
-    HIPCHK(launch_w4a16(a, act, 1, (int)(n * (h->I / 16)), (int)(n * (h->H / 64)), st));
+  // decode: an expert rarely gets more than a few of the T tokens; a narrow
+  // pass keeps the LDS small (occupancy), extra columns take another pass
+  if (ballot && a.p1_cols > kDecodeCols) a.p1_cols = kDecodeCols;
+  while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols) + a.route_lds > kMaxLds) --a.p1_cols;
+  while (a.p2_cols > 1 && w4_p2_lds_bytes((int)h->I, a.p2_cols) + a.route_lds > kMaxLds) --a.p2_cols;
+  if (ballot) {
+    HIPCHK(launch_w4a16(a, act, 1, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st));
     return MI_MOE_OK;
   }
   if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
@@ -286,7 +292,7 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
   if (!h) return MI_MOE_OK;
   (void)hipDeviceSynchronize();
   DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z,
-                    &h->arrive, &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
+                    &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
                     &h->r_active, &h->r_tok, &h->r_scat, &h->r_U};
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
@@ -347,7 +353,7 @@ MI_API int mi_moe_store_awq(mi_moe_handle* h, const int32_t* w13_q, const int32_
   HIPCHK(h->w13.alloc((size_t)E * NT13 * G1 * 1024));
   HIPCHK(h->w13_s.alloc((size_t)E * (I / 16) * 80 * G1));    // metadata blocks
   HIPCHK(h->w2.alloc((size_t)E * CH * MQ * 1024));
-  HIPCHK(h->w2_s.alloc((size_t)E * MQ * 160 * G2));          // metadata blocks
+  HIPCHK(h->w2_s.alloc((size_t)E * MQ * 4 * w2_meta_sec_bytes((int)G2)));   // metadata sections
   HIPCHK(launch_awq_repack_all((const int32_t*)a.ptr, (const int32_t*)b.ptr, (const uint16_t*)c.ptr,
                                (const int32_t*)d.ptr, (const int32_t*)e.ptr, (const uint16_t*)f.ptr,
                                h->w13.p, (unsigned char*)h->w13_s.p, h->w2.p, (unsigned char*)h->w2_s.p,

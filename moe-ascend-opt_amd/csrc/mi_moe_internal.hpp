@@ -32,7 +32,6 @@ struct SchedArgs {
   int route_global;
   RouteGlobal rg;
   float* eout;             // [n, H] per-pair expert outputs (row i = t*K+k)
-  uint32_t* arrive;        // [T, H/64] arrival counters of the decode combine (kept zero)
 };
 
 // W4A16 fused kernels (w4a16.hip).
@@ -40,21 +39,29 @@ struct W4Args {
   SchedArgs c;
   const void* w13;             // uint4 tiles [e][I/16][gate,up][H/128][64 lanes][16 B]
   const unsigned char* w13_m;  // metadata blocks of 80*(H/128) bytes per (e, I/16 slice)
-  const void* w2;              // [e][H/64][I/32][64 lanes][16 B]
-  const unsigned char* w2_m;   // metadata blocks of 160*(I/128) bytes per (e, H/64 quad)
+  const void* w2;              // [e][H/64][4][I/128][64 lanes][16 B]
+  const unsigned char* w2_m;   // metadata sections of w2_meta_sec_bytes(I/128) per (e, H/64 quad, row tile)
   uint16_t* act;               // [n, I] SiLU*mul activations (act dtype), row = pair
   int p1_cols, p2_cols;        // token columns per pass (rows staged in LDS)
   int sdt;                     // scale dtype: 1 bf16, 0 fp16
+  int x_all;                   // phase 1 copies the hidden rows of all T tokens at start
+  int route_lds;               // bytes of routing arrays in LDS (sorted path)
 };
 
-// LDS bytes of the W4A16 phase kernels (routing arrays come on top).
+// Bytes of the w2 metadata of one 16-row tile: G2 = I/128 groups of 16 u16
+// scales and 8 bytes of zero nibbles, rounded up to 16 bytes.
+__host__ __device__ inline int w2_meta_sec_bytes(int G2) { return (40 * G2 + 15) & ~15; }
+
+// LDS bytes of the W4A16 kernels (routing arrays come on top).
 constexpr int kP1RedBytes = 4 * 2 * 64 * 4 * 4;
-constexpr int kP2RedBytes = 4 * 4 * 64 * 4 * 4;
-__host__ __device__ inline size_t w4_p1_lds_bytes(int H, int cols) {
-  return (size_t)kP1RedBytes + (size_t)80 * (H >> 7) + (size_t)cols * H * 2;
+__host__ __device__ inline size_t w4_p1_lds_bytes(int H, int xrows) {
+  return (size_t)kP1RedBytes + (size_t)80 * (H >> 7) + (size_t)xrows * H * 2;
 }
 __host__ __device__ inline size_t w4_p2_lds_bytes(int I, int cols) {
-  return (size_t)kP2RedBytes + (size_t)160 * (I >> 7) + (size_t)cols * I * 2;
+  return (size_t)4 * w2_meta_sec_bytes(I >> 7) + (size_t)cols * I * 2;
+}
+__host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K) {
+  return (size_t)K * I * 2 + (size_t)K * w2_meta_sec_bytes(I >> 7) + (size_t)K * 16 * 4 + (size_t)K * 4;
 }
 
 // Q8_0 / Q4_0 fused kernel (qint.hip).

@@ -27,16 +27,18 @@
 //   w13 metadata, one block of 80*G1 bytes per (e, j): scales u32 [r 16][g]
 //     (gate scale bits | up scale bits << 16), then zeros u8 [r][g]
 //     (gate zero | up zero << 4).
-//   w2 chunks [e][m (H/64)][c (I/32)][64 lanes][16 B]: lane 16q+r word jj
-//     holds row h = 64m+16jj+r, k = 32c+8q+(0..7) (same pair packing).
-//   w2 metadata, one block of 160*G2 bytes per (e, m) (G2 = I/128): scales
-//     u16 [g2][r][jj], then zeros u16 [g2][r] (nibble jj).
+//   w2 words [e][m (H/64)][jj 4][g2 (I/128)][64 lanes][16 B]: lane 16q+r word
+//     cc holds row h = 64m+16jj+r, k = 128g2+32cc+8q+(0..7) (same pair packing).
+//   w2 metadata, one section of w2_meta_sec_bytes(G2) bytes (40*G2 rounded up
+//     to 16) per (e, m, jj) (G2 = I/128): scales u16 [g2][r], then zeros
+//     [g2][r/2] (row r in nibble r&1).
 //
 // Paths (chosen on the host); rows of act/eout are indexed by pair i = t*K+k:
-//   decode (T*K <= 64): two launches.  Work items are pairs (an item serves
-//     its expert iff it is the expert's first pair; the others exit at once).
-//     Phase 1: gate_up + SiLU*mul -> act.  Phase 2: down -> eout, then the
-//     combine, elected per (token, 64-row block) by an arrival counter.
+//   decode (T*K <= 64, K <= 16): two launches.  Phase 1 (gate_up + SiLU*mul ->
+//     act) has a work item per pair; an item serves its expert iff it is the
+//     expert's first pair, the others exit at once.  The down kernel has a
+//     workgroup per (token, 16-row tile) with a wave per routed expert, and
+//     combines in LDS.
 //   general: routing (in LDS up to 1024 pairs, else a routing kernel), phase 1,
 //     phase 2 -> eout, and a combine kernel.
 #pragma clang fp contract(off)
@@ -96,9 +98,11 @@ __device__ __forceinline__ uint64_t bits_range(int lo, int count) {
   return m << lo;
 }
 
-// scale bits -> fp32 (sdt: 1 bf16, 0 fp16; uniform)
+// scale bits -> fp32 (sdt: 1 bf16, 0 fp16), without a branch
 __device__ __forceinline__ float scale_f32(uint32_t bits, int sdt) {
-  return sdt ? bf16_to_f32(bits) : f16_to_f32(bits);
+  const uint32_t b = __float_as_uint(bf16_to_f32(bits)), h = __float_as_uint(f16_to_f32(bits));
+  const uint32_t m = 0u - (uint32_t)(sdt != 0);
+  return __uint_as_float((b & m) | (h & ~m));
 }
 
 // acc[t] += s * (G[t] - c * X[t]) for the lane's 4 token columns
@@ -113,23 +117,37 @@ __device__ __forceinline__ void fold(f32x4_t& acc, const f32x4_t G, const f32x4_
 // Copy nitems 16-byte items into LDS (contiguous from dst, 16-byte aligned)
 // with direct-to-LDS loads (global_load_lds_dwordx4): wave instruction s moves
 // items 64s..64s+63, lane l landing at dst + 1024s + 16l; instructions are
-// dealt round-robin to the 4 waves.  src(k) is evaluated by every lane of a
+// dealt round-robin to the nwaves waves of the workgroup.  src(k) is evaluated by every lane of a
 // participating wave (it may shuffle).  The caller waits for vmcnt and
 // barriers before reading the copy.
 template <class Src>
-__device__ __forceinline__ void stage_lds(unsigned char* dst, int nitems, int wave, int lane,
-                                          Src src) {
-  for (int s = wave; s * 64 < nitems; s += 4) {   // uniform per wave
+__device__ __forceinline__ void stage_lds(unsigned char* dst, int nitems, int wave, int nwaves,
+                                          int lane, Src src) {
+  for (int s = wave; s * 64 < nitems; s += nwaves) {   // uniform per wave
     const int k = s * 64 + lane;
     const void* p = src(k < nitems ? k : nitems - 1);
     if (k < nitems) __builtin_amdgcn_global_load_lds(p, dst + s * 1024, 16, 0, 0);
   }
 }
 
-__device__ __forceinline__ void wait_all_and_sync() {
-  __builtin_amdgcn_s_waitcnt(0);   // vmcnt = expcnt = lgkmcnt = 0 (direct-to-LDS copies landed)
-  __syncthreads();
+// Wait until at most N vector-memory loads of this wave are outstanding, then
+// barrier.  With the direct-to-LDS copies issued before the N weight loads
+// (vector loads complete in order), this waits for the copies only; the
+// weights are waited for one by one where they are used.
+template <int N>
+__device__ __forceinline__ void wait_copies_and_sync() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+  // a bare barrier: __syncthreads() would add fences that wait for every load
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
+
+// Keeps the compiler from moving memory operations across this point (the
+// weight loads must be issued after the direct-to-LDS copies).
+__device__ __forceinline__ void issue_order_fence() { asm volatile("" ::: "memory"); }
 
 // ================================================================ routing
 // Routing for T*K <= 64 without a sort: every wave reads all ids at once.
@@ -200,59 +218,74 @@ __device__ __forceinline__ bool get_cols(const SchedArgs& c, int item, int lane,
 // Workgroup (item, 16-row slice j): gate/up rows j*16.. of the item's expert
 // over all H (the 4 waves split the H groups), every routed pair of the expert
 // in passes of p1_cols columns; SiLU*mul into act[pair].  Each wave keeps the
-// weights of NB groups in flight together (NB from the host: min(8, H/512)
-// rounded down to an instantiated size); loads past the wave's last group
-// repeat its last group, so the load sequence has no branches.
-// LDS: red [wave][gate,up][64][4] f32 | metadata 80*G1 B | x rows [p1_cols][H] | routing.
+// weights of NB groups in flight together (NB, from the host, divides the
+// wave's H/512 groups).  Lanes of columns past the pass read the pass's last
+// column, so the loop body has no branches; their results are never stored.
+// Hidden rows: with a.x_all the rows of all T tokens are copied into LDS at
+// kernel start, in parallel with the routing read; otherwise the rows of each
+// pass's columns are copied once the routing is known.
+// LDS: red [wave][gate,up][64][4] f32 | metadata 80*G1 B | x rows | routing.
 template <int ACT, int BALLOT, int NB>
 __global__ __launch_bounds__(kBlock) void w4a16_phase1_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
-  const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, P = a.p1_cols;
+  const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, P = a.p1_cols, HI = H >> 3;
+  const int XR = a.x_all ? c.T : P;   // rows of x held in LDS
   float* red = reinterpret_cast<float*>(smem);
   unsigned char* meta = smem + kP1RedBytes;
   uint16_t* xs = reinterpret_cast<uint16_t*>(meta + 80 * G1);
-  unsigned char* route = reinterpret_cast<unsigned char*>(xs) + (size_t)P * H * 2;
+  unsigned char* route = reinterpret_cast<unsigned char*>(xs) + (size_t)XR * H * 2;
   const int item = blockIdx.x / NI1, j = blockIdx.x - item * NI1;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  if (a.x_all)   // uniform; x is [T][H] contiguous
+    stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, 4, lane,
+                 [&](int k) { return (const void*)(c.x + 8 * (size_t)k); });
   Cols<BALLOT> cl;
-  if (!get_cols<BALLOT>(c, item, lane, route, &s_U, cl)) return;  // uniform
+  if (!get_cols<BALLOT>(c, item, lane, route, &s_U, cl)) {   // uniform
+    __builtin_amdgcn_s_waitcnt(0);   // no copy into LDS outlives the workgroup
+    return;
+  }
   const int e = cl.e, cnt = cl.cnt;
   const size_t blk = (size_t)e * NI1 + j;
   const unsigned char* msrc = a.w13_m + blk * 80 * G1;
-  stage_lds(meta, 5 * G1, wave, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
+  stage_lds(meta, 5 * G1, wave, 4, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
   const int g0 = G1 * wave / 4, ng = G1 * (wave + 1) / 4 - g0;   // equal for all waves (G1 % 4 == 0)
   const char* wg = (const char*)a.w13 + (blk * 2 * G1 + g0) * 1024 + lane * 16;
   const char* wu = wg + (size_t)G1 * 1024;
   const uint32_t* msc = reinterpret_cast<const uint32_t*>(meta) + r * G1;
   const unsigned char* mz = meta + 64 * G1 + r * G1;
-  const int HI = H >> 3;
   constexpr float off = W4Consts<ACT>::offset;
   for (int cb0 = 0; cb0 < cnt; cb0 += P) {
     const int ncol = min(P, cnt - cb0);
-    stage_lds(reinterpret_cast<unsigned char*>(xs), ncol * HI, wave, lane, [&](int k) {
-      const int cc = k / HI;
-      const int t = cl.pair(cb0 + cc, true) / c.K;
-      return (const void*)(c.x + (size_t)t * H + 8 * (k - cc * HI));
-    });
+    int xr;   // LDS row of this lane's column
+    if (a.x_all) {
+      xr = cl.pair(cb0 + min(r, ncol - 1), true) / c.K;
+    } else {
+      stage_lds(reinterpret_cast<unsigned char*>(xs), ncol * HI, wave, 4, lane, [&](int k) {
+        const int cc = k / HI;
+        const int t = cl.pair(cb0 + cc, true) / c.K;
+        return (const void*)(c.x + (size_t)t * H + 8 * (k - cc * HI));
+      });
+      xr = min(r, ncol - 1);
+    }
+    const uint16_t* xrow = xs + xr * H + 32 * q;
     f32x4_t accg = {0, 0, 0, 0}, accu = {0, 0, 0, 0};
+    issue_order_fence();
     for (int gb = 0; gb < ng; gb += NB) {
       u32x4_t wgv[NB], wuv[NB];
 #pragma unroll
       for (int gi = 0; gi < NB; ++gi) {
-        const size_t go = (size_t)min(gb + gi, ng - 1) * 1024;
-        wgv[gi] = ldg16(wg + go);
-        wuv[gi] = ldg16(wu + go);
+        wgv[gi] = ldg16(wg + (size_t)(gb + gi) * 1024);
+        wuv[gi] = ldg16(wu + (size_t)(gb + gi) * 1024);
       }
-      if (gb == 0) wait_all_and_sync();   // metadata and x rows are in LDS
+      if (gb == 0) wait_copies_and_sync<2 * NB>();   // metadata and x rows are in LDS
 #pragma unroll
       for (int gi = 0; gi < NB; ++gi) {
-        if (gb + gi >= ng) break;
         const int g = g0 + gb + gi;
         u32x4_t A[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) A[i] = r < ncol ? lds16(xs + r * H + 128 * g + 32 * q + 8 * i) : zero4();
+        for (int i = 0; i < 4; ++i) A[i] = lds16(xrow + 128 * g + 8 * i);
         f32x4_t X = {0, 0, 0, 0}, Gg = {0, 0, 0, 0}, Gu = {0, 0, 0, 0};
         const uint32_t wgw[4] = {wgv[gi].x, wgv[gi].y, wgv[gi].z, wgv[gi].w};
         const uint32_t wuw[4] = {wuv[gi].x, wuv[gi].y, wuv[gi].z, wuv[gi].w};
@@ -291,143 +324,142 @@ __global__ __launch_bounds__(kBlock) void w4a16_phase1_kernel(W4Args a) {
   }
 }
 
-// ================================================================ phase 2
-// Workgroup (item, quad m = rows 64m..64m+63): down over all I (the waves
-// split the 32-k chunks), for every routed pair of the item's expert in
-// passes of p2_cols columns.
-//   BALLOT = 0: eout[pair][64m..] (a combine kernel follows).
-//   BALLOT = 1: eout rows are written with atomic exchanges; after them each
-//     column adds one arrival to the counter of (token, m).  The workgroup
-//     that completes a counter (all valid pairs of the token arrived) reads
-//     the token's K rows back with atomic reads, forms
-//     y = cast(sum_k w[t,k] * eout[t*K+k]) in k order -- Stage C1 + C2 of
-//     Int8-gemm/q8_gemm.cpp:593-641 -- and puts the counter back to zero.
-//     Data crosses workgroups only through atomic read-modify-writes.
-// Each wave keeps the weights of NB chunks in flight together (NB from the
-// host: min(12, I/128) rounded down to an instantiated size; loads past the
-// wave's last chunk repeat it).
-// LDS: red [wave][jj][64][4] f32 | metadata 160*G2 B | act rows [p2_cols][I] | routing.
-template <int ACT, int BALLOT, int NB>
+// Scales and zeros of the (16 row x 128 k) groups of one w2 row tile jj of a
+// quad block: scales u16 [g2][r], then zeros [g2][r/2] (row r in nibble r&1).
+__device__ __forceinline__ float w2_scale(const unsigned char* sec, int g2, int r, int sdt) {
+  return scale_f32(reinterpret_cast<const uint16_t*>(sec)[16 * g2 + r], sdt);
+}
+__device__ __forceinline__ float w2_zero(const unsigned char* sec, int G2, int g2, int r) {
+  return (float)((sec[32 * G2 + 8 * g2 + (r >> 1)] >> (4 * (r & 1))) & 0xfu);
+}
+
+// Down projection of one row tile (16 rows) over all I for 16 token columns:
+// acc += sum over groups of s * (G - (offset + z) X).  A rows come from LDS
+// (arow: this lane's column, k offset 8q), weights from wb (G2 words of 16 B
+// per lane, NB in flight together).  sync_first: wait for the LDS copies and
+// barrier after the first batch of weight loads is issued.
+template <int ACT, int NB>
+__device__ __forceinline__ f32x4_t down_tile(const char* wb, const uint16_t* arow,
+                                             const unsigned char* sec, int G2, int r, int sdt,
+                                             bool sync_first) {
+  constexpr float off = W4Consts<ACT>::offset;
+  f32x4_t acc = {0, 0, 0, 0};
+  issue_order_fence();
+  for (int gb = 0; gb < G2; gb += NB) {
+    u32x4_t wv[NB];
+#pragma unroll
+    for (int gi = 0; gi < NB; ++gi) wv[gi] = ldg16(wb + (size_t)(gb + gi) * 1024);
+    if (gb == 0 && sync_first) wait_copies_and_sync<NB>();   // the LDS operands are in place
+#pragma unroll
+    for (int gi = 0; gi < NB; ++gi) {
+      const int g2 = gb + gi;
+      u32x4_t A[4];
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) A[cc] = lds16(arow + 128 * g2 + 32 * cc);
+      f32x4_t X = {0, 0, 0, 0}, G = {0, 0, 0, 0};
+      const uint32_t ww[4] = {wv[gi].x, wv[gi].y, wv[gi].z, wv[gi].w};
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        X = mfma16<ACT>(A[cc], ones4<ACT>(), X);
+        G = mfma16<ACT>(A[cc], deq4<ACT>(ww[cc]), G);
+      }
+      fold(acc, G, X, w2_scale(sec, g2, r, sdt), off + w2_zero(sec, G2, g2, r));
+    }
+  }
+  return acc;
+}
+
+// ================================================================ phase 2 (general)
+// Workgroup (item, quad m = rows 64m..64m+63): down projection of the quad for
+// every routed pair of the item's expert, in passes of p2_cols columns, into
+// eout[pair][64m..] (a combine kernel follows).  Wave w owns rows
+// 64m+16w..+15 over all of I, so no cross-wave reduction is needed; a lane's
+// 16-byte weight word holds its row's four 32-k chunks of one 128-k group, so
+// the group's four MFMAs accumulate in the matrix core and its scale and zero
+// are applied once.  NB, from the host, divides I/128.
+// LDS: metadata block | act rows [p2_cols][I] | routing.
+template <int ACT, int NB>
 __global__ __launch_bounds__(kBlock) void w4a16_phase2_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
-  __shared__ int s_done[64];
-  __shared__ int s_nd;
-  const int H = c.H, I = c.I, MQ = H >> 6, CH = I >> 5, G2 = I >> 7, P = a.p2_cols;
-  float* red = reinterpret_cast<float*>(smem);
-  unsigned char* meta = smem + kP2RedBytes;
-  uint16_t* as = reinterpret_cast<uint16_t*>(meta + 160 * G2);
+  const int H = c.H, I = c.I, MQ = H >> 6, G2 = I >> 7, P = a.p2_cols, II = I >> 3;
+  const int SEC = w2_meta_sec_bytes(G2);
+  unsigned char* meta = smem;
+  uint16_t* as = reinterpret_cast<uint16_t*>(meta + 4 * SEC);
   unsigned char* route = reinterpret_cast<unsigned char*>(as) + (size_t)P * I * 2;
   const int item = blockIdx.x / MQ, m = blockIdx.x - item * MQ;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
-  Cols<BALLOT> cl;
-  const bool serve = get_cols<BALLOT>(c, item, lane, route, &s_U, cl);
-  if constexpr (BALLOT) {
-    // a token whose ids are all invalid gets y = 0 (Int8-gemm/q8_gemm.cpp:329-332, 599-611)
-    if (item % c.K == 0 && tid < 64) {
-      const int t = item / c.K;
-      if ((cl.vmask & bits_range(t * c.K, c.K)) == 0) c.y[(size_t)t * H + 64 * m + tid] = 0;
-    }
-  }
-  if (!serve) return;  // uniform
+  Cols<0> cl;
+  if (!get_cols<0>(c, item, lane, route, &s_U, cl)) return;  // uniform
   const int e = cl.e, cnt = cl.cnt;
   const size_t blk = (size_t)e * MQ + m;
-  const unsigned char* msrc = a.w2_m + blk * 160 * G2;
-  stage_lds(meta, 10 * G2, wave, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
-  const int c0 = CH * wave / 4, nc = CH * (wave + 1) / 4 - c0;   // equal for all waves (CH % 4 == 0)
-  const char* wb = (const char*)a.w2 + (blk * CH + c0) * 1024 + lane * 16;
-  const int II = I >> 3;
-  constexpr float off = W4Consts<ACT>::offset;
+  const unsigned char* msrc = a.w2_m + blk * 4 * SEC;
+  stage_lds(meta, SEC / 4, wave, 4, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
+  const char* wb = (const char*)a.w2 + (blk * 4 + wave) * G2 * 1024 + lane * 16;
   for (int cb0 = 0; cb0 < cnt; cb0 += P) {
     const int ncol = min(P, cnt - cb0);
-    stage_lds(reinterpret_cast<unsigned char*>(as), ncol * II, wave, lane, [&](int k) {
+    stage_lds(reinterpret_cast<unsigned char*>(as), ncol * II, wave, 4, lane, [&](int k) {
       const int cc = k / II;
-      const int p = cl.pair(cb0 + cc, true);
-      return (const void*)(a.act + (size_t)p * I + 8 * (k - cc * II));
+      return (const void*)(a.act + (size_t)cl.pair(cb0 + cc, true) * I + 8 * (k - cc * II));
     });
-    f32x4_t acc[4];
+    const f32x4_t acc = down_tile<ACT, NB>(wb, as + min(r, ncol - 1) * I + 8 * q, meta + wave * SEC,
+                                          G2, r, a.sdt, true);
+    // lane (r, q): row 64m + 16 wave + r, token columns 4q..4q+3
+    const float vv[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) acc[jj] = f32x4_t{0, 0, 0, 0};
-    for (int cb = 0; cb < nc; cb += NB) {
-      u32x4_t wv[NB];
-#pragma unroll
-      for (int ci = 0; ci < NB; ++ci) wv[ci] = ldg16(wb + (size_t)min(cb + ci, nc - 1) * 1024);
-      if (cb == 0) wait_all_and_sync();   // metadata and act rows are in LDS
-#pragma unroll
-      for (int ci = 0; ci < NB; ++ci) {
-        if (cb + ci >= nc) break;
-        const int ch = c0 + cb + ci, g2 = ch >> 2;
-        const u32x4_t A = r < ncol ? lds16(as + r * I + 32 * ch + 8 * q) : zero4();
-        const f32x4_t X = mfma16<ACT>(A, ones4<ACT>(), f32x4_t{0, 0, 0, 0});
-        const u32x2_t sv = *reinterpret_cast<const u32x2_t*>(meta + 8 * (g2 * 16 + r));
-        const uint32_t zv = *reinterpret_cast<const uint16_t*>(meta + 128 * G2 + 2 * (g2 * 16 + r));
-        const uint32_t ww[4] = {wv[ci].x, wv[ci].y, wv[ci].z, wv[ci].w};
-        const uint32_t sb[4] = {sv.x & 0xffffu, sv.x >> 16, sv.y & 0xffffu, sv.y >> 16};
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const f32x4_t G = mfma16<ACT>(A, deq4<ACT>(ww[jj]), f32x4_t{0, 0, 0, 0});
-          fold(acc[jj], G, X, scale_f32(sb[jj], a.sdt), off + (float)((zv >> (4 * jj)) & 0xfu));
-        }
-      }
+    for (int v = 0; v < 4; ++v) {
+      const int col = cb0 + 4 * q + v;
+      if (col < cnt) c.eout[(size_t)cl.pair(col, true) * H + 64 * m + 16 * wave + r] = vv[v];
     }
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-      *reinterpret_cast<f32x4_t*>(red + ((wave * 4 + jj) * 64 + lane) * 4) = acc[jj];
-    __syncthreads();
-    {
-      const int jj = tid >> 6, ln = tid & 63;
-      f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(red + ((0 * 4 + jj) * 64 + ln) * 4);
-#pragma unroll
-      for (int w = 1; w < 4; ++w) v4 += *reinterpret_cast<const f32x4_t*>(red + ((w * 4 + jj) * 64 + ln) * 4);
-      const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int col = cb0 + 4 * (ln >> 4) + v;
-        const int p = cl.pair(col, col < cnt);
-        if (col < cnt) {
-          float* dst = c.eout + (size_t)p * H + 64 * m + 16 * jj + (ln & 15);
-          if constexpr (BALLOT)
-            __hip_atomic_exchange(reinterpret_cast<uint32_t*>(dst), __float_as_uint(vv[v]),
-                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          else
-            *dst = vv[v];
-        }
-      }
-    }
-    __syncthreads();   // red and as are reused by the next pass
+    __syncthreads();   // the act rows are reused by the next pass
   }
-  if constexpr (BALLOT) {
-    __builtin_amdgcn_s_waitcnt(0);   // this workgroup's exchanges are performed
-    if (tid == 0) s_nd = 0;
-    __syncthreads();
-    if (tid < cnt) {                 // wave 0: lane == column
-      const int t = cl.colpair / c.K;
-      const int nv = __popcll(cl.vmask & bits_range(t * c.K, c.K));
-      const uint32_t old = __hip_atomic_fetch_add(c.arrive + (size_t)t * MQ + m, 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      if ((int)old + 1 == nv) s_done[atomicAdd(&s_nd, 1)] = t;
-    }
-    __syncthreads();
-    const int nd = s_nd;
-    for (int li = 0; li < nd; ++li) {
-      const int t = s_done[li];
-      if (tid < 64) {
-        const int h = 64 * m + tid;
-        float acc = 0.0f;
-        for (int k = 0; k < c.K; ++k) {
-          const int i = t * c.K + k;
-          if ((unsigned)c.ids[i] >= (unsigned)c.E) continue;
-          const uint32_t bits = __hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(c.eout + (size_t)i * H + h),
-                                                      0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const float prod = c.tw[i] * __uint_as_float(bits);
-          acc = acc + prod;
-        }
-        c.y[(size_t)t * H + h] = from_f32<ACT>(acc);
+}
+
+// ================================================================ down (decode)
+// Workgroup (token t, row tile of 16 rows of H), one wave per routed expert
+// k < K of the token (K <= 16): wave k computes out_k = W2[e_k] act[t*K+k] for
+// the tile; then y[t, tile] = cast(sum_k w[t,k] * out_k) over the valid ids in
+// k order -- Stage C1 + C2 of Int8-gemm/q8_gemm.cpp:593-641.  The token's act
+// rows are contiguous and are copied into LDS while the ids are read; a token
+// without a valid id gets y = 0 (Int8-gemm/q8_gemm.cpp:329-332).  No
+// workspace traffic besides act, no cross-workgroup communication.
+// LDS: act rows [K][I] | metadata sections [K][SEC] | outputs [K][16] f32 | valid [K].
+template <int ACT, int NB>
+__global__ __launch_bounds__(1024) void w4a16_down_token_kernel(W4Args a) {
+  const SchedArgs& c = a.c;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = c.H, I = c.I, K = c.K, MQ = H >> 6, G2 = I >> 7, NT = H >> 4, II = I >> 3;
+  const int SEC = w2_meta_sec_bytes(G2);
+  const int t = blockIdx.x / NT, tile = blockIdx.x - t * NT, m = tile >> 2, jj = tile & 3;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  uint16_t* as = reinterpret_cast<uint16_t*>(smem);
+  unsigned char* meta = smem + (size_t)K * I * 2;
+  float* outs = reinterpret_cast<float*>(meta + (size_t)K * SEC);
+  int* valid = reinterpret_cast<int*>(outs + 16 * K);
+  const int i = t * K + wave;   // this wave's pair
+  const int e = c.ids[i];
+  stage_lds(reinterpret_cast<unsigned char*>(as), K * II, wave, K, lane,
+                [&](int k) { return (const void*)(a.act + (size_t)t * K * I + 8 * (size_t)k); });
+  // a wave with an invalid id computes on expert 0 and its output is ignored,
+  // so every wave runs the same code (one barrier each)
+  const bool ok = (unsigned)e < (unsigned)c.E;
+  const size_t blk = ((size_t)(ok ? e : 0) * MQ + m) * 4 + jj;
+  if (lane < SEC / 16)
+    __builtin_amdgcn_global_load_lds(a.w2_m + blk * SEC + 16 * lane, meta + wave * SEC, 16, 0, 0);
+  if (lane == 0) valid[wave] = ok;
+  const char* wb = (const char*)a.w2 + blk * G2 * 1024 + lane * 16;
+  const f32x4_t acc = down_tile<ACT, NB>(wb, as + wave * I + 8 * q, meta + wave * SEC, G2, r, a.sdt, true);
+  if (lane < 16) outs[16 * wave + lane] = acc.x;   // column 0: lanes (r, q = 0)
+  __syncthreads();
+  if (tid < 16) {
+    float y = 0.0f;
+    for (int k = 0; k < K; ++k)
+      if (valid[k]) {
+        const float prod = c.tw[t * K + k] * outs[16 * k + tid];
+        y = y + prod;
       }
-      if (tid == 0)
-        __hip_atomic_exchange(c.arrive + (size_t)t * MQ + m, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    c.y[(size_t)t * H + 16 * tile + tid] = from_f32<ACT>(y);
   }
 }
 
@@ -486,20 +518,22 @@ __global__ void awq_repack_w13_meta(const uint16_t* __restrict__ scales, const i
   }
 }
 
-// w2: one thread per device u32 word: (e, quad m, chunk c, lane, word jj).
+// w2: one thread per device u32 word: (e, quad m, row tile jj, group g2,
+// lane, chunk cc of the group).
 __global__ void awq_repack_w2(const int32_t* __restrict__ src, uint32_t* __restrict__ dst, int E,
                               int H, int I) {
-  const int CH = I >> 5, MQ = H >> 6;
-  const size_t total = (size_t)E * MQ * CH * 256;
+  const int G2 = I >> 7, MQ = H >> 6;
+  const size_t total = (size_t)E * MQ * 4 * G2 * 256;
   for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (size_t)gridDim.x * blockDim.x) {
-    const int jj = idx & 3, lane = (idx >> 2) & 63;
+    const int cc = idx & 3, lane = (idx >> 2) & 63;
     size_t t = idx >> 8;
-    const int cc = t % CH; t /= CH;
+    const int g2 = t % G2; t /= G2;
+    const int jj = t % 4; t /= 4;
     const int m = t % MQ;
     const int e = (int)(t / MQ);
     const int h = 64 * m + 16 * jj + (lane & 15);
-    const int k0 = 32 * cc + 8 * (lane >> 4);
+    const int k0 = 128 * g2 + 32 * cc + 8 * (lane >> 4);
     const int32_t* base = src + (size_t)e * I * (H / 8);
     uint32_t word = 0;
 #pragma unroll
@@ -510,26 +544,30 @@ __global__ void awq_repack_w2(const int32_t* __restrict__ src, uint32_t* __restr
   }
 }
 
-// w2 metadata blocks: one thread per (e, m, g2, r).
+// w2 metadata: one section of w2_meta_sec_bytes(G2) bytes per (e, m, jj):
+// scales u16 [g2][r], then zeros [g2][r/2] (row r in nibble r&1); one thread
+// per (e, m, jj, g2, row pair).
 __global__ void awq_repack_w2_meta(const uint16_t* __restrict__ scales, const int32_t* __restrict__ qzeros,
                                    unsigned char* __restrict__ m_dst, int E, int H, int I) {
-  const int G2 = I >> 7, MQ = H >> 6;
-  const size_t total = (size_t)E * MQ * G2 * 16;
+  const int G2 = I >> 7, MQ = H >> 6, SEC = w2_meta_sec_bytes(G2);
+  const size_t total = (size_t)E * MQ * 4 * G2 * 8;
   for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (size_t)gridDim.x * blockDim.x) {
-    const int r = idx & 15;
-    size_t t = idx >> 4;
+    const int r2 = idx & 7;
+    size_t t = idx >> 3;
     const int g2 = t % G2; t /= G2;
+    const int jj = t % 4; t /= 4;
     const int m = t % MQ;
     const int e = (int)(t / MQ);
-    unsigned char* blk = m_dst + ((size_t)e * MQ + m) * 160 * G2;
-    uint32_t zq = 0;
-    for (int jj = 0; jj < 4; ++jj) {
-      const int h = 64 * m + 16 * jj + r;
-      reinterpret_cast<uint16_t*>(blk)[(g2 * 16 + r) * 4 + jj] = scales[((size_t)e * G2 + g2) * H + h];
-      zq |= awq_nib(qzeros + (size_t)e * G2 * (H / 8), H, g2, h) << (4 * jj);
+    unsigned char* sec = m_dst + (((size_t)e * MQ + m) * 4 + jj) * SEC;
+    const int32_t* zb = qzeros + (size_t)e * G2 * (H / 8);
+    uint32_t zz = 0;
+    for (int hh = 0; hh < 2; ++hh) {
+      const int r = 2 * r2 + hh, h = 64 * m + 16 * jj + r;
+      reinterpret_cast<uint16_t*>(sec)[16 * g2 + r] = scales[((size_t)e * G2 + g2) * H + h];
+      zz |= awq_nib(zb, H, g2, h) << (4 * hh);
     }
-    reinterpret_cast<uint16_t*>(blk + 128 * G2)[g2 * 16 + r] = (uint16_t)zq;
+    sec[32 * G2 + 8 * g2 + r2] = (unsigned char)zz;
   }
 }
 
@@ -549,20 +587,21 @@ hipError_t launch_awq_repack_all(const int32_t* w13q, const int32_t* w13z, const
                      st, w13s, w13z, d13m, E, H, I);
   hipLaunchKernelGGL(awq_repack_w2, dim3(grid_for((size_t)E * CH * MQ * 256)), dim3(256), 0, st,
                      w2q, (uint32_t*)d2, E, H, I);
-  hipLaunchKernelGGL(awq_repack_w2_meta, dim3(grid_for((size_t)E * G2 * MQ * 16)), dim3(256), 0, st,
+  hipLaunchKernelGGL(awq_repack_w2_meta, dim3(grid_for((size_t)E * MQ * 4 * G2 * 8)), dim3(256), 0, st,
                      w2s, w2z, d2m, E, H, I);
   return hipGetLastError();
 }
 
 // ================================================================ launchers
 // Instantiated batch sizes (weights per wave in flight together).
-constexpr int kP1Batches[] = {1, 2, 4, 6, 8};
-constexpr int kP2Batches[] = {1, 2, 4, 6, 8, 12};
+constexpr int kP1Batches[] = {1, 2, 3, 4, 6, 8};
+constexpr int kP2Batches[] = {1, 2, 3, 4, 6, 8, 12};
 
+// largest instantiated size that divides the per-wave count
 static int pick_batch(const int* sizes, int count, int need) {
-  int b = sizes[0];
+  int b = 1;
   for (int i = 0; i < count; ++i)
-    if (sizes[i] <= need) b = sizes[i];
+    if (need % sizes[i] == 0) b = sizes[i];
   return b;
 }
 
@@ -570,38 +609,43 @@ template <int ACT, int BALLOT, int NB>
 static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
   hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, BALLOT, NB>), dim3(grid), dim3(kBlock), lds, st, a);
 }
-template <int ACT, int BALLOT, int NB>
-static void launch_p2(const W4Args& a, int grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((w4a16_phase2_kernel<ACT, BALLOT, NB>), dim3(grid), dim3(kBlock), lds, st, a);
+template <int ACT, int NB>
+static void launch_p2(const W4Args& a, int ballot, int grid, size_t lds, hipStream_t st) {
+  if (ballot)
+    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB>), dim3(grid), dim3(64 * a.c.K), lds, st, a);
+  else
+    hipLaunchKernelGGL((w4a16_phase2_kernel<ACT, NB>), dim3(grid), dim3(kBlock), lds, st, a);
 }
 
 template <int ACT, int BALLOT>
 static hipError_t launch_w4_t(const W4Args& a, int grid1, int grid2, hipStream_t st) {
-  const size_t route = (BALLOT || a.c.route_global) ? 0 : route_lds_ints(a.c.E, a.c.n) * sizeof(int);
-  const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.p1_cols) + route;
-  const size_t lds2 = w4_p2_lds_bytes(a.c.I, a.p2_cols) + route;
-  switch (pick_batch(kP1Batches, 5, a.c.H / 512)) {
+  const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols) + a.route_lds;
+  const size_t lds2 = BALLOT ? w4_down_token_lds_bytes(a.c.I, a.c.K)
+                             : w4_p2_lds_bytes(a.c.I, a.p2_cols) + a.route_lds;
+  switch (pick_batch(kP1Batches, 6, a.c.H / 512)) {
     case 1: launch_p1<ACT, BALLOT, 1>(a, grid1, lds1, st); break;
     case 2: launch_p1<ACT, BALLOT, 2>(a, grid1, lds1, st); break;
+    case 3: launch_p1<ACT, BALLOT, 3>(a, grid1, lds1, st); break;
     case 4: launch_p1<ACT, BALLOT, 4>(a, grid1, lds1, st); break;
     case 6: launch_p1<ACT, BALLOT, 6>(a, grid1, lds1, st); break;
     default: launch_p1<ACT, BALLOT, 8>(a, grid1, lds1, st); break;
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  switch (pick_batch(kP2Batches, 6, a.c.I / 128)) {
-    case 1: launch_p2<ACT, BALLOT, 1>(a, grid2, lds2, st); break;
-    case 2: launch_p2<ACT, BALLOT, 2>(a, grid2, lds2, st); break;
-    case 4: launch_p2<ACT, BALLOT, 4>(a, grid2, lds2, st); break;
-    case 6: launch_p2<ACT, BALLOT, 6>(a, grid2, lds2, st); break;
-    case 8: launch_p2<ACT, BALLOT, 8>(a, grid2, lds2, st); break;
-    default: launch_p2<ACT, BALLOT, 12>(a, grid2, lds2, st); break;
+  switch (pick_batch(kP2Batches, 7, a.c.I / 128)) {
+    case 1: launch_p2<ACT, 1>(a, BALLOT, grid2, lds2, st); break;
+    case 2: launch_p2<ACT, 2>(a, BALLOT, grid2, lds2, st); break;
+    case 3: launch_p2<ACT, 3>(a, BALLOT, grid2, lds2, st); break;
+    case 4: launch_p2<ACT, 4>(a, BALLOT, grid2, lds2, st); break;
+    case 6: launch_p2<ACT, 6>(a, BALLOT, grid2, lds2, st); break;
+    case 8: launch_p2<ACT, 8>(a, BALLOT, grid2, lds2, st); break;
+    default: launch_p2<ACT, 12>(a, BALLOT, grid2, lds2, st); break;
   }
   return hipGetLastError();
 }
 
-// ballot = 1 (T*K <= 64): grid1 = T*K * I/16, grid2 = T*K * H/64, phase 2
-// combines and writes y.  ballot = 0: grid1 = U * I/16, grid2 = U * H/64 with
+// ballot = 1 (T*K <= 64, K <= 16): grid1 = T*K * I/16, grid2 = T * H/16 (down
+// kernel, writes y).  ballot = 0: grid1 = U * I/16, grid2 = U * H/64 with
 // U = min(T*K, E) and sorted routing; the caller launches the combine.
 hipError_t launch_w4a16(const W4Args& a, int act, int ballot, int grid1, int grid2, hipStream_t st) {
   if (act == 1) return ballot ? launch_w4_t<1, 1>(a, grid1, grid2, st) : launch_w4_t<1, 0>(a, grid1, grid2, st);
