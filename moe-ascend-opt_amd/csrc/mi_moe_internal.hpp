@@ -52,17 +52,26 @@ struct W4Args {
 // scales and 8 bytes of zero nibbles, rounded up to 16 bytes.
 __host__ __device__ inline int w2_meta_sec_bytes(int G2) { return (40 * G2 + 15) & ~15; }
 
+// The decode down kernel runs a wave per routed expert of a token.
+constexpr int kDownMaxK = 8;
+
 // LDS bytes of the W4A16 kernels (routing arrays come on top).
 constexpr int kP1RedBytes = 4 * 2 * 64 * 4 * 4;
-__host__ __device__ inline size_t w4_p1_lds_bytes(int H, int xrows) {
-  return (size_t)kP1RedBytes + (size_t)80 * (H >> 7) + (size_t)xrows * H * 2;
+__host__ __device__ inline size_t w4_p1_lds_bytes(int H, int xrows, int slices) {
+  return (size_t)slices * (kP1RedBytes + 80 * (H >> 7)) + (size_t)xrows * H * 2;
 }
 __host__ __device__ inline size_t w4_p2_lds_bytes(int I, int cols) {
   return (size_t)4 * w2_meta_sec_bytes(I >> 7) + (size_t)cols * I * 2;
 }
-__host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K) {
-  return (size_t)K * I * 2 + (size_t)K * w2_meta_sec_bytes(I >> 7) + (size_t)K * 16 * 4 + (size_t)K * 4;
+__host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) {
+  return (size_t)K * I * 2 + (size_t)K * RT * w2_meta_sec_bytes(I >> 7) + (size_t)K * 16 * RT * 4 + (size_t)K * 4;
 }
+
+// Launch geometry of the W4A16 kernels (see w4a16_plan).
+struct W4Plan {
+  int nb1, s1;    // phase 1: groups per load batch, 16-row slices per workgroup
+  int nb2, rt2;   // down: groups per load batch, 16-row tiles per wave
+};
 
 // Q8_0 / Q4_0 fused kernel (qint.hip).
 struct QArgs {

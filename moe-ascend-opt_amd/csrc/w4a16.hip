@@ -215,46 +215,44 @@ __device__ __forceinline__ bool get_cols(const SchedArgs& c, int item, int lane,
 }
 
 // ================================================================ phase 1
-// Workgroup (item, 16-row slice j): gate/up rows j*16.. of the item's expert
-// over all H (the 4 waves split the H groups), every routed pair of the expert
-// in passes of p1_cols columns; SiLU*mul into act[pair].  Each wave keeps the
-// weights of NB groups in flight together (NB, from the host, divides the
-// wave's H/512 groups).  Lanes of columns past the pass read the pass's last
-// column, so the loop body has no branches; their results are never stored.
-// Hidden rows: with a.x_all the rows of all T tokens are copied into LDS at
-// kernel start, in parallel with the routing read; otherwise the rows of each
-// pass's columns are copied once the routing is known.
-// LDS: red [wave][gate,up][64][4] f32 | metadata 80*G1 B | x rows | routing.
-template <int ACT, int BALLOT, int NB>
+// Workgroup (item, slices j = S*js .. S*js+S-1 of 16 rows): gate/up rows of
+// the item's expert over all H (the 4 waves split the H groups), every routed
+// pair of the expert in passes of p1_cols columns; SiLU*mul into act[pair].
+// Each wave keeps the weights of NB groups x S slices in flight together (NB,
+// from the host, divides the wave's H/512 groups); the column sums X of a
+// group are shared by the S slices.  Lanes of columns past the pass read the
+// pass's last column, so the loop body has no branches; their results are
+// never stored.  Hidden rows: with a.x_all the rows of all T tokens are copied
+// into LDS at kernel start, in parallel with the routing read; otherwise the
+// rows of each pass's columns are copied once the routing is known.
+// LDS (w4_p1_lds_bytes): red [S][wave][gate,up][64][4] f32 | metadata S x 80*G1 B | x rows | routing.
+template <int ACT, int BALLOT, int NB, int S>
 __global__ __launch_bounds__(kBlock) void w4a16_phase1_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
-  const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, P = a.p1_cols, HI = H >> 3;
+  const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, NJS = NI1 / S, P = a.p1_cols, HI = H >> 3;
   const int XR = a.x_all ? c.T : P;   // rows of x held in LDS
   float* red = reinterpret_cast<float*>(smem);
-  unsigned char* meta = smem + kP1RedBytes;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(meta + 80 * G1);
+  unsigned char* meta = smem + S * kP1RedBytes;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(meta + S * 80 * G1);
   unsigned char* route = reinterpret_cast<unsigned char*>(xs) + (size_t)XR * H * 2;
-  const int item = blockIdx.x / NI1, j = blockIdx.x - item * NI1;
+  const int item = blockIdx.x / NJS, j0 = (blockIdx.x - item * NJS) * S;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   if (a.x_all)   // uniform; x is [T][H] contiguous
     stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, 4, lane,
-                 [&](int k) { return (const void*)(c.x + 8 * (size_t)k); });
+              [&](int k) { return (const void*)(c.x + 8 * (size_t)k); });
   Cols<BALLOT> cl;
   if (!get_cols<BALLOT>(c, item, lane, route, &s_U, cl)) {   // uniform
     __builtin_amdgcn_s_waitcnt(0);   // no copy into LDS outlives the workgroup
     return;
   }
   const int e = cl.e, cnt = cl.cnt;
-  const size_t blk = (size_t)e * NI1 + j;
+  const size_t blk = (size_t)e * NI1 + j0;   // S consecutive slices: contiguous weights and metadata
   const unsigned char* msrc = a.w13_m + blk * 80 * G1;
-  stage_lds(meta, 5 * G1, wave, 4, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
+  stage_lds(meta, S * 5 * G1, wave, 4, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
   const int g0 = G1 * wave / 4, ng = G1 * (wave + 1) / 4 - g0;   // equal for all waves (G1 % 4 == 0)
-  const char* wg = (const char*)a.w13 + (blk * 2 * G1 + g0) * 1024 + lane * 16;
-  const char* wu = wg + (size_t)G1 * 1024;
-  const uint32_t* msc = reinterpret_cast<const uint32_t*>(meta) + r * G1;
-  const unsigned char* mz = meta + 64 * G1 + r * G1;
+  const char* wg = (const char*)a.w13 + (blk * 2 * G1 + g0) * 1024 + lane * 16;   // slice s: + 2*G1 KB
   constexpr float off = W4Consts<ACT>::offset;
   for (int cb0 = 0; cb0 < cnt; cb0 += P) {
     const int ncol = min(P, cnt - cb0);
@@ -270,62 +268,80 @@ __global__ __launch_bounds__(kBlock) void w4a16_phase1_kernel(W4Args a) {
       xr = min(r, ncol - 1);
     }
     const uint16_t* xrow = xs + xr * H + 32 * q;
-    f32x4_t accg = {0, 0, 0, 0}, accu = {0, 0, 0, 0};
+    f32x4_t accg[S], accu[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) accg[s] = accu[s] = f32x4_t{0, 0, 0, 0};
     issue_order_fence();
     for (int gb = 0; gb < ng; gb += NB) {
-      u32x4_t wgv[NB], wuv[NB];
+      u32x4_t wgv[S][NB], wuv[S][NB];
 #pragma unroll
-      for (int gi = 0; gi < NB; ++gi) {
-        wgv[gi] = ldg16(wg + (size_t)(gb + gi) * 1024);
-        wuv[gi] = ldg16(wu + (size_t)(gb + gi) * 1024);
-      }
-      if (gb == 0) wait_copies_and_sync<2 * NB>();   // metadata and x rows are in LDS
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int gi = 0; gi < NB; ++gi) {
+          const char* p = wg + ((size_t)s * 2 * G1 + gb + gi) * 1024;
+          wgv[s][gi] = ldg16(p);
+          wuv[s][gi] = ldg16(p + (size_t)G1 * 1024);
+        }
+      if (gb == 0) wait_copies_and_sync<2 * NB * S>();   // metadata and x rows are in LDS
 #pragma unroll
       for (int gi = 0; gi < NB; ++gi) {
         const int g = g0 + gb + gi;
         u32x4_t A[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) A[i] = lds16(xrow + 128 * g + 8 * i);
-        f32x4_t X = {0, 0, 0, 0}, Gg = {0, 0, 0, 0}, Gu = {0, 0, 0, 0};
-        const uint32_t wgw[4] = {wgv[gi].x, wgv[gi].y, wgv[gi].z, wgv[gi].w};
-        const uint32_t wuw[4] = {wuv[gi].x, wuv[gi].y, wuv[gi].z, wuv[gi].w};
+        f32x4_t X = {0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          X = mfma16<ACT>(A[i], ones4<ACT>(), X);
-          Gg = mfma16<ACT>(A[i], deq4<ACT>(wgw[i]), Gg);
-          Gu = mfma16<ACT>(A[i], deq4<ACT>(wuw[i]), Gu);
+        for (int i = 0; i < 4; ++i) X = mfma16<ACT>(A[i], ones4<ACT>(), X);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          f32x4_t Gg = {0, 0, 0, 0}, Gu = {0, 0, 0, 0};
+          const uint32_t wgw[4] = {wgv[s][gi].x, wgv[s][gi].y, wgv[s][gi].z, wgv[s][gi].w};
+          const uint32_t wuw[4] = {wuv[s][gi].x, wuv[s][gi].y, wuv[s][gi].z, wuv[s][gi].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            Gg = mfma16<ACT>(A[i], deq4<ACT>(wgw[i]), Gg);
+            Gu = mfma16<ACT>(A[i], deq4<ACT>(wuw[i]), Gu);
+          }
+          const unsigned char* ms = meta + s * 80 * G1;
+          const uint32_t sc = reinterpret_cast<const uint32_t*>(ms)[r * G1 + g];
+          const uint32_t zz = ms[64 * G1 + r * G1 + g];
+          fold(accg[s], Gg, X, scale_f32(sc & 0xffffu, a.sdt), off + (float)(zz & 0xfu));
+          fold(accu[s], Gu, X, scale_f32(sc >> 16, a.sdt), off + (float)(zz >> 4));
         }
-        const uint32_t sc = msc[g];
-        const uint32_t zz = mz[g];
-        fold(accg, Gg, X, scale_f32(sc & 0xffffu, a.sdt), off + (float)(zz & 0xfu));
-        fold(accu, Gu, X, scale_f32(sc >> 16, a.sdt), off + (float)(zz >> 4));
       }
     }
-    *reinterpret_cast<f32x4_t*>(red + ((wave * 2 + 0) * 64 + lane) * 4) = accg;
-    *reinterpret_cast<f32x4_t*>(red + ((wave * 2 + 1) * 64 + lane) * 4) = accu;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      float* rs = red + s * (kP1RedBytes / 4);
+      *reinterpret_cast<f32x4_t*>(rs + ((wave * 2 + 0) * 64 + lane) * 4) = accg[s];
+      *reinterpret_cast<f32x4_t*>(rs + ((wave * 2 + 1) * 64 + lane) * 4) = accu[s];
+    }
     __syncthreads();
-    if (tid < 64) {
-      f32x4_t g = *reinterpret_cast<const f32x4_t*>(red + ((0 * 2 + 0) * 64 + tid) * 4);
-      f32x4_t u = *reinterpret_cast<const f32x4_t*>(red + ((0 * 2 + 1) * 64 + tid) * 4);
+    if (tid < 64 * S) {   // thread (slice s, lane ln)
+      const int s = tid >> 6, ln = tid & 63;
+      const float* rs = red + s * (kP1RedBytes / 4);
+      f32x4_t g = *reinterpret_cast<const f32x4_t*>(rs + ((0 * 2 + 0) * 64 + ln) * 4);
+      f32x4_t u = *reinterpret_cast<const f32x4_t*>(rs + ((0 * 2 + 1) * 64 + ln) * 4);
 #pragma unroll
       for (int w = 1; w < 4; ++w) {
-        g += *reinterpret_cast<const f32x4_t*>(red + ((w * 2 + 0) * 64 + tid) * 4);
-        u += *reinterpret_cast<const f32x4_t*>(red + ((w * 2 + 1) * 64 + tid) * 4);
+        g += *reinterpret_cast<const f32x4_t*>(rs + ((w * 2 + 0) * 64 + ln) * 4);
+        u += *reinterpret_cast<const f32x4_t*>(rs + ((w * 2 + 1) * 64 + ln) * 4);
       }
       const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int col = cb0 + 4 * (tid >> 4) + v;
+        const int col = cb0 + 4 * (ln >> 4) + v;
         const int p = cl.pair(col, col < cnt);
-        if (col < cnt) a.act[(size_t)p * c.I + 16 * j + (tid & 15)] = from_f32<ACT>(silu_mul(gv[v], uv[v]));
+        if (col < cnt)
+          a.act[(size_t)p * c.I + 16 * (j0 + s) + (ln & 15)] = from_f32<ACT>(silu_mul(gv[v], uv[v]));
       }
     }
     __syncthreads();   // red and xs are reused by the next pass
   }
 }
 
-// Scales and zeros of the (16 row x 128 k) groups of one w2 row tile jj of a
-// quad block: scales u16 [g2][r], then zeros [g2][r/2] (row r in nibble r&1).
+// Scales and zeros of the (16 row x 128 k) groups of one w2 row tile: a
+// section holds scales u16 [g2][r], then zeros [g2][r/2] (row r in nibble r&1).
 __device__ __forceinline__ float w2_scale(const unsigned char* sec, int g2, int r, int sdt) {
   return scale_f32(reinterpret_cast<const uint16_t*>(sec)[16 * g2 + r], sdt);
 }
@@ -333,40 +349,48 @@ __device__ __forceinline__ float w2_zero(const unsigned char* sec, int G2, int g
   return (float)((sec[32 * G2 + 8 * g2 + (r >> 1)] >> (4 * (r & 1))) & 0xfu);
 }
 
-// Down projection of one row tile (16 rows) over all I for 16 token columns:
-// acc += sum over groups of s * (G - (offset + z) X).  A rows come from LDS
-// (arow: this lane's column, k offset 8q), weights from wb (G2 words of 16 B
-// per lane, NB in flight together).  sync_first: wait for the LDS copies and
-// barrier after the first batch of weight loads is issued.
-template <int ACT, int NB>
-__device__ __forceinline__ f32x4_t down_tile(const char* wb, const uint16_t* arow,
-                                             const unsigned char* sec, int G2, int r, int sdt,
-                                             bool sync_first) {
+// Down projection of RT consecutive row tiles (16 rows each) over all I for 16
+// token columns: acc[rt] += sum over groups of s * (G - (offset + z) X).  A
+// rows come from LDS (arow: this lane's column, k offset 8q), weights from wb
+// (tile rt at wb + rt*G2 KB, G2 words of 16 B per lane, NB groups x RT tiles
+// in flight together), metadata sections from secs (tile rt at secs +
+// rt*SEC).  The column sums X of a group are shared by the RT tiles.  Waits
+// for the LDS copies and barriers after the first batch of loads is issued.
+template <int ACT, int NB, int RT>
+__device__ __forceinline__ void down_tiles(const char* wb, const uint16_t* arow,
+                                           const unsigned char* secs, int SEC, int G2, int r,
+                                           int sdt, f32x4_t (&acc)[RT]) {
   constexpr float off = W4Consts<ACT>::offset;
-  f32x4_t acc = {0, 0, 0, 0};
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0, 0, 0, 0};
   issue_order_fence();
   for (int gb = 0; gb < G2; gb += NB) {
-    u32x4_t wv[NB];
+    u32x4_t wv[RT][NB];
 #pragma unroll
-    for (int gi = 0; gi < NB; ++gi) wv[gi] = ldg16(wb + (size_t)(gb + gi) * 1024);
-    if (gb == 0 && sync_first) wait_copies_and_sync<NB>();   // the LDS operands are in place
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int gi = 0; gi < NB; ++gi) wv[rt][gi] = ldg16(wb + ((size_t)rt * G2 + gb + gi) * 1024);
+    if (gb == 0) wait_copies_and_sync<NB * RT>();   // the LDS operands are in place
 #pragma unroll
     for (int gi = 0; gi < NB; ++gi) {
       const int g2 = gb + gi;
       u32x4_t A[4];
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) A[cc] = lds16(arow + 128 * g2 + 32 * cc);
-      f32x4_t X = {0, 0, 0, 0}, G = {0, 0, 0, 0};
-      const uint32_t ww[4] = {wv[gi].x, wv[gi].y, wv[gi].z, wv[gi].w};
+      f32x4_t X = {0, 0, 0, 0};
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) {
-        X = mfma16<ACT>(A[cc], ones4<ACT>(), X);
-        G = mfma16<ACT>(A[cc], deq4<ACT>(ww[cc]), G);
+      for (int cc = 0; cc < 4; ++cc) X = mfma16<ACT>(A[cc], ones4<ACT>(), X);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        f32x4_t G = {0, 0, 0, 0};
+        const uint32_t ww[4] = {wv[rt][gi].x, wv[rt][gi].y, wv[rt][gi].z, wv[rt][gi].w};
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) G = mfma16<ACT>(A[cc], deq4<ACT>(ww[cc]), G);
+        const unsigned char* sec = secs + rt * SEC;
+        fold(acc[rt], G, X, w2_scale(sec, g2, r, sdt), off + w2_zero(sec, G2, g2, r));
       }
-      fold(acc, G, X, w2_scale(sec, g2, r, sdt), off + w2_zero(sec, G2, g2, r));
     }
   }
-  return acc;
 }
 
 // ================================================================ phase 2 (general)
@@ -377,7 +401,7 @@ __device__ __forceinline__ f32x4_t down_tile(const char* wb, const uint16_t* aro
 // 16-byte weight word holds its row's four 32-k chunks of one 128-k group, so
 // the group's four MFMAs accumulate in the matrix core and its scale and zero
 // are applied once.  NB, from the host, divides I/128.
-// LDS: metadata block | act rows [p2_cols][I] | routing.
+// LDS: metadata sections [4][SEC] | act rows [p2_cols][I] | routing.
 template <int ACT, int NB>
 __global__ __launch_bounds__(kBlock) void w4a16_phase2_kernel(W4Args a) {
   const SchedArgs& c = a.c;
@@ -403,10 +427,11 @@ __global__ __launch_bounds__(kBlock) void w4a16_phase2_kernel(W4Args a) {
       const int cc = k / II;
       return (const void*)(a.act + (size_t)cl.pair(cb0 + cc, true) * I + 8 * (k - cc * II));
     });
-    const f32x4_t acc = down_tile<ACT, NB>(wb, as + min(r, ncol - 1) * I + 8 * q, meta + wave * SEC,
-                                          G2, r, a.sdt, true);
+    f32x4_t acc[1];
+    down_tiles<ACT, NB, 1>(wb, as + min(r, ncol - 1) * I + 8 * q, meta + wave * SEC, SEC, G2, r,
+                           a.sdt, acc);
     // lane (r, q): row 64m + 16 wave + r, token columns 4q..4q+3
-    const float vv[4] = {acc.x, acc.y, acc.z, acc.w};
+    const float vv[4] = {acc[0].x, acc[0].y, acc[0].z, acc[0].w};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int col = cb0 + 4 * q + v;
@@ -417,49 +442,54 @@ __global__ __launch_bounds__(kBlock) void w4a16_phase2_kernel(W4Args a) {
 }
 
 // ================================================================ down (decode)
-// Workgroup (token t, row tile of 16 rows of H), one wave per routed expert
-// k < K of the token (K <= 16): wave k computes out_k = W2[e_k] act[t*K+k] for
-// the tile; then y[t, tile] = cast(sum_k w[t,k] * out_k) over the valid ids in
-// k order -- Stage C1 + C2 of Int8-gemm/q8_gemm.cpp:593-641.  The token's act
-// rows are contiguous and are copied into LDS while the ids are read; a token
-// without a valid id gets y = 0 (Int8-gemm/q8_gemm.cpp:329-332).  No
-// workspace traffic besides act, no cross-workgroup communication.
-// LDS: act rows [K][I] | metadata sections [K][SEC] | outputs [K][16] f32 | valid [K].
-template <int ACT, int NB>
-__global__ __launch_bounds__(1024) void w4a16_down_token_kernel(W4Args a) {
+// Workgroup (token t, RT consecutive 16-row tiles of H), one wave per routed
+// expert k < K of the token (K <= kDownMaxK): wave k computes out_k = W2[e_k]
+// act[t*K+k] for the tiles; then y[t, tiles] = cast(sum_k w[t,k] * out_k)
+// over the valid ids in k order -- Stage C1 + C2 of
+// Int8-gemm/q8_gemm.cpp:593-641.  The token's act rows are contiguous and are
+// copied into LDS while the ids are read; a token without a valid id gets
+// y = 0 (Int8-gemm/q8_gemm.cpp:329-332).  No workspace traffic besides act,
+// no cross-workgroup communication.
+// LDS: act rows [K][I] | metadata [K][RT][SEC] | outputs [K][16 RT] f32 | valid [K].
+template <int ACT, int NB, int RT>
+__global__ __launch_bounds__(kDownMaxK * 64) void w4a16_down_token_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, I = c.I, K = c.K, MQ = H >> 6, G2 = I >> 7, NT = H >> 4, II = I >> 3;
+  const int H = c.H, I = c.I, K = c.K, MQ = H >> 6, G2 = I >> 7, NTG = (H >> 4) / RT, II = I >> 3;
   const int SEC = w2_meta_sec_bytes(G2);
-  const int t = blockIdx.x / NT, tile = blockIdx.x - t * NT, m = tile >> 2, jj = tile & 3;
+  const int t = blockIdx.x / NTG, tile0 = (blockIdx.x - t * NTG) * RT, m = tile0 >> 2, jj0 = tile0 & 3;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   uint16_t* as = reinterpret_cast<uint16_t*>(smem);
   unsigned char* meta = smem + (size_t)K * I * 2;
-  float* outs = reinterpret_cast<float*>(meta + (size_t)K * SEC);
-  int* valid = reinterpret_cast<int*>(outs + 16 * K);
+  float* outs = reinterpret_cast<float*>(meta + (size_t)K * RT * SEC);
+  int* valid = reinterpret_cast<int*>(outs + 16 * RT * K);
   const int i = t * K + wave;   // this wave's pair
   const int e = c.ids[i];
   stage_lds(reinterpret_cast<unsigned char*>(as), K * II, wave, K, lane,
-                [&](int k) { return (const void*)(a.act + (size_t)t * K * I + 8 * (size_t)k); });
+            [&](int k) { return (const void*)(a.act + (size_t)t * K * I + 8 * (size_t)k); });
   // a wave with an invalid id computes on expert 0 and its output is ignored,
   // so every wave runs the same code (one barrier each)
   const bool ok = (unsigned)e < (unsigned)c.E;
-  const size_t blk = ((size_t)(ok ? e : 0) * MQ + m) * 4 + jj;
-  if (lane < SEC / 16)
-    __builtin_amdgcn_global_load_lds(a.w2_m + blk * SEC + 16 * lane, meta + wave * SEC, 16, 0, 0);
+  const size_t sec0 = ((size_t)(ok ? e : 0) * MQ + m) * 4 + jj0;   // RT tiles within one quad: contiguous
+  unsigned char* mdst = meta + wave * RT * SEC;
+  for (int l = lane; l < RT * SEC / 16; l += 64)
+    __builtin_amdgcn_global_load_lds(a.w2_m + sec0 * SEC + 16 * l, mdst + (l - lane) * 16, 16, 0, 0);
   if (lane == 0) valid[wave] = ok;
-  const char* wb = (const char*)a.w2 + blk * G2 * 1024 + lane * 16;
-  const f32x4_t acc = down_tile<ACT, NB>(wb, as + wave * I + 8 * q, meta + wave * SEC, G2, r, a.sdt, true);
-  if (lane < 16) outs[16 * wave + lane] = acc.x;   // column 0: lanes (r, q = 0)
+  const char* wb = (const char*)a.w2 + sec0 * G2 * 1024 + lane * 16;
+  f32x4_t acc[RT];
+  down_tiles<ACT, NB, RT>(wb, as + wave * I + 8 * q, mdst, SEC, G2, r, a.sdt, acc);
+  if (lane < 16)   // column 0: lanes (r, q = 0)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) outs[16 * (RT * wave + rt) + lane] = acc[rt].x;
   __syncthreads();
-  if (tid < 16) {
+  if (tid < 16 * RT) {
     float y = 0.0f;
     for (int k = 0; k < K; ++k)
       if (valid[k]) {
-        const float prod = c.tw[t * K + k] * outs[16 * k + tid];
+        const float prod = c.tw[t * K + k] * outs[16 * RT * k + tid];
         y = y + prod;
       }
-    c.y[(size_t)t * H + 16 * tile + tid] = from_f32<ACT>(y);
+    c.y[(size_t)t * H + 16 * tile0 + tid] = from_f32<ACT>(y);
   }
 }
 
@@ -593,63 +623,83 @@ hipError_t launch_awq_repack_all(const int32_t* w13q, const int32_t* w13z, const
 }
 
 // ================================================================ launchers
-// Instantiated batch sizes (weights per wave in flight together).
-constexpr int kP1Batches[] = {1, 2, 3, 4, 6, 8};
-constexpr int kP2Batches[] = {1, 2, 3, 4, 6, 8, 12};
+template <int ACT, int BALLOT, int NB, int S>
+static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, BALLOT, NB, S>), dim3(grid), dim3(kBlock), lds, st, a);
+}
 
-// largest instantiated size that divides the per-wave count
-static int pick_batch(const int* sizes, int count, int need) {
+// (NB, S) pairs instantiated for phase 1.  S > 1 measured slower on the
+// decode shapes (occupancy), so only S = 1 is built.
+template <int ACT, int BALLOT>
+static hipError_t dispatch_p1(const W4Args& a, int nb, int s, int grid, size_t lds, hipStream_t st) {
+#define P1_CASE(NB_, S_) \
+  if (nb == NB_ && s == S_) { launch_p1<ACT, BALLOT, NB_, S_>(a, grid, lds, st); return hipGetLastError(); }
+  P1_CASE(1, 1) P1_CASE(2, 1) P1_CASE(3, 1) P1_CASE(4, 1) P1_CASE(6, 1) P1_CASE(8, 1)
+#undef P1_CASE
+  return hipErrorInvalidValue;
+}
+
+// (NB, RT) pairs instantiated for the down kernels.  RT > 1 (2-4 tiles per
+// wave) measured no faster on the decode shapes, so only RT = 1 is built.
+template <int ACT, int BALLOT>
+static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int grid, size_t lds, hipStream_t st) {
+#define P2_CASE(NB_, RT_)                                                                          \
+  if (nb == NB_ && rt == RT_) {                                                                    \
+    if constexpr (BALLOT)                                                                          \
+      hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3(grid), dim3(64 * a.c.K), lds, \
+                         st, a);                                                                   \
+    else if constexpr (RT_ == 1)                                                                   \
+      hipLaunchKernelGGL((w4a16_phase2_kernel<ACT, NB_>), dim3(grid), dim3(kBlock), lds, st, a);  \
+    return hipGetLastError();                                                                      \
+  }
+  P2_CASE(1, 1) P2_CASE(2, 1) P2_CASE(3, 1) P2_CASE(4, 1) P2_CASE(6, 1) P2_CASE(8, 1) P2_CASE(12, 1)
+#undef P2_CASE
+  return hipErrorInvalidValue;
+}
+
+// largest size in `sizes` that divides `need`
+static int pick_div(const int* sizes, int count, int need) {
   int b = 1;
   for (int i = 0; i < count; ++i)
     if (need % sizes[i] == 0) b = sizes[i];
   return b;
 }
 
-template <int ACT, int BALLOT, int NB>
-static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, BALLOT, NB>), dim3(grid), dim3(kBlock), lds, st, a);
-}
-template <int ACT, int NB>
-static void launch_p2(const W4Args& a, int ballot, int grid, size_t lds, hipStream_t st) {
-  if (ballot)
-    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB>), dim3(grid), dim3(64 * a.c.K), lds, st, a);
-  else
-    hipLaunchKernelGGL((w4a16_phase2_kernel<ACT, NB>), dim3(grid), dim3(kBlock), lds, st, a);
+// Launch geometry: batch sizes divide the per-wave group counts; phase 1 puts
+// S slices in a workgroup and the down kernel RT row tiles in a wave once the
+// grids are large enough to fill the GPU without them.
+W4Plan w4a16_plan(int H, int I, int64_t T, int64_t K, int ballot) {
+  static const int nb1[] = {1, 2, 3, 4, 6, 8}, nb2[] = {1, 2, 3, 4, 6, 8, 12};
+  W4Plan p;
+  const int ng = H / 512, G2 = I / 128, NI1 = I / 16, NT = H / 16;
+  const int64_t n = T * K;
+  p.nb1 = pick_div(nb1, 6, ng);
+  p.s1 = 1;
+  (void)NI1; (void)n;
+  p.nb2 = pick_div(nb2, 7, G2);
+  p.rt2 = 1;
+  (void)NT; (void)T;
+  return p;
 }
 
 template <int ACT, int BALLOT>
-static hipError_t launch_w4_t(const W4Args& a, int grid1, int grid2, hipStream_t st) {
-  const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols) + a.route_lds;
-  const size_t lds2 = BALLOT ? w4_down_token_lds_bytes(a.c.I, a.c.K)
+static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int grid2, hipStream_t st) {
+  const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1) + a.route_lds;
+  const size_t lds2 = BALLOT ? w4_down_token_lds_bytes(a.c.I, a.c.K, p.rt2)
                              : w4_p2_lds_bytes(a.c.I, a.p2_cols) + a.route_lds;
-  switch (pick_batch(kP1Batches, 6, a.c.H / 512)) {
-    case 1: launch_p1<ACT, BALLOT, 1>(a, grid1, lds1, st); break;
-    case 2: launch_p1<ACT, BALLOT, 2>(a, grid1, lds1, st); break;
-    case 3: launch_p1<ACT, BALLOT, 3>(a, grid1, lds1, st); break;
-    case 4: launch_p1<ACT, BALLOT, 4>(a, grid1, lds1, st); break;
-    case 6: launch_p1<ACT, BALLOT, 6>(a, grid1, lds1, st); break;
-    default: launch_p1<ACT, BALLOT, 8>(a, grid1, lds1, st); break;
-  }
-  hipError_t err = hipGetLastError();
+  hipError_t err = dispatch_p1<ACT, BALLOT>(a, p.nb1, p.s1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
-  switch (pick_batch(kP2Batches, 7, a.c.I / 128)) {
-    case 1: launch_p2<ACT, 1>(a, BALLOT, grid2, lds2, st); break;
-    case 2: launch_p2<ACT, 2>(a, BALLOT, grid2, lds2, st); break;
-    case 3: launch_p2<ACT, 3>(a, BALLOT, grid2, lds2, st); break;
-    case 4: launch_p2<ACT, 4>(a, BALLOT, grid2, lds2, st); break;
-    case 6: launch_p2<ACT, 6>(a, BALLOT, grid2, lds2, st); break;
-    case 8: launch_p2<ACT, 8>(a, BALLOT, grid2, lds2, st); break;
-    default: launch_p2<ACT, 12>(a, BALLOT, grid2, lds2, st); break;
-  }
-  return hipGetLastError();
+  return dispatch_p2<ACT, BALLOT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
 }
 
-// ballot = 1 (T*K <= 64, K <= 16): grid1 = T*K * I/16, grid2 = T * H/16 (down
-// kernel, writes y).  ballot = 0: grid1 = U * I/16, grid2 = U * H/64 with
-// U = min(T*K, E) and sorted routing; the caller launches the combine.
-hipError_t launch_w4a16(const W4Args& a, int act, int ballot, int grid1, int grid2, hipStream_t st) {
-  if (act == 1) return ballot ? launch_w4_t<1, 1>(a, grid1, grid2, st) : launch_w4_t<1, 0>(a, grid1, grid2, st);
-  return ballot ? launch_w4_t<0, 1>(a, grid1, grid2, st) : launch_w4_t<0, 0>(a, grid1, grid2, st);
+// ballot = 1 (T*K <= 64, K <= kDownMaxK): grid1 = T*K * I/16, grid2 = T * H/16 (down
+// kernel, writes y); ballot = 0: grid1 = U * I/16, grid2 = U * H/64 with
+// U = min(T*K, E) and sorted routing; the caller launches the combine.  The
+// plan divides the grids by its slice / tile counts.
+hipError_t launch_w4a16(const W4Args& a, const W4Plan& p, int act, int ballot, int grid1, int grid2,
+                        hipStream_t st) {
+  if (act == 1) return ballot ? launch_w4_t<1, 1>(a, p, grid1, grid2, st) : launch_w4_t<1, 0>(a, p, grid1, grid2, st);
+  return ballot ? launch_w4_t<0, 1>(a, p, grid1, grid2, st) : launch_w4_t<0, 0>(a, p, grid1, grid2, st);
 }
 
 }  // namespace mimoe

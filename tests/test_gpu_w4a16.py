@@ -60,6 +60,19 @@ def test_small_parity(cuda, small, T, K):
     assert max_rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("T,K", [(3, 10), (64, 1), (5, 7)])
+def test_decode_boundary_shapes(cuda, T, K):
+    """K > 8 leaves the decode path for the sorted one; K = 1 runs single-wave
+    down workgroups; odd K exercises the per-token wave count."""
+    E, H, I = 16, 512, 256
+    w = w4a16_random(E, H, I, seed=400 + K)
+    h = _handle(E, H, I, w, True, cuda)
+    ids, tw = topk_routing(T, E, K, seed=T + K)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(T + K)).to(torch.bfloat16)
+    y = _run(h, x, ids, tw, cuda)
+    assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, torch.bfloat16)) <= TOL
+
+
 def test_invalid_duplicate_and_empty_ids(cuda, small):
     w, h = small
     E, H, I = SMALL["E"], SMALL["H"], SMALL["I"]
