@@ -61,7 +61,7 @@ def algo_bytes(ids_cpu, bs, fmt):
     return U * fmt.bytes_per_expert(2, H, I, GROUP) + 4 * bs * H + 8 * bs * TOPK, U
 
 
-def cpu_baseline(torch, fmt, wire_cpu, inputs_cpu):
+def cpu_baseline(torch, fmt, wire_cpu, inputs_cpu, batches=BATCHES):
     """Oracle W4A16 forward (scalar C, OpenMP over routed rows) on a bounded
     sample: one call per batch size on the first routing."""
     import numpy as np
@@ -73,7 +73,7 @@ def cpu_baseline(torch, fmt, wire_cpu, inputs_cpu):
                                              t.view(torch.int16).numpy().view(np.uint16)
                                              for t in wire_cpu]
     tot_bytes, tot_s = 0, 0.0
-    for bs in BATCHES:
+    for bs in batches:
         x, ids, w = inputs_cpu[bs]
         xb = x.view(torch.int16).numpy().view(np.uint16)
         t0 = time.perf_counter()
@@ -111,12 +111,58 @@ def cpu_baseline(torch, fmt, wire_cpu, inputs_cpu):
     }
 
 
+def phase1_bytes(ids_cpu, bs):
+    """Algorithmic bytes of the gate_up (+SiLU) launch: the routed experts'
+    w13 (int4 + bf16 scales + 4-bit zeros), x in, ids in, act out."""
+    import torch
+    U = int(torch.unique(ids_cpu[(ids_cpu >= 0) & (ids_cpu < E)]).numel())
+    w13 = 2 * I * H // 2 + 2 * I * (H // GROUP) * 2 + 2 * I * (H // GROUP) // 2
+    return U * w13 + 2 * bs * H + 4 * bs * TOPK + 2 * bs * TOPK * I
+
+
+def read_traffic(path):
+    """HBM traffic of one gate_up launch at bs 8 from a committed rocprofv3
+    PMC summary (lines 'key: value'); None when the file is absent."""
+    if not path or not os.path.exists(path):
+        return None
+    kv = {}
+    for line in open(path):
+        if ":" in line and not line.lstrip().startswith("#"):
+            k, v = line.split(":", 1)
+            kv[k.strip()] = v.strip()
+    try:
+        return {"bytes_per_launch": int(float(kv["hbm_bytes_per_launch"])),
+                "algorithmic_bytes_per_launch": int(float(kv["algorithmic_bytes_per_launch"])),
+                "source": os.path.relpath(path, ROOT)}
+    except (KeyError, ValueError):
+        return None
+
+
+def copy_calibration(mb):
+    """A plain device copy of known size, for scaling the PMC byte counters."""
+    import torch
+    n = mb * (1 << 20)
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n, "launches": 4}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=NSETS)
+    ap.add_argument("--batches", type=str, default=",".join(str(b) for b in BATCHES))
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager calls instead of HIP-graph replays (profiler counter runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="only run a plain copy of MB mebibytes (PMC byte-counter scale) and exit")
+    ap.add_argument("--traffic-file", type=str,
+                    default=os.path.join(ROOT, "profiles", "w4a16_phase1_traffic_qwen3_bs8.txt"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -124,6 +170,10 @@ def main():
               "the single-GPU kernel is the unit of work, see DESIGN.md for sharding.",
               file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
+    batches = tuple(int(b) for b in args.batches.split(","))
 
     import torch
     import nanovllm_moe
@@ -148,18 +198,20 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] {args.sets} weight copies ready in {time.time() - t0:.1f}s")
 
-    inputs = {bs: [make_inputs(torch, bs, i, dev) for i in range(NROUTES)] for bs in BATCHES}
-    nbytes = {bs: [algo_bytes(ids.cpu(), bs, fmt) for (_, ids, _) in inputs[bs]] for bs in BATCHES}
+    inputs = {bs: [make_inputs(torch, bs, i, dev) for i in range(NROUTES)] for bs in batches}
+    nbytes = {bs: [algo_bytes(ids.cpu(), bs, fmt) for (_, ids, _) in inputs[bs]] for bs in batches}
+    p1bytes = {bs: [phase1_bytes(ids.cpu(), bs) for (_, ids, _) in inputs[bs]] for bs in batches}
     op = torch.ops.nanovllm.moe_forward
-    outs = {bs: torch.empty(bs, H, dtype=torch.bfloat16, device=dev) for bs in BATCHES}
+    outs = {bs: torch.empty(bs, H, dtype=torch.bfloat16, device=dev) for bs in batches}
     op_out = torch.ops.nanovllm.moe_forward_out
 
     # Each batch size gets one HIP graph holding `steps` consecutive layer
     # calls (cycling routings and weight copies); a timed step is one layer
-    # call at each of bs 1, 2, 4, 8.  Graph replay removes the per-call Python
-    # and dispatcher cost, so the events bracket GPU work only.
+    # call at each batch size.  Graph replay removes the per-call Python and
+    # dispatcher cost, so the events bracket GPU work only.  --eager times the
+    # same calls issued one by one.
     per, eager, graphs = {}, {}, {}
-    for bs in BATCHES:
+    for bs in batches:
         seq = inputs[bs]
         calls = [(seq[i % NROUTES], handles[i % args.sets]) for i in range(args.steps)]
         for i in range(max(args.warmup, 2)):
@@ -176,20 +228,27 @@ def main():
         ev1.record()
         torch.cuda.synchronize()
         eager[bs] = ev0.elapsed_time(ev1) * 1e3 / n_e
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for (x, ids, w), h in calls:
-                op_out(x, ids, w, h, outs[bs])
-        g.replay()   # untimed: first replay uploads the graph
-        graphs[bs] = g
+        if not args.eager:
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for (x, ids, w), h in calls:
+                    op_out(x, ids, w, h, outs[bs])
+            gr.replay()   # untimed: first replay uploads the graph
+            graphs[bs] = gr
     torch.cuda.synchronize()
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(BATCHES) + 1)]
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(batches) + 1)]
     evs[0].record()
-    for j, bs in enumerate(BATCHES):
-        graphs[bs].replay()
+    for j, bs in enumerate(batches):
+        if args.eager:
+            seq = inputs[bs]
+            for i in range(args.steps):
+                x, ids, w = seq[i % NROUTES]
+                op_out(x, ids, w, handles[i % args.sets], outs[bs])
+        else:
+            graphs[bs].replay()
         evs[j + 1].record()
     torch.cuda.synchronize()
-    for j, bs in enumerate(BATCHES):
+    for j, bs in enumerate(batches):
         ms = evs[j].elapsed_time(evs[j + 1])
         byts = sum(nbytes[bs][i % NROUTES][0] for i in range(args.steps))
         us = ms * 1e3 / args.steps
@@ -203,19 +262,51 @@ def main():
             f"eager {eager[bs]:.1f} us/call")
     del graphs
 
+    # per-launch times of the two kernels (HIP events the library records
+    # around / between its launches on the call's stream), for the roofline of
+    # the dominant kernel (gate_up).  Each timed call is queued behind a few
+    # untimed calls, so it starts on a busy GPU right after the previous layer
+    # call (as in the graph replays) and the host's enqueue latency stays out
+    # of the events.
+    nph, lead = 48, 3
+    p1_t, p1_b = 0.0, 0.0
+    for bs in batches:
+        seq = inputs[bs]
+        t1 = t2 = 0.0
+        for i in range(nph):
+            for j in range(lead):
+                x, ids, w = seq[(i + j + 1) % NROUTES]
+                op_out(x, ids, w, handles[(i + j + 1) % args.sets], outs[bs])
+            x, ids, w = seq[i % NROUTES]
+            h = handles[i % args.sets]
+            h.set_timing(True)
+            op_out(x, ids, w, h, outs[bs])
+            ph = h.get_last_phase_times_ms()
+            h.set_timing(False)
+            t1 += ph[0]
+            t2 += ph[1]
+        b1 = sum(p1bytes[bs][i % NROUTES] for i in range(nph)) / nph
+        per[bs]["gate_up_us"] = round(t1 * 1e3 / nph, 3)
+        per[bs]["down_us"] = round(t2 * 1e3 / nph, 3)
+        per[bs]["gate_up_GB_per_s"] = round(b1 / (t1 / nph * 1e-3) / 1e9, 1)
+        p1_t += t1 / nph
+        p1_b += b1
+
     # whole-sweep figures
-    tot_us = sum(per[bs]["us_per_layer"] for bs in BATCHES)
-    tot_bytes = sum(per[bs]["bytes_per_call_mean"] for bs in BATCHES)
+    tot_us = sum(per[bs]["us_per_layer"] for bs in batches)
+    tot_bytes = sum(per[bs]["bytes_per_call_mean"] for bs in batches)
     value = tot_bytes / (tot_us * 1e-6) / 1e9
+    p1_gbs = p1_b / (p1_t * 1e-3) / 1e9
 
     # correctness spot check of the timed configuration against torch fp32
-    x, ids, w = inputs[8][0]
+    bsc = batches[-1]
+    x, ids, w = inputs[bsc][0]
     y = op(x, ids, w, handles[0])
     torch.cuda.synchronize()
     W13 = fmt.awq_dequant(*wire[:3], GROUP)
     W2 = fmt.awq_dequant(*wire[3:], GROUP)
-    ref = torch.zeros(8, H, dtype=torch.float32, device=dev)
-    for t in range(8):
+    ref = torch.zeros(bsc, H, dtype=torch.float32, device=dev)
+    for t in range(bsc):
         for k in range(TOPK):
             e = int(ids[t, k])
             gu = W13[e] @ x[t].float()
@@ -224,6 +315,7 @@ def main():
     check = float((y.float() - ref).abs().max() / ref.abs().max())
     del W13, W2
 
+    traffic = read_traffic(args.traffic_file)
     result = {
         "metric": "fused-MoE µs/layer + achieved HBM GB/s (% of peak), bs 1–8, 1×MI355X",
         "value": round(value, 1),
@@ -238,18 +330,27 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 hidden, AWQ int4 from N(0,0.02) weights, uniform top-8)",
         "config": {"workload": "W4A16 fused MoE decode layer, Qwen3-30B-A3B shape "
-                               "(H=2048, I=768, E=128, top-8, group 128), bs 1/2/4/8",
-                   "batches": list(BATCHES), "weight_copies": args.sets, "routings": NROUTES},
-        "per_batch": {str(bs): per[bs] for bs in BATCHES},
+                               "(H=2048, I=768, E=128, top-8, group 128)",
+                   "batches": list(batches), "weight_copies": args.sets, "routings": NROUTES,
+                   "timing": "eager calls" if args.eager else "HIP-graph replay"},
+        "per_batch": {str(bs): per[bs] for bs in batches},
         "check_max_rel_err_vs_torch_fp32": round(check, 6),
-        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / PEAK_GBS, 4), "traffic": None,
-                     "kernel": "w4a16_decode_kernel<1,1,4> (one launch per layer call at T*K<=64)"},
+        "roofline": {"bound": "hbm", "achieved": round(p1_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(p1_gbs / PEAK_GBS, 4),
+                     "traffic": traffic["bytes_per_launch"] if traffic else None,
+                     "kernel": "w4a16_phase1_kernel (gate_up + SiLU*mul; the longer of the two launches)",
+                     "achieved_basis": "algorithmic bytes (routed experts' w13 + x + ids + act) / "
+                                       "HIP-event launch time, summed over the batch sweep",
+                     "traffic_basis": (f"rocprofv3 FETCH_SIZE+WRITE_SIZE at bs 8, copy-scaled "
+                                       f"({traffic['source']}; algorithmic "
+                                       f"{traffic['algorithmic_bytes_per_launch']} B)") if traffic else None},
+        "layer_roofline": {"achieved": round(value, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                           "frac": round(value / PEAK_GBS, 4)},
     }
     if not args.no_cpu_baseline:
         wire_cpu = [t.cpu() for t in wire]
-        inputs_cpu = {bs: tuple(t.cpu() for t in inputs[bs][0]) for bs in BATCHES}
-        result["cpu_baseline"] = cpu_baseline(torch, fmt, wire_cpu, inputs_cpu)
+        inputs_cpu = {bs: tuple(t.cpu() for t in inputs[bs][0]) for bs in batches}
+        result["cpu_baseline"] = cpu_baseline(torch, fmt, wire_cpu, inputs_cpu, batches)
     print(json.dumps(result), flush=True)
 
 

@@ -121,6 +121,14 @@ double mi_moe_get_last_run_time_ms(mi_moe_handle* h);
 /* Enable (1) / disable (0) the per-call HIP-event timing (default 1). */
 int mi_moe_set_timing(mi_moe_handle* h, int enable);
 
+/* Per-launch-phase times of the last timed mi_moe_forward, in ms: W4A16
+ * fills ms[0] = routing + gate_up (+SiLU) launch(es), ms[1] = down (+combine)
+ * launch(es) and returns 2; the integer path returns 1 (whole call).
+ * Synchronizes on the end event.  No counterpart in the reference (its timer
+ * covers the whole op); it is the measurement hook behind the per-kernel
+ * roofline figures. */
+int mi_moe_get_last_phase_times_ms(mi_moe_handle* h, double* ms, int max_phases);
+
 /* Stage A activation quantization alone: x [T,H] fp16/bf16 -> x_qs [T,H]
  * int8, x_d [T,H/32] fp32, with the device block quantizer used inside the
  * fused kernels.  Replaces Stage A of moe_forward_ptr_impl

@@ -35,7 +35,7 @@ hipError_t launch_awq_repack_all(const int32_t*, const int32_t*, const uint16_t*
                                  unsigned char*, int, int, int, hipStream_t);
 hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*, hipStream_t);
 W4Plan w4a16_plan(int, int, int64_t, int64_t, int);
-hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, int, hipStream_t);
+hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, hipStream_t);
 hipError_t launch_q_repack(int, const void*, const uint16_t*, void*, uint16_t*, int, int, int, int,
                            int, hipStream_t);
@@ -114,6 +114,8 @@ struct mi_moe_handle {
   bool timing = true;
   bool timed_once = false;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  hipEvent_t evmid = nullptr;   // between the gate_up and down launches (W4A16)
+  bool mid_recorded = false;
   // weights (device layout)
   DevBuf w13, w13_s, w13_z, w2, w2_s, w2_z;
   // workspace
@@ -212,14 +214,17 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
   while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1) + a.route_lds > kMaxLds) --a.p1_cols;
   while (a.p2_cols > 1 && w4_p2_lds_bytes((int)h->I, a.p2_cols) + a.route_lds > kMaxLds) --a.p2_cols;
   const W4Plan plan = w4a16_plan((int)h->H, (int)h->I, T, K, ballot);
+  hipEvent_t mid = h->timing ? h->evmid : nullptr;
   if (ballot) {
-    HIPCHK(launch_w4a16(a, plan, act, 1, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st));
+    HIPCHK(launch_w4a16(a, plan, act, 1, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st, mid));
+    h->mid_recorded = mid != nullptr;
     return MI_MOE_OK;
   }
   if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
   const int64_t umax = n < h->E ? n : h->E;
   const int64_t grid1 = umax * (h->I / 16), grid2 = umax * (h->H / 64);
-  HIPCHK(launch_w4a16(a, plan, act, 0, (int)grid1, (int)grid2, st));
+  HIPCHK(launch_w4a16(a, plan, act, 0, (int)grid1, (int)grid2, st, mid));
+  h->mid_recorded = mid != nullptr;
   HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
   return MI_MOE_OK;
 }
@@ -282,7 +287,8 @@ MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe
   h->E = E; h->H = H; h->I = I; h->quant = quant_type;
   if (hipGetDevice(&h->device) != hipSuccess ||
       hipDeviceGetAttribute(&h->num_cu, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess ||
-      hipEventCreate(&h->ev0) != hipSuccess || hipEventCreate(&h->ev1) != hipSuccess) {
+      hipEventCreate(&h->ev0) != hipSuccess || hipEventCreate(&h->ev1) != hipSuccess ||
+      hipEventCreate(&h->evmid) != hipSuccess) {
     delete h;
     return fail(MI_MOE_EHIP, "HIP device query / event creation failed");
   }
@@ -299,6 +305,7 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
   if (h->ev1) (void)hipEventDestroy(h->ev1);
+  if (h->evmid) (void)hipEventDestroy(h->evmid);
   delete h;
   return MI_MOE_OK;
 }
@@ -457,6 +464,7 @@ MI_API int mi_moe_forward(mi_moe_handle* h, const void* x, void* y, const float*
   if (!aligned16(x) || !aligned16(y)) return fail(MI_MOE_EINVAL, "hidden/out must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   if (h->timing) HIPCHK(hipEventRecord(h->ev0, st));
+  h->mid_recorded = false;
   if (h->quant == MI_MOE_W4A16) rc = forward_w4a16(h, x, y, topk_w, topk_ids, T, K, act_dtype, st);
   else rc = forward_q(h, x, y, topk_w, topk_ids, T, K, act_dtype, st);
   if (rc) return rc;
@@ -465,6 +473,23 @@ MI_API int mi_moe_forward(mi_moe_handle* h, const void* x, void* y, const float*
     h->timed_once = true;
   }
   return MI_MOE_OK;
+}
+
+MI_API int mi_moe_get_last_phase_times_ms(mi_moe_handle* h, double* ms, int max_phases) {
+  if (!h || !ms || max_phases < 1) return fail(MI_MOE_EINVAL, "null handle / buffer");
+  if (!h->timing || !h->timed_once) return fail(MI_MOE_EINVAL, "timing off or no timed call");
+  HIPCHK(hipEventSynchronize(h->ev1));
+  float t = 0.0f;
+  if (!h->mid_recorded || max_phases < 2) {
+    HIPCHK(hipEventElapsedTime(&t, h->ev0, h->ev1));
+    ms[0] = t;
+    return 1;
+  }
+  HIPCHK(hipEventElapsedTime(&t, h->ev0, h->evmid));
+  ms[0] = t;
+  HIPCHK(hipEventElapsedTime(&t, h->evmid, h->ev1));
+  ms[1] = t;
+  return 2;
 }
 
 MI_API int mi_moe_quantize_act_q8_0(const void* x, int act_dtype, int64_t T, int64_t H,

@@ -7,6 +7,7 @@
 // include/mi_moe.h on the current HIP stream.
 #include <c10/hip/HIPStream.h>
 #include <torch/custom_class.h>
+#include <vector>
 #include <torch/library.h>
 #include <ATen/ATen.h>
 
@@ -208,6 +209,13 @@ TORCH_LIBRARY_FRAGMENT(nanovllm, m) {
       .def("get_last_run_time_ms",
            [](const c10::intrusive_ptr<MoEInferHandle>& self) {
              return mi_moe_get_last_run_time_ms(self->h);
+           })
+      .def("get_last_phase_times_ms",
+           [](const c10::intrusive_ptr<MoEInferHandle>& self) {
+             double ms[2] = {0.0, 0.0};
+             const int n = mi_moe_get_last_phase_times_ms(self->h, ms, 2);
+             TORCH_CHECK(n > 0, "get_last_phase_times_ms: ", mi_moe_last_error());
+             return std::vector<double>(ms, ms + n);
            })
       .def("set_timing",
            [](const c10::intrusive_ptr<MoEInferHandle>& self, bool enable) {

@@ -683,23 +683,27 @@ W4Plan w4a16_plan(int H, int I, int64_t T, int64_t K, int ballot) {
 }
 
 template <int ACT, int BALLOT>
-static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int grid2, hipStream_t st) {
+static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int grid2, hipStream_t st,
+                              hipEvent_t mid) {
   const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1) + a.route_lds;
   const size_t lds2 = BALLOT ? w4_down_token_lds_bytes(a.c.I, a.c.K, p.rt2)
                              : w4_p2_lds_bytes(a.c.I, a.p2_cols) + a.route_lds;
   hipError_t err = dispatch_p1<ACT, BALLOT>(a, p.nb1, p.s1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
+  if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
   return dispatch_p2<ACT, BALLOT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
 }
 
 // ballot = 1 (T*K <= 64, K <= kDownMaxK): grid1 = T*K * I/16, grid2 = T * H/16 (down
 // kernel, writes y); ballot = 0: grid1 = U * I/16, grid2 = U * H/64 with
 // U = min(T*K, E) and sorted routing; the caller launches the combine.  The
-// plan divides the grids by its slice / tile counts.
+// plan divides the grids by its slice / tile counts.  mid (optional) is
+// recorded between the gate_up and down launches.
 hipError_t launch_w4a16(const W4Args& a, const W4Plan& p, int act, int ballot, int grid1, int grid2,
-                        hipStream_t st) {
-  if (act == 1) return ballot ? launch_w4_t<1, 1>(a, p, grid1, grid2, st) : launch_w4_t<1, 0>(a, p, grid1, grid2, st);
-  return ballot ? launch_w4_t<0, 1>(a, p, grid1, grid2, st) : launch_w4_t<0, 0>(a, p, grid1, grid2, st);
+                        hipStream_t st, hipEvent_t mid) {
+  if (act == 1)
+    return ballot ? launch_w4_t<1, 1>(a, p, grid1, grid2, st, mid) : launch_w4_t<1, 0>(a, p, grid1, grid2, st, mid);
+  return ballot ? launch_w4_t<0, 1>(a, p, grid1, grid2, st, mid) : launch_w4_t<0, 0>(a, p, grid1, grid2, st, mid);
 }
 
 }  // namespace mimoe

@@ -35,6 +35,7 @@ C_SYMBOLS = (
     "mi_moe_get_info", "mi_moe_store_quantized", "mi_moe_quantize_and_store_expert",
     "mi_moe_store_awq", "mi_moe_forward", "mi_moe_get_last_run_time_ms",
     "mi_moe_set_timing", "mi_moe_quantize_act_q8_0", "mi_moe_route", "mi_moe_block_dots",
+    "mi_moe_get_last_phase_times_ms",
 )
 
 
@@ -80,6 +81,7 @@ def capi():
     L.mi_moe_get_last_run_time_ms.restype = ctypes.c_double
     L.mi_moe_get_last_run_time_ms.argtypes = [P]
     L.mi_moe_set_timing.argtypes = [P, I]
+    L.mi_moe_get_last_phase_times_ms.argtypes = [P, ctypes.POINTER(ctypes.c_double), I]
     L.mi_moe_quantize_act_q8_0.argtypes = [P, I, I64, I64, P, P, P]
     L.mi_moe_route.argtypes = [P, I64, I64, I64, P, P, P, P, P]
     L.mi_moe_block_dots.argtypes = [P, I64, I, P, I64, P, P]
