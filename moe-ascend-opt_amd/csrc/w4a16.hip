@@ -215,6 +215,10 @@ __device__ __forceinline__ bool get_cols(const SchedArgs& c, int item, int lane,
 }
 
 // ================================================================ phase 1
+// Register budgets, as waves per SIMD: phase 1 spills above 4; the down
+// kernel (8-wave workgroups) fits 6 without spills, i.e. 3 workgroups per CU.
+constexpr int kP1WavesPerEU = 4;
+constexpr int kDownWavesPerEU = 6;
 // Workgroup (item, slices j = S*js .. S*js+S-1 of 16 rows): gate/up rows of
 // the item's expert over all H (the 4 waves split the H groups), every routed
 // pair of the expert in passes of p1_cols columns; SiLU*mul into act[pair].
@@ -227,7 +231,8 @@ __device__ __forceinline__ bool get_cols(const SchedArgs& c, int item, int lane,
 // rows of each pass's columns are copied once the routing is known.
 // LDS (w4_p1_lds_bytes): red [S][wave][gate,up][64][4] f32 | metadata S x 80*G1 B | x rows | routing.
 template <int ACT, int BALLOT, int NB, int S>
-__global__ __launch_bounds__(kBlock) void w4a16_phase1_kernel(W4Args a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kP1WavesPerEU)))
+void w4a16_phase1_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
@@ -452,7 +457,8 @@ __global__ __launch_bounds__(kBlock) void w4a16_phase2_kernel(W4Args a) {
 // no cross-workgroup communication.
 // LDS: act rows [K][I] | metadata [K][RT][SEC] | outputs [K][16 RT] f32 | valid [K].
 template <int ACT, int NB, int RT>
-__global__ __launch_bounds__(kDownMaxK * 64) void w4a16_down_token_kernel(W4Args a) {
+__global__ __launch_bounds__(kDownMaxK * 64) __attribute__((amdgpu_waves_per_eu(kDownWavesPerEU)))
+void w4a16_down_token_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = c.H, I = c.I, K = c.K, MQ = H >> 6, G2 = I >> 7, NTG = (H >> 4) / RT, II = I >> 3;
