@@ -83,6 +83,14 @@ __device__ __forceinline__ float silu_mul(float g, float up) {
   return up * sig;
 }
 
+// The same with the hardware exponential and reciprocal (v_exp_f32,
+// v_rcp_f32: about 1 ulp each), for the W4A16 path whose output is rounded to
+// 16 bits; the Q8_0 path keeps silu_mul, which its CPU checker reproduces.
+__device__ __forceinline__ float silu_mul_fast(float g, float up) {
+  const float eg = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+  return up * (g * __builtin_amdgcn_rcpf(1.0f + eg));
+}
+
 // ------------------------------------------------------------ Q8_0 block
 // amax over 32 values, d = amax/127, id = 1/d, q = sat8(RNE(x*id)).
 __device__ __forceinline__ int8_t q8_round(float v) {

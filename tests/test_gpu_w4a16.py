@@ -159,6 +159,34 @@ def test_dtypes(cuda, adt, sdt):
     assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, adt)) <= TOL
 
 
+@pytest.mark.parametrize("H,T,K", [(1024, 4, 8), (1536, 8, 6), (3072, 5, 8), (2048, 8, 8), (512, 3, 4)])
+def test_decode_widths(cuda, H, T, K):
+    """Decode path at every H/512 group count the kernels are built for."""
+    E, I = 16, 256
+    w = w4a16_random(E, H, I, seed=H + T)
+    h = _handle(E, H, I, w, True, cuda)
+    ids, tw = topk_routing(T, E, K, seed=H + K)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
+    y = _run(h, x, ids, tw, cuda)
+    assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, torch.bfloat16)) <= TOL
+
+
+def test_decode_expert_over_16_columns(cuda, small):
+    """Repeated ids give one expert 52 of the 64 pairs: the decode gate_up
+    takes several column passes for it."""
+    w, h = small
+    E, H, I = SMALL["E"], SMALL["H"], SMALL["I"]
+    T, K = 32, 2
+    ids, tw = topk_routing(T, E, K, seed=31)
+    ids = ids.clone()
+    ids[:20, :] = 3
+    ids[20:, 0] = 3
+    ids[20:, 1] = torch.where(ids[20:, 1] == 3, torch.full_like(ids[20:, 1], 4), ids[20:, 1])
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(31)).to(torch.bfloat16)
+    y = _run(h, x, ids, tw, cuda)
+    assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, torch.bfloat16)) <= TOL
+
+
 def test_many_rows_per_expert_and_global_routing(cuda, small):
     """T*K > 1024 takes the separate routing kernel; experts get > 64 rows."""
     w, h = small
