@@ -150,6 +150,108 @@ def copy_calibration(mb):
     print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n, "launches": 4}))
 
 
+def time_graph(torch, op_out, calls, out, warmup):
+    """Mean µs per call of `calls` (tuples x, ids, w, handle) replayed from one
+    HIP graph, after `warmup` eager calls."""
+    for i in range(max(warmup, 2)):
+        x, ids, w, h = calls[i % len(calls)]
+        op_out(x, ids, w, h, out)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for x, ids, w, h in calls:
+            op_out(x, ids, w, h, out)
+    gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / len(calls)
+
+
+def run_config(cfg, steps, warmup):
+    """The other BASELINE configurations, as one JSON line each (not the
+    headline line): 3 = Q4_0 prefill, Qwen3 shape, T 32..4096; 4 = MiniMax-M2
+    W4A16, bs 1/8/64; 5 = Zipf-skewed routing (p ~ r^-1.2), T = 512, Qwen3
+    W4A16.  Weights are random in the format (timing does not depend on the
+    values); enough copies rotate that the 256 MB Infinity Cache cannot hold
+    what a call reads."""
+    import torch
+    import nanovllm_moe
+    from nanovllm_moe import formats as fmt
+    from nanovllm_moe.synthetic import zipf_routing
+    nanovllm_moe.load()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rint32(*shape):
+        v = torch.randint(0, 2**32, shape, generator=g, dtype=torch.int64, device=dev)
+        return torch.where(v >= 2**31, v - 2**32, v).to(torch.int32)
+
+    if cfg == 3:
+        E_, H_, I_, K_, quant, Ts, copies = 128, 2048, 768, 8, 1, (32, 128, 1024, 4096), 2
+    elif cfg == 4:
+        E_, H_, I_, K_, quant, Ts, copies = 256, 3072, 1536, 8, 2, (1, 8, 64), 4
+    else:
+        E_, H_, I_, K_, quant, Ts, copies = 128, 2048, 768, 8, 2, (512,), 4
+    handles = []
+    for _ in range(copies):
+        h = torch.classes.nanovllm.MoEInfer(E_, H_, I_, quant)
+        if quant == 1:
+            q13, d13 = fmt.q4_0_random((E_, 2 * I_), H_, generator=g, device=dev)
+            q2, d2 = fmt.q4_0_random((E_, H_), I_, generator=g, device=dev)
+            h.store_quantized_repack(q13, d13, q2, d2)
+            del q13, q2
+        else:
+            s13 = (torch.rand(E_, H_ // GROUP, 2 * I_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
+            s2 = (torch.rand(E_, I_ // GROUP, H_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
+            h.store_awq_repack(rint32(E_, H_, 2 * I_ // 8), rint32(E_, H_ // GROUP, 2 * I_ // 8), s13,
+                               rint32(E_, I_, H_ // 8), rint32(E_, I_ // GROUP, H_ // 8), s2, GROUP)
+        h.set_timing(False)
+        handles.append(h)
+    torch.cuda.synchronize()
+    bpe = fmt.bytes_per_expert(quant, H_, I_, GROUP)
+    op_out = torch.ops.nanovllm.moe_forward_out
+    per = {}
+    nroutes = 8
+    for T in Ts:
+        calls, nbytes, us_list = [], [], []
+        for i in range(nroutes):
+            gg = torch.Generator().manual_seed(7000 + 10 * T + i)
+            x = torch.randn(T, H_, generator=gg).to(torch.bfloat16).to(dev)
+            if cfg == 5:
+                ids, w = zipf_routing(T, E_, K_, seed=i)
+            else:
+                val, ids = torch.topk(torch.randn(T, E_, generator=gg), K_, dim=-1)
+                w = torch.softmax(val, dim=-1)
+            ids_c = ids.to(torch.int32)
+            U = int(torch.unique(ids_c).numel())
+            nbytes.append(U * bpe + 4 * T * H_ + 8 * T * K_)
+            calls.append((x, ids_c.to(dev), w.to(torch.float32).to(dev), handles[i % copies]))
+        seq = [calls[i % nroutes] for i in range(max(steps // 4, nroutes))]
+        out = torch.empty(T, H_, dtype=torch.bfloat16, device=dev)
+        us = time_graph(torch, op_out, seq, out, warmup)
+        byts = sum(nbytes[i % nroutes] for i in range(len(seq))) / len(seq)
+        flops = 6 * T * K_ * H_ * I_
+        per[str(T)] = {"us_per_layer": round(us, 2), "GB_per_s": round(byts / (us * 1e-6) / 1e9, 1),
+                       "frac_of_hbm_peak": round(byts / (us * 1e-6) / 1e9 / PEAK_GBS, 4),
+                       "TFLOP_per_s": round(flops / (us * 1e-6) / 1e12, 2), "bytes_per_call_mean": int(byts),
+                       "calls": len(seq)}
+        if cfg == 5:
+            c = torch.bincount(calls[0][1].reshape(-1).long().cpu(), minlength=E_)
+            per[str(T)]["routing_histogram"] = {"max_rows": int(c.max()), "min_rows": int(c.min()),
+                                                "experts_at_zero": int((c == 0).sum())}
+        log(f"[bench config {cfg}] T={T}: {us:.2f} us/layer, {per[str(T)]['GB_per_s']} GB/s")
+    names = {3: "Q4_0 prefill, Qwen3-30B-A3B shape (H=2048, I=768, E=128, top-8), Q8_0 activations",
+             4: "W4A16, MiniMax-M2 shape (H=3072, I=1536, E=256, top-8, group 128)",
+             5: "W4A16, Qwen3-30B-A3B shape, Zipf-skewed routing (p ~ r^-1.2, distinct top-8)"}
+    print(json.dumps({"config_id": cfg, "workload": names[cfg], "unit": "us/layer and GB/s",
+                      "timing": "HIP-graph replay", "weight_copies": copies, "routings": nroutes,
+                      "per_T": per}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,6 +266,9 @@ def main():
     ap.add_argument("--traffic-file", type=str,
                     default=os.path.join(ROOT, "profiles", "w4a16_decode_traffic_qwen3_bs8.txt"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
+                    help="BASELINE configuration: 2 (default) is the headline line; 3/4/5 print a "
+                         "measurement line for Q4_0 prefill / MiniMax / Zipf routing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -172,6 +277,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.config != 2:
+        run_config(args.config, args.steps, args.warmup)
         return
     batches = tuple(int(b) for b in args.batches.split(","))
 

@@ -53,3 +53,18 @@ def max_rel_err(y, ref):
     y = y.to(torch.float64)
     ref = ref.to(torch.float64)
     return float((y - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+def zipf_routing(T, E, K, seed, alpha=1.2):
+    """BASELINE config 5 routing (nanovllm_moe.synthetic.zipf_routing)."""
+    from nanovllm_moe.synthetic import zipf_routing as z
+    return z(T, E, K, seed, alpha)
+
+
+def token_sample(T, n, seed, must=()):
+    """Sorted sample of n token indices (all when T <= n), plus `must`."""
+    if T <= n:
+        return list(range(T))
+    rng = np.random.default_rng(seed)
+    s = set(int(v) for v in rng.choice(T, size=n, replace=False)) | set(int(v) for v in must)
+    return sorted(s)
