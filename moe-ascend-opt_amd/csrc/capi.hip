@@ -36,6 +36,7 @@ hipError_t launch_awq_repack_all(const int32_t*, const int32_t*, const uint16_t*
 hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*, hipStream_t);
 W4Plan w4a16_plan(int, int, int64_t, int64_t, int);
 hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, int, hipStream_t, hipEvent_t);
+hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, hipStream_t);
 hipError_t launch_q_repack(int, const void*, const uint16_t*, void*, uint16_t*, int, int, int, int,
                            int, hipStream_t);
@@ -120,7 +121,7 @@ struct mi_moe_handle {
   DevBuf w13, w13_s, w13_z, w2, w2_s, w2_z;
   // workspace
   int64_t cap_T = 0, cap_n = 0;
-  DevBuf act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U;
+  DevBuf act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U, r_tiles, r_ntiles;
 };
 
 namespace {
@@ -143,6 +144,7 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
     HIPCHK(h->r_starts.alloc((size_t)(h->E + 1) * sizeof(int32_t)));
     HIPCHK(h->r_active.alloc((size_t)h->E * sizeof(int32_t)));
     HIPCHK(h->r_U.alloc(sizeof(int32_t)));
+    HIPCHK(h->r_ntiles.alloc(sizeof(int32_t)));
   }
   if (T <= h->cap_T && n <= h->cap_n) return MI_MOE_OK;
   int64_t capT = h->cap_T ? h->cap_T : 16;
@@ -156,6 +158,7 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
   HIPCHK(h->eout.alloc((size_t)capn * h->H * sizeof(float)));
   HIPCHK(h->r_tok.alloc((size_t)capn * sizeof(int32_t)));
   HIPCHK(h->r_scat.alloc((size_t)capn * sizeof(int32_t)));
+  HIPCHK(h->r_tiles.alloc((size_t)gemm_tiles_max(capn, (int)h->E) * 4 * sizeof(int32_t)));
   h->cap_T = capT;
   h->cap_n = capn;
   return MI_MOE_OK;
@@ -184,6 +187,8 @@ RouteGlobal route_view(mi_moe_handle* h) {
   rg.tok = (int32_t*)h->r_tok.p;
   rg.scat = (int32_t*)h->r_scat.p;
   rg.U = (int32_t*)h->r_U.p;
+  rg.tiles = (int32_t*)h->r_tiles.p;
+  rg.ntiles = (int32_t*)h->r_ntiles.p;
   return rg;
 }
 
@@ -220,10 +225,9 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
     h->mid_recorded = mid != nullptr;
     return MI_MOE_OK;
   }
-  if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
-  const int64_t umax = n < h->E ? n : h->E;
-  const int64_t grid1 = umax * (h->I / 16), grid2 = umax * (h->H / 64);
-  HIPCHK(launch_w4a16(a, plan, act, 0, (int)grid1, (int)grid2, st, mid));
+  // sorted path: routing with row tiles, the two grouped GEMMs, the combine
+  HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
+  HIPCHK(launch_w4a16_gemm(a, act, (int)gemm_tiles_max(n, (int)h->E), st, mid));
   h->mid_recorded = mid != nullptr;
   HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
   return MI_MOE_OK;
@@ -301,7 +305,7 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
   (void)hipDeviceSynchronize();
   DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z,
                     &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
-                    &h->r_active, &h->r_tok, &h->r_scat, &h->r_U};
+                    &h->r_active, &h->r_tok, &h->r_scat, &h->r_U, &h->r_tiles, &h->r_ntiles};
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
   if (h->ev1) (void)hipEventDestroy(h->ev1);

@@ -13,11 +13,13 @@ constexpr int kRouteWaves = kRouteThreads / kWave;
 // preprocess_moe_routing (Int8-gemm/moe_common.cpp:146-216) for any number of
 // (t,k) pairs.  Each wave owns a contiguous segment of ids; per-wave
 // per-expert counts are prefix-summed across waves so the ranks stay in
-// (t,k) order.  LDS: (kRouteWaves + 1) * E ints (E <= 512).
+// (t,k) order.  With tiles_out, also the row tiles of the grouped GEMMs: per
+// active expert in ascending order, its sorted rows in chunks of kGemmRows.
+// LDS: (kRouteWaves + 1) * E ints (E <= 512).
 __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
     const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
     int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out,
-    int tok_div) {
+    int tok_div, int32_t* tiles_out, int32_t* ntiles_out) {
   extern __shared__ int lds[];
   int* counts = lds;            // [E]
   int* cw = lds + E;            // [kRouteWaves][E]
@@ -39,14 +41,20 @@ __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
       const int e = base + i;
       if (e < E) { const int c = counts[e]; s += c; a += (c > 0); }
     }
-    int sinc = s, ainc = a;
+    int tl = 0;   // row tiles of this lane's experts
+    for (int i = 0; i < per; ++i) {
+      const int e = base + i;
+      if (e < E) tl += (counts[e] + kGemmRows - 1) / kGemmRows;
+    }
+    int sinc = s, ainc = a, tinc = tl;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
       const int v = __shfl_up(sinc, off);
       const int w = __shfl_up(ainc, off);
-      if (lane >= off) { sinc += v; ainc += w; }
+      const int u = __shfl_up(tinc, off);
+      if (lane >= off) { sinc += v; ainc += w; tinc += u; }
     }
-    int sx = sinc - s, ax = ainc - a;
+    int sx = sinc - s, ax = ainc - a, tx = tinc - tl;
     for (int i = 0; i < per; ++i) {
       const int e = base + i;
       if (e < E) {
@@ -55,10 +63,20 @@ __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
         starts_out[e] = sx;
         counts[e] = sx;  // counts[] now holds starts
         if (c > 0) active_out[ax++] = e;
+        if (tiles_out)
+          for (int r0 = 0; r0 < c; r0 += kGemmRows, ++tx) {
+            tiles_out[4 * tx + 0] = e;
+            tiles_out[4 * tx + 1] = sx + r0;
+            tiles_out[4 * tx + 2] = min(kGemmRows, c - r0);
+            tiles_out[4 * tx + 3] = 0;
+          }
         sx += c;
       }
     }
-    if (lane == kWave - 1) { starts_out[E] = sinc; *U_out = ainc; s_U = ainc; }
+    if (lane == kWave - 1) {
+      starts_out[E] = sinc; *U_out = ainc; s_U = ainc;
+      if (ntiles_out) *ntiles_out = tinc;
+    }
   }
   __syncthreads();
   int nbits = 0;
@@ -121,7 +139,8 @@ hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const Ro
                                hipStream_t st, int tok_div) {
   const size_t lds = (size_t)(kRouteWaves + 1) * E * sizeof(int);
   hipLaunchKernelGGL(route_global_kernel, dim3(1), dim3(kRouteThreads), lds, st, ids, n, K, E,
-                     rg.counts, rg.starts, rg.active, rg.tok, rg.scat, rg.U, tok_div);
+                     rg.counts, rg.starts, rg.active, rg.tok, rg.scat, rg.U, tok_div, rg.tiles,
+                     rg.ntiles);
   return hipGetLastError();
 }
 

@@ -20,7 +20,15 @@ struct RouteGlobal {
   int32_t* tok;      // [n]
   int32_t* scat;     // [n]
   int32_t* U;        // [1]
+  int32_t* tiles;    // [n/kGemmRows + E][4]: expert, first sorted row, rows (<= kGemmRows), 0; or null
+  int32_t* ntiles;   // [1]
 };
+
+// Row tile of the grouped GEMMs of the sorted path: routed rows of one expert.
+constexpr int kGemmRows = 64;
+__host__ __device__ inline int64_t gemm_tiles_max(int64_t n, int E) {
+  return n / kGemmRows + (n < E ? n : E);
+}
 
 // Arguments every fused kernel shares (routing, schedule, combine).
 struct SchedArgs {

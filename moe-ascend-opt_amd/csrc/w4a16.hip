@@ -506,6 +506,249 @@ void w4a16_down_token_kernel(W4Args a) {
   }
 }
 
+// ================================================================ grouped GEMMs (sorted path)
+// Work item: a row tile (up to kGemmRows = 64 routed rows of one expert, from
+// the routing kernel's tile list) x a 64-row block of the output, one wave per
+// 16-row tile of the block and all of K per wave, so no cross-wave reduction.
+// Per 128-k group the workgroup stages the tile's activation rows (bf16, row
+// stride kGemmRowStride) and their sums into LDS, double-buffered with one
+// barrier per group; each wave holds its 16 weight rows of the group (16 B per
+// lane) and the lane's scale and zero in registers, and the next group's
+// loads are issued before the current group is computed.  The MFMA A operand
+// is 16 rows of the tile (sub-tiles of 16 rows; only the sub-tiles holding
+// rows are computed), B the dequantized weights:
+//   acc += s * (sum_k x (magic + q) - (offset + z) * sum_k x)   per group,
+// the same arithmetic as the decode kernels, with the row sums from v_dot2
+// instead of a ones-MFMA.  Every weight byte is read and dequantized once per
+// row tile, so an expert with many rows streams its weights a few times and
+// the MFMAs work on full 16-row operands.
+constexpr int kGemmRowStride = 272;   // 256 B of a row + 16 B that spread the rows over the LDS banks
+constexpr int kGemmABytes = kGemmRows * kGemmRowStride;
+// LDS: staged rows [2][kGemmABytes] | row sums [2][kGemmRows] f32 | pair of each row [kGemmRows]
+constexpr size_t kGemmLds = 2 * (size_t)kGemmABytes + 3 * kGemmRows * sizeof(float);
+
+// The staging thread's 32 values of its row (4 x 16 B) and their sum over the
+// row's 128 values (v_dot2 with (1, 1), then the row's 4 threads, which are
+// adjacent lanes).
+template <int ACT>
+__device__ __forceinline__ float gemm_row_sum(const u32x4_t (&v)[4]) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (ACT == 1)
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[k]),
+                                              __builtin_bit_cast(bf16x2_t, 0x3f803f80u), acc, false);
+      else
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w[k]),
+                                     __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
+    }
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  return acc;
+}
+
+__device__ __forceinline__ void gemm_stage_store(unsigned char* buf, float* sums, int srow, int spart,
+                                                 const u32x4_t (&v)[4], float sum) {
+  unsigned char* d = buf + srow * kGemmRowStride + spart * 64;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(d + 16 * i) = v[i];
+  if (spart == 0) sums[srow] = sum;
+}
+
+// acc[p][s] += scale[p] * (W_p x - cz[p] * sum x) for the sub-tiles holding
+// rows, for NP weight sets (gate and up, or one down tile) of the group: the
+// A operand of a sub-tile is read from LDS once for all of them.  MFMA i takes
+// from lane 16q + r the values at k = 32q + 8i + (0..7) of the group (QMAJOR:
+// the w13 word order) or at k = 32i + 8q + (0..7) (the w2 word order).
+template <int ACT, int NP, bool QMAJOR>
+__device__ __forceinline__ void gemm_group(const unsigned char* buf, const float* sums, int nsub, int q,
+                                           int r, const u32x4_t (&B)[NP][4], const float (&scale)[NP],
+                                           const float (&cz)[NP], f32x4_t (&acc)[NP][4]) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s < nsub) {   // uniform
+      u32x4_t A[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        A[i] = lds16(buf + (16 * s + r) * kGemmRowStride + (QMAJOR ? 64 * q + 16 * i : 64 * i + 16 * q));
+      const f32x4_t X = *reinterpret_cast<const f32x4_t*>(sums + 16 * s + 4 * q);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        f32x4_t G = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) G = mfma16<ACT>(A[i], B[p][i], G);
+        fold(acc[p][s], G, X, scale[p], cz[p]);
+      }
+    }
+  }
+}
+
+// gate_up + SiLU*mul: work item (row tile, block of 4 slices = 64 gate and 64
+// up rows); wave w owns slice 4*sb + w.  act[pair] gets the slice's 16 values.
+template <int ACT>
+__global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
+  const SchedArgs& c = a.c;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = c.H, NI1 = c.I >> 4, G1 = H >> 7, NSB = NI1 >> 2;
+  const int ti = blockIdx.x / NSB, sb = blockIdx.x - ti * NSB;
+  if (ti >= *c.rg.ntiles) return;   // uniform
+  const int4 tl = reinterpret_cast<const int4*>(c.rg.tiles)[ti];
+  const int e = tl.x, row0 = tl.y, rows = tl.z, nsub = (rows + 15) >> 4;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  const int j = 4 * sb + wave;
+  const int srow = tid >> 2, spart = tid & 3;
+  const int spair = c.rg.tok[row0 + min(srow, rows - 1)];
+  const uint16_t* xsrc = c.x + (size_t)(spair / c.K) * H + 32 * spart;
+  const size_t blk = (size_t)e * NI1 + j;
+  const char* wg = (const char*)a.w13 + blk * 2 * G1 * 1024 + lane * 16;
+  const unsigned char* mb = a.w13_m + blk * 80 * G1;
+  const uint32_t* msc = reinterpret_cast<const uint32_t*>(mb) + r * G1;
+  const unsigned char* mz = mb + 64 * G1 + r * G1;
+  float* sums0 = reinterpret_cast<float*>(smem + 2 * kGemmABytes);
+  int* pairs = reinterpret_cast<int*>(sums0 + 2 * kGemmRows);   // the tile's pair indices
+  constexpr float off = W4Consts<ACT>::offset;
+
+  u32x4_t sv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sv[i] = ldg16(xsrc + 8 * i);
+  u32x4_t wgc = ldg16(wg), wuc = ldg16(wg + (size_t)G1 * 1024);
+  uint32_t scc = msc[0], zzc = mz[0];
+  if (spart == 0) pairs[srow] = spair;
+  gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
+  __syncthreads();
+  f32x4_t acc[2][4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc[0][s] = acc[1][s] = f32x4_t{0, 0, 0, 0};
+  for (int g = 0; g < G1; ++g) {
+    const int b = g & 1;
+    const bool more = g + 1 < G1;   // uniform
+    const int gn = more ? g + 1 : g;
+    // next group: issued before this one is computed
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = ldg16(xsrc + 128 * gn + 8 * i);
+    const u32x4_t wgn = ldg16(wg + (size_t)gn * 1024), wun = ldg16(wg + (size_t)(G1 + gn) * 1024);
+    const uint32_t scn = msc[gn], zzn = mz[gn];
+    {
+      const uint32_t wg4[4] = {wgc.x, wgc.y, wgc.z, wgc.w}, wu4[4] = {wuc.x, wuc.y, wuc.z, wuc.w};
+      u32x4_t B[2][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        B[0][i] = deq4<ACT>(wg4[i]);
+        B[1][i] = deq4<ACT>(wu4[i]);
+      }
+      const float sc2[2] = {scale_f32(scc & 0xffffu, a.sdt), scale_f32(scc >> 16, a.sdt)};
+      const float cz2[2] = {off + (float)(zzc & 0xfu), off + (float)((zzc >> 4) & 0xfu)};
+      gemm_group<ACT, 2, true>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, sc2, cz2, acc);
+    }
+    if (more) gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
+                               gemm_row_sum<ACT>(sv));
+    wgc = wgn; wuc = wun; scc = scn; zzc = zzn;
+    __syncthreads();
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s < nsub) {
+      const float gv[4] = {acc[0][s].x, acc[0][s].y, acc[0][s].z, acc[0][s].w};
+      const float uv[4] = {acc[1][s].x, acc[1][s].y, acc[1][s].z, acc[1][s].w};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * s + 4 * q + v;
+        if (row < rows)
+          a.act[(size_t)pairs[row] * c.I + 16 * j + r] = from_f32<ACT>(silu_mul_fast(gv[v], uv[v]));
+      }
+    }
+  }
+}
+
+// down: work item (row tile, quad m = rows 64m..64m+63 of H); wave w owns the
+// 16-row tile 64m + 16w.  eout[pair] gets the tile's 16 fp32 values; the
+// combine kernel sums over k.
+template <int ACT>
+__global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
+  const SchedArgs& c = a.c;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = c.H, I = c.I, G2 = I >> 7, MQ = H >> 6;
+  const int SEC = w2_meta_sec_bytes(G2);
+  const int ti = blockIdx.x / MQ, m = blockIdx.x - ti * MQ;
+  if (ti >= *c.rg.ntiles) return;   // uniform
+  const int4 tl = reinterpret_cast<const int4*>(c.rg.tiles)[ti];
+  const int e = tl.x, row0 = tl.y, rows = tl.z, nsub = (rows + 15) >> 4;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  const int srow = tid >> 2, spart = tid & 3;
+  const int spair = c.rg.tok[row0 + min(srow, rows - 1)];
+  const uint16_t* asrc = a.act + (size_t)spair * I + 32 * spart;
+  const size_t tile = ((size_t)e * MQ + m) * 4 + wave;
+  const char* wb = (const char*)a.w2 + tile * G2 * 1024 + lane * 16;
+  const unsigned char* sec = a.w2_m + tile * SEC;
+  float* sums0 = reinterpret_cast<float*>(smem + 2 * kGemmABytes);
+  int* pairs = reinterpret_cast<int*>(sums0 + 2 * kGemmRows);
+  constexpr float off = W4Consts<ACT>::offset;
+
+  u32x4_t sv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sv[i] = ldg16(asrc + 8 * i);
+  u32x4_t wc = ldg16(wb);
+  float sc = w2_scale(sec, 0, r, a.sdt), zc = w2_zero(sec, G2, 0, r);
+  if (spart == 0) pairs[srow] = spair;
+  gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
+  __syncthreads();
+  f32x4_t acc[1][4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc[0][s] = f32x4_t{0, 0, 0, 0};
+  for (int g2 = 0; g2 < G2; ++g2) {
+    const int b = g2 & 1;
+    const bool more = g2 + 1 < G2;   // uniform
+    const int gn = more ? g2 + 1 : g2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = ldg16(asrc + 128 * gn + 8 * i);
+    const u32x4_t wn = ldg16(wb + (size_t)gn * 1024);
+    const float sn = w2_scale(sec, gn, r, a.sdt), zn = w2_zero(sec, G2, gn, r);
+    {
+      const uint32_t w4[4] = {wc.x, wc.y, wc.z, wc.w};
+      u32x4_t B[1][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) B[0][i] = deq4<ACT>(w4[i]);
+      const float sc1[1] = {sc}, cz1[1] = {off + zc};
+      gemm_group<ACT, 1, false>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, sc1, cz1, acc);
+    }
+    if (more) gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
+                               gemm_row_sum<ACT>(sv));
+    wc = wn; sc = sn; zc = zn;
+    __syncthreads();
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s < nsub) {
+      const float vv[4] = {acc[0][s].x, acc[0][s].y, acc[0][s].z, acc[0][s].w};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * s + 4 * q + v;
+        if (row < rows) c.eout[(size_t)pairs[row] * H + 64 * m + 16 * wave + r] = vv[v];
+      }
+    }
+  }
+}
+
+hipError_t launch_w4a16_gemm(const W4Args& a, int act, int tiles_max, hipStream_t st, hipEvent_t mid) {
+  const int g13 = tiles_max * (a.c.I / 64), g2 = tiles_max * (a.c.H / 64);
+  if (act == 1)
+    hipLaunchKernelGGL((w4a16_gemm13_kernel<1>), dim3(g13), dim3(kBlock), kGemmLds, st, a);
+  else
+    hipLaunchKernelGGL((w4a16_gemm13_kernel<0>), dim3(g13), dim3(kBlock), kGemmLds, st, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
+  if (act == 1)
+    hipLaunchKernelGGL((w4a16_gemm2_kernel<1>), dim3(g2), dim3(kBlock), kGemmLds, st, a);
+  else
+    hipLaunchKernelGGL((w4a16_gemm2_kernel<0>), dim3(g2), dim3(kBlock), kGemmLds, st, a);
+  return hipGetLastError();
+}
+
 // ================================================================ repack
 // AWQ wire (qweight [E][K][N/8], nibble slot {0,4,1,5,2,6,3,7}[n%8]) -> tiles.
 __device__ __forceinline__ int awq_slot(int col) {
