@@ -34,8 +34,8 @@ hipError_t launch_awq_repack_all(const int32_t*, const int32_t*, const uint16_t*
                                  const int32_t*, const uint16_t*, void*, unsigned char*, void*,
                                  unsigned char*, int, int, int, hipStream_t);
 hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*, hipStream_t);
-W4Plan w4a16_plan(int, int, int64_t, int64_t, int);
-hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, int, hipStream_t, hipEvent_t);
+W4Plan w4a16_plan(int, int);
+hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, hipStream_t);
 hipError_t launch_q_repack(int, const void*, const uint16_t*, void*, uint16_t*, int, int, int, int,
@@ -206,22 +206,16 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
   a.sdt = h->scale_dtype;
   // decode path: T*K <= 64 pairs, at most kDownMaxK experts per token (a
   // wave each in the down kernel)
-  const bool ballot = n <= 64 && K <= kDownMaxK;
-  a.route_lds = (ballot || a.c.route_global) ? 0 : (int)(route_lds_ints((int)h->E, (int)n) * sizeof(int));
-  // phase 1 copies the hidden rows of every token when they are few
-  a.x_all = ballot && (size_t)T * h->H * 2 <= kXAllBytes;
-  // token columns per pass: up to 16, as many as fit 64 KB of LDS with the
-  // routing arrays (cnt <= T unless a token repeats an expert; more passes then)
-  a.p1_cols = a.p2_cols = (int)(T < 16 ? T : 16);
-  // decode: an expert rarely gets more than a few of the T tokens; a narrow
-  // pass keeps the LDS small (occupancy), extra columns take another pass
-  if (ballot && a.p1_cols > kDecodeCols) a.p1_cols = kDecodeCols;
-  while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1) + a.route_lds > kMaxLds) --a.p1_cols;
-  while (a.p2_cols > 1 && w4_p2_lds_bytes((int)h->I, a.p2_cols) + a.route_lds > kMaxLds) --a.p2_cols;
-  const W4Plan plan = w4a16_plan((int)h->H, (int)h->I, T, K, ballot);
   hipEvent_t mid = h->timing ? h->evmid : nullptr;
-  if (ballot) {
-    HIPCHK(launch_w4a16(a, plan, act, 1, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st, mid));
+  if (n <= 64 && K <= kDownMaxK) {
+    // phase 1 copies the hidden rows of every token when they are few
+    a.x_all = (size_t)T * h->H * 2 <= kXAllBytes;
+    // an expert rarely gets more than a few of the T tokens; a narrow pass
+    // keeps the LDS small (occupancy), extra columns take another pass
+    a.p1_cols = (int)(T < kDecodeCols ? T : kDecodeCols);
+    while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1) > kMaxLds) --a.p1_cols;
+    const W4Plan plan = w4a16_plan((int)h->H, (int)h->I);
+    HIPCHK(launch_w4a16(a, plan, act, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st, mid));
     h->mid_recorded = mid != nullptr;
     return MI_MOE_OK;
   }

@@ -50,10 +50,9 @@ struct W4Args {
   const void* w2;              // [e][H/64][4][I/128][64 lanes][16 B]
   const unsigned char* w2_m;   // metadata sections of w2_meta_sec_bytes(I/128) per (e, H/64 quad, row tile)
   uint16_t* act;               // [n, I] SiLU*mul activations (act dtype), row = pair
-  int p1_cols, p2_cols;        // token columns per pass (rows staged in LDS)
+  int p1_cols;                 // phase-1 token columns per pass (rows staged in LDS)
   int sdt;                     // scale dtype: 1 bf16, 0 fp16
   int x_all;                   // phase 1 copies the hidden rows of all T tokens at start
-  int route_lds;               // bytes of routing arrays in LDS (sorted path)
 };
 
 // Bytes of the w2 metadata of one 16-row tile: G2 = I/128 groups of 16 u16
@@ -63,13 +62,10 @@ __host__ __device__ inline int w2_meta_sec_bytes(int G2) { return (40 * G2 + 15)
 // The decode down kernel runs a wave per routed expert of a token.
 constexpr int kDownMaxK = 8;
 
-// LDS bytes of the W4A16 kernels (routing arrays come on top).
+// LDS bytes of the W4A16 decode kernels.
 constexpr int kP1RedBytes = 4 * 2 * 64 * 4 * 4;
 __host__ __device__ inline size_t w4_p1_lds_bytes(int H, int xrows, int slices) {
   return (size_t)slices * (kP1RedBytes + 80 * (H >> 7)) + (size_t)xrows * H * 2;
-}
-__host__ __device__ inline size_t w4_p2_lds_bytes(int I, int cols) {
-  return (size_t)4 * w2_meta_sec_bytes(I >> 7) + (size_t)cols * I * 2;
 }
 __host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) {
   return (size_t)K * I * 2 + (size_t)K * RT * w2_meta_sec_bytes(I >> 7) + (size_t)K * 16 * RT * 4 + (size_t)K * 4;

@@ -1,12 +1,12 @@
-// mi_moe_sched.hpp -- routing view shared by the multi-launch MoE paths.
+// mi_moe_sched.hpp -- routing view of the Q8_0 / Q4_0 multi-launch path.
 //
-// Multi-launch path (any T*K): phase 1 (one workgroup per (expert, slice of
-// I)) computes gate_up + SiLU*mul into act[i] for every routed pair i = t*K+k
-// of the expert; phase 2 (one workgroup per (expert, 64-row block of H))
-// computes the down projection into eout[i]; a combine kernel sums eout over k
-// in order and casts (Stage C1 + C2 of Int8-gemm/q8_gemm.cpp:593-641, tp = 1).
-// Kernel boundaries are the only dependencies; nothing waits inside a kernel.
-// Every workgroup routes the pairs itself -- the stable counting sort of
+// Phase 1 (one workgroup per (expert, slice of I)) computes gate_up +
+// SiLU*mul (+ the intermediate Q8_0) into act[i] for every routed pair
+// i = t*K+k of the expert; phase 2 (one workgroup per (expert, 64-row block of
+// H)) computes the down projection into eout[i]; a combine kernel sums eout
+// over k in order and casts (Stage C1 + C2 of Int8-gemm/q8_gemm.cpp:593-641,
+// tp = 1).  Kernel boundaries are the only dependencies.  Every workgroup
+// routes the pairs itself -- the stable counting sort of
 // preprocess_moe_routing (Int8-gemm/moe_common.cpp:146-216) -- in LDS for
 // small T*K, or reads the arrays the routing kernel wrote.  Workgroups whose
 // item index is past the active experts exit at once.

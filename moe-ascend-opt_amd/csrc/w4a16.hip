@@ -34,17 +34,17 @@
 //     [g2][r/2] (row r in nibble r&1).
 //
 // Paths (chosen on the host); rows of act/eout are indexed by pair i = t*K+k:
-//   decode (T*K <= 64, K <= 16): two launches.  Phase 1 (gate_up + SiLU*mul ->
-//     act) has a work item per pair; an item serves its expert iff it is the
-//     expert's first pair, the others exit at once.  The down kernel has a
-//     workgroup per (token, 16-row tile) with a wave per routed expert, and
-//     combines in LDS.
-//   general: routing (in LDS up to 1024 pairs, else a routing kernel), phase 1,
-//     phase 2 -> eout, and a combine kernel.
+//   decode (T*K <= 64, K <= kDownMaxK): two launches.  Phase 1 (gate_up +
+//     SiLU*mul -> act) has a work item per pair; an item serves its expert iff
+//     it is the expert's first pair, the others exit at once.  The down kernel
+//     has a workgroup per (token, 16-row tile) with a wave per routed expert,
+//     and combines in LDS.
+//   sorted (any other T, K): the routing kernel (with 64-row tiles of each
+//     expert's rows), the grouped GEMMs gate_up (-> act) and down (-> eout),
+//     and the combine kernel.
 #pragma clang fp contract(off)
 #include "mi_moe_device.hpp"
 #include "mi_moe_internal.hpp"
-#include "mi_moe_sched.hpp"
 
 namespace mimoe {
 
@@ -184,43 +184,6 @@ __device__ __forceinline__ BallotCols ballot_cols(const SchedArgs& c, int pi, in
   return b;
 }
 
-// Expert and columns of a work item: ballot routing (BALLOT) or the sorted
-// routing arrays.
-template <int BALLOT>
-struct Cols {
-  int e = 0, cnt = 0, colpair = 0;
-  const int* pairs = nullptr;
-  uint64_t vmask = 0;
-  // pair index of column col; every lane of the wave must call it (BALLOT)
-  __device__ __forceinline__ int pair(int col, bool valid) const {
-    if constexpr (BALLOT) {
-      const int p = __shfl(colpair, col & 63);
-      return valid ? p : 0;
-    } else {
-      return valid ? pairs[col] : 0;
-    }
-  }
-};
-
-// Returns false when the item has nothing to do.
-template <int BALLOT>
-__device__ __forceinline__ bool get_cols(const SchedArgs& c, int item, int lane, void* route_lds,
-                                         int* s_U, Cols<BALLOT>& out) {
-  if constexpr (BALLOT) {
-    const BallotCols b = ballot_cols(c, item, lane);
-    out.e = b.e; out.cnt = b.cnt; out.colpair = b.colpair; out.vmask = b.vmask;
-    return b.serve;
-  } else {
-    const RouteView rv = sched_route(c, reinterpret_cast<int*>(route_lds), s_U);
-    if (item >= rv.U) return false;
-    out.e = rv.active[item];
-    const int p0 = rv.starts[out.e];
-    out.cnt = rv.starts[out.e + 1] - p0;
-    out.pairs = rv.pair + p0;
-    return true;
-  }
-}
-
 // ================================================================ phase 1
 // Register budgets, as waves per SIMD: phase 1 spills above 4; the down
 // kernel (8-wave workgroups) fits 6 without spills, i.e. 3 workgroups per CU.
@@ -235,30 +198,30 @@ constexpr int kDownWavesPerEU = 6;
 // pass's last column, so the loop body has no branches; their results are
 // never stored.  Hidden rows: with a.x_all the rows of all T tokens are copied
 // into LDS at kernel start, in parallel with the routing read; otherwise the
-// rows of each pass's columns are copied once the routing is known.
-// LDS (w4_p1_lds_bytes): red [S][wave][gate,up][64][4] f32 | metadata S x 80*G1 B | x rows | routing.
-template <int ACT, int BALLOT, int NB, int S>
+// rows of each pass's columns are copied once the routing is known.  Work
+// item = pair index; the items of an expert's later pairs exit at once.
+// LDS (w4_p1_lds_bytes): red [S][wave][gate,up][64][4] f32 | metadata S x 80*G1 B | x rows.
+template <int ACT, int NB, int S>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kP1WavesPerEU)))
 void w4a16_phase1_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_U;
   const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, NJS = NI1 / S, P = a.p1_cols, HI = H >> 3;
-  const int XR = a.x_all ? c.T : P;   // rows of x held in LDS
   float* red = reinterpret_cast<float*>(smem);
   unsigned char* meta = smem + S * kP1RedBytes;
   uint16_t* xs = reinterpret_cast<uint16_t*>(meta + S * 80 * G1);
-  unsigned char* route = reinterpret_cast<unsigned char*>(xs) + (size_t)XR * H * 2;
   const int item = blockIdx.x / NJS, j0 = (blockIdx.x - item * NJS) * S;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   if (a.x_all)   // uniform; x is [T][H] contiguous
     stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, 4, lane,
               [&](int k) { return (const void*)(c.x + 8 * (size_t)k); });
-  Cols<BALLOT> cl;
-  if (!get_cols<BALLOT>(c, item, lane, route, &s_U, cl)) {   // uniform
+  const BallotCols cl = ballot_cols(c, item, lane);
+  if (!cl.serve) {   // uniform
     __builtin_amdgcn_s_waitcnt(0);   // no copy into LDS outlives the workgroup
     return;
   }
+  // pair index of column col; every lane of the wave calls it
+  auto pair_of = [&](int col) { return __shfl(cl.colpair, col & 63); };
   const int e = cl.e, cnt = cl.cnt;
   const size_t blk = (size_t)e * NI1 + j0;   // S consecutive slices: contiguous weights and metadata
   const unsigned char* msrc = a.w13_m + blk * 80 * G1;
@@ -270,11 +233,11 @@ void w4a16_phase1_kernel(W4Args a) {
     const int ncol = min(P, cnt - cb0);
     int xr;   // LDS row of this lane's column
     if (a.x_all) {
-      xr = cl.pair(cb0 + min(r, ncol - 1), true) / c.K;
+      xr = pair_of(cb0 + min(r, ncol - 1)) / c.K;
     } else {
       stage_lds(reinterpret_cast<unsigned char*>(xs), ncol * HI, wave, 4, lane, [&](int k) {
         const int cc = k / HI;
-        const int t = cl.pair(cb0 + cc, true) / c.K;
+        const int t = pair_of(cb0 + cc) / c.K;
         return (const void*)(c.x + (size_t)t * H + 8 * (k - cc * HI));
       });
       xr = min(r, ncol - 1);
@@ -343,7 +306,7 @@ void w4a16_phase1_kernel(W4Args a) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int col = cb0 + 4 * (ln >> 4) + v;
-        const int p = cl.pair(col, col < cnt);
+        const int p = pair_of(col);
         if (col < cnt)
           a.act[(size_t)p * c.I + 16 * (j0 + s) + (ln & 15)] = from_f32<ACT>(silu_mul_fast(gv[v], uv[v]));
       }
@@ -402,54 +365,6 @@ __device__ __forceinline__ void down_tiles(const char* wb, const uint16_t* arow,
         fold(acc[rt], G, X, w2_scale(sec, g2, r, sdt), off + w2_zero(sec, G2, g2, r));
       }
     }
-  }
-}
-
-// ================================================================ phase 2 (general)
-// Workgroup (item, quad m = rows 64m..64m+63): down projection of the quad for
-// every routed pair of the item's expert, in passes of p2_cols columns, into
-// eout[pair][64m..] (a combine kernel follows).  Wave w owns rows
-// 64m+16w..+15 over all of I, so no cross-wave reduction is needed; a lane's
-// 16-byte weight word holds its row's four 32-k chunks of one 128-k group, so
-// the group's four MFMAs accumulate in the matrix core and its scale and zero
-// are applied once.  NB, from the host, divides I/128.
-// LDS: metadata sections [4][SEC] | act rows [p2_cols][I] | routing.
-template <int ACT, int NB>
-__global__ __launch_bounds__(kBlock) void w4a16_phase2_kernel(W4Args a) {
-  const SchedArgs& c = a.c;
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_U;
-  const int H = c.H, I = c.I, MQ = H >> 6, G2 = I >> 7, P = a.p2_cols, II = I >> 3;
-  const int SEC = w2_meta_sec_bytes(G2);
-  unsigned char* meta = smem;
-  uint16_t* as = reinterpret_cast<uint16_t*>(meta + 4 * SEC);
-  unsigned char* route = reinterpret_cast<unsigned char*>(as) + (size_t)P * I * 2;
-  const int item = blockIdx.x / MQ, m = blockIdx.x - item * MQ;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
-  Cols<0> cl;
-  if (!get_cols<0>(c, item, lane, route, &s_U, cl)) return;  // uniform
-  const int e = cl.e, cnt = cl.cnt;
-  const size_t blk = (size_t)e * MQ + m;
-  const unsigned char* msrc = a.w2_m + blk * 4 * SEC;
-  stage_lds(meta, SEC / 4, wave, 4, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
-  const char* wb = (const char*)a.w2 + (blk * 4 + wave) * G2 * 1024 + lane * 16;
-  for (int cb0 = 0; cb0 < cnt; cb0 += P) {
-    const int ncol = min(P, cnt - cb0);
-    stage_lds(reinterpret_cast<unsigned char*>(as), ncol * II, wave, 4, lane, [&](int k) {
-      const int cc = k / II;
-      return (const void*)(a.act + (size_t)cl.pair(cb0 + cc, true) * I + 8 * (k - cc * II));
-    });
-    f32x4_t acc[1];
-    down_tiles<ACT, NB, 1>(wb, as + min(r, ncol - 1) * I + 8 * q, meta + wave * SEC, SEC, G2, r,
-                           a.sdt, acc);
-    // lane (r, q): row 64m + 16 wave + r, token columns 4q..4q+3
-    const float vv[4] = {acc[0].x, acc[0].y, acc[0].z, acc[0].w};
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int col = cb0 + 4 * q + v;
-      if (col < cnt) c.eout[(size_t)cl.pair(col, true) * H + 64 * m + 16 * wave + r] = vv[v];
-    }
-    __syncthreads();   // the act rows are reused by the next pass
   }
 }
 
@@ -519,7 +434,8 @@ void w4a16_down_token_kernel(W4Args a) {
 // rows are computed), B the dequantized weights:
 //   acc += s * (sum_k x (magic + q) - (offset + z) * sum_k x)   per group,
 // the same arithmetic as the decode kernels, with the row sums from v_dot2
-// instead of a ones-MFMA.  Every weight byte is read and dequantized once per
+// instead of a ones-MFMA.  Only the waves of sub-tiles that hold rows store
+// staged rows.  Every weight byte is read and dequantized once per
 // row tile, so an expert with many rows streams its weights a few times and
 // the MFMAs work on full 16-row operands.
 constexpr int kGemmRowStride = 272;   // 256 B of a row + 16 B that spread the rows over the LDS banks
@@ -612,13 +528,16 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
   int* pairs = reinterpret_cast<int*>(sums0 + 2 * kGemmRows);   // the tile's pair indices
   constexpr float off = W4Consts<ACT>::offset;
 
+  // only the waves of the sub-tiles holding rows store staged activations
+  // (uniform per wave); every wave loads, so the loads stay unconditional
+  const bool stager = wave < nsub;
   u32x4_t sv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sv[i] = ldg16(xsrc + 8 * i);
   u32x4_t wgc = ldg16(wg), wuc = ldg16(wg + (size_t)G1 * 1024);
   uint32_t scc = msc[0], zzc = mz[0];
   if (spart == 0) pairs[srow] = spair;
-  gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
+  if (stager) gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
   __syncthreads();
   f32x4_t acc[2][4];
 #pragma unroll
@@ -644,8 +563,9 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
       const float cz2[2] = {off + (float)(zzc & 0xfu), off + (float)((zzc >> 4) & 0xfu)};
       gemm_group<ACT, 2, true>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, sc2, cz2, acc);
     }
-    if (more) gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
-                               gemm_row_sum<ACT>(sv));
+    if (more && stager)
+      gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
+                       gemm_row_sum<ACT>(sv));
     wgc = wgn; wuc = wun; scc = scn; zzc = zzn;
     __syncthreads();
   }
@@ -688,13 +608,14 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
   int* pairs = reinterpret_cast<int*>(sums0 + 2 * kGemmRows);
   constexpr float off = W4Consts<ACT>::offset;
 
+  const bool stager = wave < nsub;
   u32x4_t sv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sv[i] = ldg16(asrc + 8 * i);
   u32x4_t wc = ldg16(wb);
   float sc = w2_scale(sec, 0, r, a.sdt), zc = w2_zero(sec, G2, 0, r);
   if (spart == 0) pairs[srow] = spair;
-  gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
+  if (stager) gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
   __syncthreads();
   f32x4_t acc[1][4];
 #pragma unroll
@@ -715,8 +636,9 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
       const float sc1[1] = {sc}, cz1[1] = {off + zc};
       gemm_group<ACT, 1, false>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, sc1, cz1, acc);
     }
-    if (more) gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
-                               gemm_row_sum<ACT>(sv));
+    if (more && stager)
+      gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
+                       gemm_row_sum<ACT>(sv));
     wc = wn; sc = sn; zc = zn;
     __syncthreads();
   }
@@ -879,36 +801,33 @@ hipError_t launch_awq_repack_all(const int32_t* w13q, const int32_t* w13z, const
 }
 
 // ================================================================ launchers
-template <int ACT, int BALLOT, int NB, int S>
+template <int ACT, int NB, int S>
 static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, BALLOT, NB, S>), dim3(grid), dim3(kBlock), lds, st, a);
+  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, NB, S>), dim3(grid), dim3(kBlock), lds, st, a);
 }
 
 // (NB, S) pairs instantiated for phase 1.  S > 1 measured slower on the
 // decode shapes (occupancy), so only S = 1 is built.
-template <int ACT, int BALLOT>
+template <int ACT>
 static hipError_t dispatch_p1(const W4Args& a, int nb, int s, int grid, size_t lds, hipStream_t st) {
 #define P1_CASE(NB_, S_) \
-  if (nb == NB_ && s == S_) { launch_p1<ACT, BALLOT, NB_, S_>(a, grid, lds, st); return hipGetLastError(); }
+  if (nb == NB_ && s == S_) { launch_p1<ACT, NB_, S_>(a, grid, lds, st); return hipGetLastError(); }
   P1_CASE(1, 1) P1_CASE(2, 1) P1_CASE(3, 1) P1_CASE(4, 1) P1_CASE(6, 1) P1_CASE(8, 1)
 #undef P1_CASE
   return hipErrorInvalidValue;
 }
 
-// (NB, RT) pairs instantiated for the down kernels.  RT > 1 (2-4 tiles per
+// (NB, RT) pairs instantiated for the down kernel.  RT > 1 (2-4 tiles per
 // wave) measured no faster on the decode shapes, so only RT = 1 is built.
-template <int ACT, int BALLOT>
+template <int ACT>
 static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int grid, size_t lds, hipStream_t st) {
-#define P2_CASE(NB_, RT_)                                                                          \
-  if (nb == NB_ && rt == RT_) {                                                                    \
-    if constexpr (BALLOT)                                                                          \
-      hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3(grid), dim3(64 * a.c.K), lds, \
-                         st, a);                                                                   \
-    else if constexpr (RT_ == 1)                                                                   \
-      hipLaunchKernelGGL((w4a16_phase2_kernel<ACT, NB_>), dim3(grid), dim3(kBlock), lds, st, a);  \
-    return hipGetLastError();                                                                      \
+#define P2_CASE(NB_, RT_)                                                                           \
+  if (nb == NB_ && rt == RT_) {                                                                     \
+    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3(grid), dim3(64 * a.c.K), lds, \
+                       st, a);                                                                      \
+    return hipGetLastError();                                                                       \
   }
-  P2_CASE(1, 1) P2_CASE(2, 1) P2_CASE(3, 1) P2_CASE(4, 1) P2_CASE(6, 1) P2_CASE(8, 1) P2_CASE(12, 1)
+  P2_CASE(1, 1) P2_CASE(2, 1) P2_CASE(3, 1) P2_CASE(4, 1) P2_CASE(6, 1) P2_CASE(8, 1)
 #undef P2_CASE
   return hipErrorInvalidValue;
 }
@@ -921,44 +840,39 @@ static int pick_div(const int* sizes, int count, int need) {
   return b;
 }
 
-// Launch geometry: batch sizes divide the per-wave group counts (S slices per
-// phase-1 workgroup and RT row tiles per down wave are 1: larger values
-// measured no faster on the decode shapes).
-W4Plan w4a16_plan(int H, int I, int64_t T, int64_t K, int ballot) {
-  (void)T; (void)K;
-  static const int nb1[] = {1, 2, 3, 4, 6, 8}, nb2[] = {1, 2, 3, 4, 6, 8, 12};
+// Launch geometry of the decode path: batch sizes divide the per-wave group
+// counts (S slices per phase-1 workgroup and RT row tiles per down wave are 1:
+// larger values measured no faster on the decode shapes).  The token-major
+// down kernel spills at NB = 12 within its 6-waves-per-SIMD register budget,
+// so NB <= 8 there.
+W4Plan w4a16_plan(int H, int I) {
+  static const int nb1[] = {1, 2, 3, 4, 6, 8}, nb2[] = {1, 2, 3, 4, 6, 8};
   W4Plan p;
   p.nb1 = pick_div(nb1, 6, H / 512);
   p.s1 = 1;
-  // the token-major down kernel (ballot) spills at NB = 12 within its
-  // 6-waves-per-SIMD register budget
-  p.nb2 = pick_div(nb2, ballot ? 6 : 7, I / 128);
+  p.nb2 = pick_div(nb2, 6, I / 128);
   p.rt2 = 1;
   return p;
 }
 
-template <int ACT, int BALLOT>
+template <int ACT>
 static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int grid2, hipStream_t st,
                               hipEvent_t mid) {
-  const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1) + a.route_lds;
-  const size_t lds2 = BALLOT ? w4_down_token_lds_bytes(a.c.I, a.c.K, p.rt2)
-                             : w4_p2_lds_bytes(a.c.I, a.p2_cols) + a.route_lds;
-  hipError_t err = dispatch_p1<ACT, BALLOT>(a, p.nb1, p.s1, grid1 / p.s1, lds1, st);
+  const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1);
+  const size_t lds2 = w4_down_token_lds_bytes(a.c.I, a.c.K, p.rt2);
+  hipError_t err = dispatch_p1<ACT>(a, p.nb1, p.s1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
-  return dispatch_p2<ACT, BALLOT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
+  return dispatch_p2<ACT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
 }
 
-// ballot = 1 (T*K <= 64, K <= kDownMaxK): grid1 = T*K * I/16, grid2 = T * H/16 (down
-// kernel, writes y); ballot = 0: grid1 = U * I/16, grid2 = U * H/64 with
-// U = min(T*K, E) and sorted routing; the caller launches the combine.  The
-// plan divides the grids by its slice / tile counts.  mid (optional) is
-// recorded between the gate_up and down launches.
-hipError_t launch_w4a16(const W4Args& a, const W4Plan& p, int act, int ballot, int grid1, int grid2,
-                        hipStream_t st, hipEvent_t mid) {
-  if (act == 1)
-    return ballot ? launch_w4_t<1, 1>(a, p, grid1, grid2, st, mid) : launch_w4_t<1, 0>(a, p, grid1, grid2, st, mid);
-  return ballot ? launch_w4_t<0, 1>(a, p, grid1, grid2, st, mid) : launch_w4_t<0, 0>(a, p, grid1, grid2, st, mid);
+// Decode path (T*K <= 64, K <= kDownMaxK): grid1 = T*K * I/16 (phase 1),
+// grid2 = T * H/16 (down kernel, writes y); the plan divides them by its
+// slice / tile counts.  mid (optional) is recorded between the two launches.
+hipError_t launch_w4a16(const W4Args& a, const W4Plan& p, int act, int grid1, int grid2, hipStream_t st,
+                        hipEvent_t mid) {
+  if (act == 1) return launch_w4_t<1>(a, p, grid1, grid2, st, mid);
+  return launch_w4_t<0>(a, p, grid1, grid2, st, mid);
 }
 
 }  // namespace mimoe
