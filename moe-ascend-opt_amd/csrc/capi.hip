@@ -38,6 +38,7 @@ W4Plan w4a16_plan(int, int);
 hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, hipStream_t);
+hipError_t launch_qint_gemm(const QArgs&, int, int, int, hipStream_t);
 hipError_t launch_q_repack(int, const void*, const uint16_t*, void*, uint16_t*, int, int, int, int,
                            int, hipStream_t);
 hipError_t launch_q8_online_quant(const void*, int, int, int, int, int, int, void*, uint16_t*,
@@ -122,6 +123,7 @@ struct mi_moe_handle {
   // workspace
   int64_t cap_T = 0, cap_n = 0;
   DevBuf act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U, r_tiles, r_ntiles;
+  DevBuf xq, xd;   // Q8_0 activations of the grouped-GEMM path
 };
 
 namespace {
@@ -159,6 +161,10 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
   HIPCHK(h->r_tok.alloc((size_t)capn * sizeof(int32_t)));
   HIPCHK(h->r_scat.alloc((size_t)capn * sizeof(int32_t)));
   HIPCHK(h->r_tiles.alloc((size_t)gemm_tiles_max(capn, (int)h->E) * 4 * sizeof(int32_t)));
+  if (h->quant != MI_MOE_W4A16) {
+    HIPCHK(h->xq.alloc((size_t)capT * h->H));
+    HIPCHK(h->xd.alloc((size_t)capT * (h->H / 32) * sizeof(float)));
+  }
   h->cap_T = capT;
   h->cap_n = capn;
   return MI_MOE_OK;
@@ -253,6 +259,17 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   a.w2 = h->w2.p; a.w2_d = (const uint16_t*)h->w2_s.p;
   a.act_q = (int8_t*)h->act.p;
   a.act_d = (float*)h->act_d.p;
+  if (n > kQGemmMinPairs && h->H % 128 == 0 && h->I % 128 == 0) {
+    // sorted path: Q8_0 activations once per token, routing with row tiles,
+    // the two int8 grouped GEMMs, the combine
+    a.xq = (const int8_t*)h->xq.p;
+    a.xd = (const float*)h->xd.p;
+    HIPCHK(launch_quant_act(x, act, T, h->H, (int8_t*)h->xq.p, (float*)h->xd.p, st));
+    HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
+    HIPCHK(launch_qint_gemm(a, h->quant, h->scale_dtype, (int)gemm_tiles_max(n, (int)h->E), st));
+    HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
+    return MI_MOE_OK;
+  }
   if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
   const int64_t umax = n < h->E ? n : h->E;
   const int64_t grid1 = umax * (h->I / 32), grid2 = umax * (h->H / 64);
@@ -299,7 +316,8 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
   (void)hipDeviceSynchronize();
   DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z,
                     &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
-                    &h->r_active, &h->r_tok, &h->r_scat, &h->r_U, &h->r_tiles, &h->r_ntiles};
+                    &h->r_active, &h->r_tok, &h->r_scat, &h->r_U, &h->r_tiles, &h->r_ntiles,
+                    &h->xq, &h->xd};
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
   if (h->ev1) (void)hipEventDestroy(h->ev1);

@@ -26,6 +26,8 @@ struct RouteGlobal {
 
 // Row tile of the grouped GEMMs of the sorted path: routed rows of one expert.
 constexpr int kGemmRows = 64;
+// Q8_0 / Q4_0: above this many routed pairs the int8 grouped GEMMs run
+constexpr int kQGemmMinPairs = 64;
 __host__ __device__ inline int64_t gemm_tiles_max(int64_t n, int E) {
   return n / kGemmRows + (n < E ? n : E);
 }
@@ -86,6 +88,8 @@ struct QArgs {
   const uint16_t* w2_d;    // [E][H/64][I/32][64]
   int8_t* act_q;           // [n, I] intermediate Q8_0 bytes, row = pair
   float* act_d;            // [n, I/32] intermediate Q8_0 scales
+  const int8_t* xq;        // [T, H] Q8_0 activations (grouped GEMM path)
+  const float* xd;         // [T, H/32]
 };
 
 }  // namespace mimoe

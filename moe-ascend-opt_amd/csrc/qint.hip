@@ -318,6 +318,319 @@ hipError_t launch_qint(const QArgs& a, int qt, int act, int sc, int grid1, int g
   return sc == 1 ? launch_q_t<1, 0, 1>(a, grid1, grid2, st) : launch_q_t<1, 0, 0>(a, grid1, grid2, st);
 }
 
+// ---------------------------------------------------------------- grouped GEMMs (int8 MFMA)
+// Sorted path for the prefill sizes: the routing kernel's row tiles (up to
+// kGemmRows = 64 routed rows of one expert) x a 64-row block of the output,
+// with v_mfma_i32_16x16x32_i8 giving the exact int32 dot of one 32-element
+// block for 16 rows x 16 output rows, then per element, in k-block order,
+//     c += ((float)isum * dw[n, kb]) * da[m, kb]
+// (Int8-gemm/gemm_kernels.cpp:156-179; Q4_0: dot with nibble - 8,
+// :262-309).  The first product is bit-identical to the reference's; the
+// second is fused with the add (one rounding fewer than its vmulq + vmlaq,
+// inside the fp32 tolerance).  Wave w owns output rows 16w..16w+15 of the
+// block for all rows of the tile (NSUB sub-tiles of 16) and all of K.
+// Activations were Q8_0-quantized once per token (x) or are the intermediate
+// Q8_0 rows (act); the workgroup stages kQgStage blocks of the tile's rows and
+// their scales into LDS per step, double-buffered, and each wave loads its
+// weights for the next step before computing the current one.
+// MFMA operands: A = the wave's 16 weight rows, B = 16 tile rows (lane 16q + r:
+// row r, bytes 8q..8q+7 of the block for both); D lane 16q + r = tile row r of
+// the sub-tile x weight rows 4q..4q+3, so a lane needs one activation scale
+// per sub-tile and four weight scales per block.
+//
+// Two exact rewrites keep the VALU work at two fma per output and block:
+// * the accumulator starts from the bits of 1.5 * 2^23 (kQgBias), so with
+//   |isum| < 2^22 the int32 result read as a float is 1.5 * 2^23 + isum, and
+//   fma(that, dw, -1.5 * 2^23 * dw) = round(isum * dw): the product
+//   1.5 * 2^23 * dw is exact (dw has at most 11 significant bits) and the fma
+//   rounds once;
+// * Q4_0 nibbles n enter the MFMA as bytes 16 * (n - 8) (n ^ 8 in the high
+//   half of the byte), so the int32 result is 16 * isum exactly, the first
+//   product 16 * round(isum * dw), and the activation scale is staged as
+//   da / 16 (powers of two: the same products and roundings).
+// The activation scales of a step are staged [row][block] (one 16-byte read
+// per sub-tile and step).
+constexpr int kQgStage = 4;                          // 32-element blocks per step
+constexpr int kQgRowStride = kQgStage * 32 + 16;     // bytes per staged row (pad spreads the banks)
+constexpr int kQgABytes = kGemmRows * kQgRowStride;  // 9216
+constexpr int kQgBufBytes = kQgABytes + kGemmRows * kQgStage * 4;   // + scales [row][block]
+// LDS: [2][kQgBufBytes] | act tile [64][kQgActStride] f32 (gate_up epilogue) | pairs [64]
+constexpr int kQgActStride = 36;   // 32 columns + pad (16-byte rows, spread banks)
+constexpr size_t kQgLds = 2 * (size_t)kQgBufBytes + kGemmRows * kQgActStride * 4 + kGemmRows * 4;
+constexpr int kQgBias = 0x4B400000;      // bits of 1.5 * 2^23
+constexpr float kQgBiasF = 12582912.0f;  // 1.5 * 2^23
+
+struct QgStage { u32x4_t v[2]; float d; };
+
+// this thread's 32-byte block of its row (one of kQgStage blocks of the step)
+__device__ __forceinline__ QgStage qg_load(const int8_t* rowq, const float* rowd, int kb) {
+  QgStage s;
+  const u32x4_t* p = reinterpret_cast<const u32x4_t*>(rowq + 32 * kb);
+  s.v[0] = p[0];
+  s.v[1] = p[1];
+  s.d = rowd[kb];
+  return s;
+}
+
+template <int QT>
+__device__ __forceinline__ void qg_store(unsigned char* buf, int srow, int sblk, const QgStage& s) {
+  *reinterpret_cast<u32x4_t*>(buf + srow * kQgRowStride + 32 * sblk) = s.v[0];
+  *reinterpret_cast<u32x4_t*>(buf + srow * kQgRowStride + 32 * sblk + 16) = s.v[1];
+  reinterpret_cast<float*>(buf + kQgABytes)[srow * kQgStage + sblk] = QT == 1 ? s.d * 0.0625f : s.d;
+}
+
+// The lane's 8 weight bytes (k = 8q..8q+7 of the block) of tile lane `tl` for
+// block kb: Q8_0 from the chunk of bytes 16*(q/2).., Q4_0 word q (elements
+// 8q+m in the low nibble of byte m, 8q+4+m in the high one).
+template <int QT>
+__device__ __forceinline__ uint64_t qg_wload(const char* tile, int kb, int tl, int q) {
+  const char* blk = tile + (size_t)kb * QFmt<QT>::block_bytes;
+  if constexpr (QT == 0) {
+    return *reinterpret_cast<const uint64_t*>(blk + (q >> 1) * 1024 + tl * 16 + 8 * (q & 1));
+  } else {
+    return *reinterpret_cast<const uint32_t*>(blk + tl * 16 + 4 * q);
+  }
+}
+// MFMA B bytes: Q8_0 as stored; Q4_0 as 16 * (n - 8), elements 8q..8q+7
+template <int QT>
+__device__ __forceinline__ long qg_wbytes(uint64_t w) {
+  if constexpr (QT == 0) {
+    return (long)w;
+  } else {
+    const uint32_t x = (uint32_t)w ^ 0x88888888u;   // n ^ 8: the 4-bit two's complement of n - 8
+    return (long)((uint64_t)((x << 4) & 0xf0f0f0f0u) | ((uint64_t)(x & 0xf0f0f0f0u) << 32));
+  }
+}
+
+// acc[s] += round(isum * dw) * da (fused) for block `sblk` of the step and the
+// NSUB sub-tiles.  raw = the fp16/bf16 scales of weight rows 4q..4q+3;
+// dq[s] = the staged activation scales of tile row 16s + r for the step's
+// blocks.
+template <int SC, int NSUB>
+__device__ __forceinline__ void qg_block(const unsigned char* buf, int sblk, int r, int q, long wb,
+                                         u32x2_t raw, const f32x4_t (&dq)[4], f32x4_t (&acc)[4]) {
+  const uint32_t rw[4] = {raw.x & 0xffffu, raw.x >> 16, raw.y & 0xffffu, raw.y >> 16};
+  float dws[4], nb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dws[i] = to_f32<SC>(rw[i]);
+    nb[i] = -kQgBiasF * dws[i];
+  }
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s) {
+    const long av = *reinterpret_cast<const long*>(buf + (16 * s + r) * kQgRowStride + 32 * sblk + 8 * q);
+    i32x4_t d = {kQgBias, kQgBias, kQgBias, kQgBias};
+    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(wb, av, d, 0, 0, 0);
+    const float da = dq[s][sblk];
+    const int dv[4] = {d.x, d.y, d.z, d.w};
+    float* ac = reinterpret_cast<float*>(&acc[s]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t1 = __builtin_fmaf(__int_as_float(dv[i]), dws[i], nb[i]);
+      ac[i] = __builtin_fmaf(t1, da, ac[i]);
+    }
+  }
+}
+
+// One GEMM over K = 32*KB for the tile's NSUB*16 rows (rowq/rowd: this
+// thread's staging row) against the wave's 16 weight rows (tile lanes
+// tlb..tlb+15 of the weight tile wtile, scales stile), accumulating into acc.
+template <int QT, int SC, int NSUB>
+__device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq, const float* rowd, int KB,
+                                        const char* wtile, const uint16_t* stile, int tlb, int tid,
+                                        f32x4_t (&acc)[4]) {
+  const bool stager = (tid >> 6) < NSUB;   // waves holding the tile's rows
+  const int lane = tid & 63, q = lane >> 4, r = lane & 15;
+  const int srow = tid >> 2, sblk = tid & 3;   // staging: row, block within the step
+  const int tl = tlb + r;
+  const uint16_t* sp = stile + tlb + 4 * q;    // scales of weight rows 4q..4q+3
+  const int NS = KB / kQgStage;                // steps (KB is a multiple of kQgStage)
+  QgStage sv = qg_load(rowq, rowd, sblk);
+  uint64_t wv[kQgStage];
+  u32x2_t dv[kQgStage];
+#pragma unroll
+  for (int b = 0; b < kQgStage; ++b) {
+    wv[b] = qg_wload<QT>(wtile, b, tl, q);
+    dv[b] = *reinterpret_cast<const u32x2_t*>(sp + b * 64);
+  }
+  if (stager) qg_store<QT>(smem, srow, sblk, sv);
+  __syncthreads();
+  for (int st = 0; st < NS; ++st) {
+    const int bufi = st & 1;
+    const bool more = st + 1 < NS;   // uniform
+    const int kn = (more ? st + 1 : st) * kQgStage;
+    sv = qg_load(rowq, rowd, kn + sblk);
+    uint64_t wn[kQgStage];
+    u32x2_t dn[kQgStage];
+#pragma unroll
+    for (int b = 0; b < kQgStage; ++b) {
+      wn[b] = qg_wload<QT>(wtile, kn + b, tl, q);
+      dn[b] = *reinterpret_cast<const u32x2_t*>(sp + (kn + b) * 64);
+    }
+    const unsigned char* buf = smem + bufi * kQgBufBytes;
+    f32x4_t dq[4];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+      dq[s] = *reinterpret_cast<const f32x4_t*>(buf + kQgABytes + (16 * s + r) * kQgStage * 4);
+#pragma unroll
+    for (int b = 0; b < kQgStage; ++b) {
+      qg_block<SC, NSUB>(buf, b, r, q, qg_wbytes<QT>(wv[b]), dv[b], dq, acc);
+      // keep each block's scaling next to its MFMAs: left free, the fma
+      // chains sink below all of the step's MFMAs and every MFMA result and
+      // scale of the step is live at once
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s) asm volatile("" : "+v"(acc[s]));
+    }
+    if (more && stager) qg_store<QT>(smem + (bufi ^ 1) * kQgBufBytes, srow, sblk, sv);
+#pragma unroll
+    for (int b = 0; b < kQgStage; ++b) { wv[b] = wn[b]; dv[b] = dn[b]; }
+    __syncthreads();
+  }
+}
+
+// gate_up + SiLU*mul + Q8_0 intermediate: work item (row tile, slice s = the
+// 64-lane weight tile of gate rows 32s..32s+31 and up rows I+32s..); waves 0-1
+// gate rows 0-15 / 16-31, waves 2-3 the matching up rows.  The slice's 32
+// intermediate values of a row form one Q8_0 block (pack_A_q8_0,
+// Int8-gemm/gemm_kernels.cpp:394-425).
+template <int QT, int SC>
+__global__ __launch_bounds__(kBlock) void q_gemm13_kernel(QArgs a) {
+  const SchedArgs& c = a.c;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = c.H, I = c.I, S = I / 32, KB = H / 32;
+  const int ti = blockIdx.x / S, sl = blockIdx.x - ti * S;
+  if (ti >= *c.rg.ntiles) return;   // uniform
+  const int4 tlv = reinterpret_cast<const int4*>(c.rg.tiles)[ti];
+  const int e = tlv.x, row0 = tlv.y, rows = tlv.z, nsub = (rows + 15) >> 4;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  const int srow = tid >> 2;
+  const int spair = c.rg.tok[row0 + min(srow, rows - 1)];
+  const int tok = spair / c.K;
+  float* actt = reinterpret_cast<float*>(smem + 2 * kQgBufBytes);   // [64 rows][kQgActStride]
+  int* pairs = reinterpret_cast<int*>(actt + kGemmRows * kQgActStride);
+  if ((tid & 3) == 0) pairs[srow] = spair;
+  const size_t tile = (size_t)e * S + sl;
+  f32x4_t acc[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0, 0, 0, 0};
+  {
+    const int8_t* rq = a.xq + (size_t)tok * H;
+    const float* rd = a.xd + (size_t)tok * KB;
+    const char* wt = (const char*)a.w13 + tile * KB * QFmt<QT>::block_bytes;
+    const uint16_t* stl = a.w13_d + tile * KB * 64;
+    const int tlb = (wave & 1) * 16 + (wave >> 1) * 32;
+    switch (nsub) {   // uniform
+      case 1: qg_gemm<QT, SC, 1>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
+      case 2: qg_gemm<QT, SC, 2>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
+      case 3: qg_gemm<QT, SC, 3>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
+      default: qg_gemm<QT, SC, 4>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
+    }
+  }
+  // up waves hand their sums to the gate waves; acc[s] = tile row 16s + r,
+  // slice columns (wave & 1) * 16 + 4q .. +3
+  if (wave >= 2)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      *reinterpret_cast<f32x4_t*>(actt + (16 * s + r) * kQgActStride + (wave - 2) * 16 + 4 * q) = acc[s];
+  __syncthreads();
+  if (wave < 2)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      f32x4_t* p = reinterpret_cast<f32x4_t*>(actt + (16 * s + r) * kQgActStride + wave * 16 + 4 * q);
+      f32x4_t u = *p;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) u[i] = silu_mul(acc[s][i], u[i]);
+      *p = u;
+    }
+  __syncthreads();
+  // thread (row tid/4, 8 columns): amax over the row's 32 values, then q
+  {
+    const int row = tid >> 2, c8 = (tid & 3) * 8;
+    float v[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      v[k] = actt[row * kQgActStride + c8 + k];
+      const float av = __builtin_fabsf(v[k]);
+      amax = av > amax ? av : amax;
+    }
+#pragma unroll
+    for (int m = 1; m <= 2; m <<= 1) {
+      const float o = __shfl_xor(amax, m);
+      amax = o > amax ? o : amax;
+    }
+    const float d = amax / 127.0f;
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo |= (uint32_t)(uint8_t)q8_round(v[k] * id) << (8 * k);
+      hi |= (uint32_t)(uint8_t)q8_round(v[k + 4] * id) << (8 * k);
+    }
+    if (row < rows) {
+      const size_t p = (size_t)pairs[row];
+      *reinterpret_cast<u32x2_t*>(a.act_q + p * I + 32 * sl + c8) = u32x2_t{lo, hi};
+      if (c8 == 0) a.act_d[p * S + sl] = d;
+    }
+  }
+}
+
+// down: work item (row tile, 64-row block hb of H = one weight tile); wave w
+// owns output rows 64hb + 16w..+15.  eout[pair] gets the fp32 sums (the combine
+// kernel follows).
+template <int QT, int SC>
+__global__ __launch_bounds__(kBlock) void q_gemm2_kernel(QArgs a) {
+  const SchedArgs& c = a.c;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = c.H, I = c.I, HB = H / 64, KB2 = I / 32;
+  const int ti = blockIdx.x / HB, hb = blockIdx.x - ti * HB;
+  if (ti >= *c.rg.ntiles) return;   // uniform
+  const int4 tlv = reinterpret_cast<const int4*>(c.rg.tiles)[ti];
+  const int e = tlv.x, row0 = tlv.y, rows = tlv.z, nsub = (rows + 15) >> 4;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  const int srow = tid >> 2;
+  const int spair = c.rg.tok[row0 + min(srow, rows - 1)];
+  int* pairs = reinterpret_cast<int*>(smem + 2 * kQgBufBytes + kGemmRows * kQgActStride * 4);
+  if ((tid & 3) == 0) pairs[srow] = spair;
+  const size_t tile = (size_t)e * HB + hb;
+  f32x4_t acc[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0, 0, 0, 0};
+  {
+    const int8_t* rq = a.act_q + (size_t)spair * I;
+    const float* rd = a.act_d + (size_t)spair * KB2;
+    const char* wt = (const char*)a.w2 + tile * KB2 * QFmt<QT>::block_bytes;
+    const uint16_t* stl = a.w2_d + tile * KB2 * 64;
+    switch (nsub) {   // uniform
+      case 1: qg_gemm<QT, SC, 1>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
+      case 2: qg_gemm<QT, SC, 2>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
+      case 3: qg_gemm<QT, SC, 3>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
+      default: qg_gemm<QT, SC, 4>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
+    }
+  }
+  // acc[s] = tile row 16s + r, output rows 64hb + 16 * wave + 4q .. +3
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int row = 16 * s + r;
+    if (s < nsub && row < rows)
+      *reinterpret_cast<f32x4_t*>(c.eout + (size_t)pairs[row] * H + 64 * hb + 16 * wave + 4 * q) = acc[s];
+  }
+}
+
+template <int QT, int SC>
+static hipError_t launch_qg_t(const QArgs& a, int tiles_max, hipStream_t st) {
+  hipLaunchKernelGGL((q_gemm13_kernel<QT, SC>), dim3(tiles_max * (a.c.I / 32)), dim3(kBlock), kQgLds, st, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((q_gemm2_kernel<QT, SC>), dim3(tiles_max * (a.c.H / 64)), dim3(kBlock), kQgLds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_qint_gemm(const QArgs& a, int qt, int sc, int tiles_max, hipStream_t st) {
+  if (qt == 0) return sc == 1 ? launch_qg_t<0, 1>(a, tiles_max, st) : launch_qg_t<0, 0>(a, tiles_max, st);
+  return sc == 1 ? launch_qg_t<1, 1>(a, tiles_max, st) : launch_qg_t<1, 0>(a, tiles_max, st);
+}
+
 // ---------------------------------------------------------------- weights
 // Tile coordinates of wire row `row` of projection proj (0 gate_up [2I rows],
 // 1 down [H rows]).

@@ -27,6 +27,10 @@ HIP_SOURCES = ["capi.hip", "common_kernels.hip", "w4a16.hip", "qint.hip"]
 # Packed-FP32 instructions are disabled for all device code (only scalar /
 # float2 source is written; the compiler must not form v_pk_* fp32 ops).
 NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Per-file device flags.  The int8 grouped GEMMs read every MFMA result with
+# VALU ops (the per-block fp32 scaling); the VGPR form of the MFMA saves a
+# v_accvgpr_read per element.
+FILE_FLAGS = {"qint.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd):
@@ -39,13 +43,25 @@ def _run(cmd):
 
 
 def build_lib(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    from concurrent.futures import ThreadPoolExecutor
+    srcs = [s for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    objdir = os.path.join(PKG_DIR, "_obj")
+    os.makedirs(objdir, exist_ok=True)
+
+    def compile_one(src):
+        obj = os.path.join(objdir, src.replace(".hip", ".o"))
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-c",
+               "-fvisibility=hidden", f"-I{INCLUDE}", f"-I{CSRC}", *NO_PK_FP32,
+               *FILE_FLAGS.get(src, []), os.path.join(CSRC, src), "-o", obj]
+        return obj, _run(cmd)
+
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        results = list(ex.map(compile_one, srcs))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-           "-fvisibility=hidden", f"-I{INCLUDE}", f"-I{CSRC}", *NO_PK_FP32, *srcs, "-o", tmp]
-    out = _run(cmd)
-    if verbose and out.strip():
-        print(out)
+    out = _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for o, _ in results], "-o", tmp])
+    text = "\n".join(t for _, t in results if t.strip()) + out
+    if verbose and text.strip():
+        print(text)
     os.replace(tmp, LIB)
     return LIB
 

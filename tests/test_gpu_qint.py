@@ -5,7 +5,9 @@ Int8-gemm/q8_gemm.cpp:276-646) against the oracle on identical inputs.
   device routine the fused kernels use), Q8_0 and Q4_0, both projections;
 * the fused layer: fp32 sums differ from the oracle only by the wave-split
   summation order, so outputs agree to max-rel-err <= 1e-2 (observed ~1e-3,
-  dominated by rare intermediate Q8_0 rounding flips);
+  dominated by rare intermediate Q8_0 rounding flips); above 64 routed pairs
+  the int8-MFMA grouped GEMMs run instead (k blocks summed in the reference's
+  order), covered here by the (16, 10) and (200, 8) cases and the tile test;
 * online Q8_0 weight quantization (quantize_and_store_expert) gives the same
   bytes as the oracle's quantize_weight_only restatement (checked through
   block dots) and the same layer output as the wire-format loader."""
@@ -85,6 +87,27 @@ def test_forward_dtypes_and_invalid_ids(cuda, qt):
     ids[1, :] = E + 3          # no valid id -> zeros
     ids[2, :] = 5              # one expert eight times
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(5)).to(torch.float16)
+    y = _run(h, x, ids, tw, cuda)
+    assert y.dtype == torch.float16
+    assert torch.all(y[1] == 0)
+    assert max_rel_err(y, _oracle(qt, x, ids, tw, w, E, I)) <= TOL
+
+
+@pytest.mark.parametrize("qt", [0, 1])
+def test_gemm_path_tiles_and_invalid_ids(cuda, qt):
+    """Grouped-GEMM path: an expert with 64 + 64 + 2 rows (two full row tiles
+    and a ragged one), one with 65, ids outside [0, E), fp16 activations and
+    bf16 scales."""
+    E, H, I, T, K = 8, 384, 256, 130, 8
+    w = _weights(qt, E, H, I, seed=30 + qt, sdt=torch.bfloat16)
+    h = _handle(qt, E, H, I, w, True, cuda)
+    ids, tw = topk_routing(T, E, K, seed=31)
+    ids = ids.clone()
+    ids[:, 0] = 3                        # expert 3 in every token: 130 rows
+    ids[:65, 1] = 6                      # expert 6 in 65 tokens (duplicates allowed)
+    ids[0, 2] = -1
+    ids[1, :] = E + 3                    # no valid id -> zeros
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(32)).to(torch.float16)
     y = _run(h, x, ids, tw, cuda)
     assert y.dtype == torch.float16
     assert torch.all(y[1] == 0)
