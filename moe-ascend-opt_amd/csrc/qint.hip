@@ -11,17 +11,19 @@
 // the four waves of a workgroup split the k blocks and their fp32 partial
 // sums are added in wave order.
 //
-// Device weight layout (lane-per-row tiles of 64 rows, one 32-element block
-// per step):
-//   gate_up: [E][I/32 slices][H/32 blocks][chunk][64 lanes][16 B]; lane r<32
-//            is gate row 32s+r, lane r>=32 is up row I+32s+r-32, so SiLU*mul
-//            pairs lanes r and r+32 and one slice yields one Q8_0 block of
-//            the intermediate.
-//   down:    [E][H/64][I/32 blocks][chunk][64 lanes][16 B]; lane r = row 64hb+r
-//   Q8_0: 2 chunks (bytes 0-15, 16-31 of the row's block); Q4_0: 1 chunk of
-//   4 words, word d holding elements 8d+m (low nibble of byte m) and 8d+4+m
+// Device weight layout: tiles of 64 weight rows ("lanes") x all K blocks.
+//   gate_up: [E][I/32 slices] tiles; lane r<32 is gate row 32s+r, lane r>=32
+//            is up row I+32s+r-32, so SiLU*mul pairs lanes r and r+32 and one
+//            slice yields one Q8_0 block of the intermediate.
+//   down:    [E][H/64] tiles; lane r = row 64hb+r.
+//   A row's block splits into four quarters q of 8 elements: Q8_0 8 bytes,
+//   Q4_0 one word holding elements 8q+m (low nibble of byte m) and 8q+4+m
 //   (high nibble), so (w & 0x0F0F0F0F) and (w >> 4 & 0x0F0F0F0F) line up with
-//   activation dwords 2d and 2d+1.
+//   activation dwords 2q and 2q+1.  Inside a tile, blocks go in groups of 4
+//   along K (the last group may hold fewer, G) and a group is stored
+//   [lane][quarter][block in group][quarter bytes] (QLay): a lane-per-row
+//   reader takes the row's whole group, the grouped GEMM one 16-byte (Q4_0)
+//   or 32-byte (Q8_0) run per lane and group.
 //   scales: [tile][block][64 lanes] (fp16 or bf16 bits).
 #pragma clang fp contract(off)
 #include "mi_moe_device.hpp"
@@ -35,6 +37,36 @@ struct QFmt {
   static constexpr int chunks = QT == 0 ? 2 : 1;
   static constexpr int block_bytes = chunks * 64 * 16;  // one (tile, block)
 };
+
+// Byte offset inside a tile of (block kb, lane, quarter q); WB bytes per quarter.
+template <int QT>
+struct QLay {
+  static constexpr int WB = QT == 0 ? 8 : 4;
+  __host__ __device__ static size_t off(int KB, int kb, int lane, int q) {
+    const int g0 = kb & ~3, G = KB - g0 < 4 ? KB - g0 : 4, b = kb - g0;
+    return (size_t)g0 * QFmt<QT>::block_bytes + (size_t)lane * (4 * WB * G) + q * (WB * G) + b * WB;
+  }
+};
+
+// One block of one lane as the legacy 16-byte chunks: w0 = quarters 0-3 (Q4_0)
+// or 0-1 (Q8_0), w1 = Q8_0 quarters 2-3.
+template <int QT>
+__device__ __forceinline__ void load_block(const char* wtile, int KB, int kb, int lane, u32x4_t& w0,
+                                           u32x4_t& w1) {
+  if constexpr (QT == 1) {
+    uint32_t v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const uint32_t*>(wtile + QLay<1>::off(KB, kb, lane, q));
+    w0 = u32x4_t{v[0], v[1], v[2], v[3]};
+    w1 = u32x4_t{0, 0, 0, 0};
+  } else {
+    u32x2_t v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const u32x2_t*>(wtile + QLay<0>::off(KB, kb, lane, q));
+    w0 = u32x4_t{v[0].x, v[0].y, v[1].x, v[1].y};
+    w1 = u32x4_t{v[2].x, v[2].y, v[3].x, v[3].y};
+  }
+}
 
 template <int QT>
 __device__ __forceinline__ void unpack_w(const u32x4_t w0, const u32x4_t w1, int (&wd)[8]) {
@@ -94,17 +126,14 @@ __device__ __forceinline__ float quant_block_q8_0(const float (&v)[32], int8_t* 
 }
 
 // Dot of this lane's weight row against the staged activations for k blocks
-// [kb0, kb1), accumulating into acc[c] for the cntp staged tokens.
+// [kb0, kb1), accumulating into acc[c] for the cntp staged tokens.  Whole
+// layout groups are read; blocks of a group outside the range are skipped
+// (the neighbouring wave reads the same group, mostly from the cache).
 template <int QT, int SC>
 __device__ __forceinline__ void rows_dot(const char* wtile, const uint16_t* stile, int lane, int kb0,
                                          int kb1, const int8_t* xq, const float* xd, const int* xs,
                                          int K, int KB, int cntp, float (&acc)[kQTokPerPass]) {
-  constexpr int BB = QFmt<QT>::block_bytes;
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const char* wp = wtile + (size_t)kb * BB + lane * 16;
-    const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(wp);
-    u32x4_t w1 = {0, 0, 0, 0};
-    if constexpr (QT == 0) w1 = *reinterpret_cast<const u32x4_t*>(wp + 1024);
+  auto block = [&](int kb, const u32x4_t& w0, const u32x4_t& w1) {
     const float dw = to_f32<SC>(stile[kb * 64 + lane]);
     int wd[8];
     unpack_w<QT>(w0, w1, wd);
@@ -116,6 +145,34 @@ __device__ __forceinline__ void rows_dot(const char* wtile, const uint16_t* stil
       const float t1 = (float)s * dw;
       const float t2 = t1 * xd[cc * KB + kb];
       acc[cc] = acc[cc] + t2;
+    }
+  };
+  for (int g0 = kb0 & ~3; g0 < kb1; g0 += 4) {
+    if (g0 + 4 <= KB) {
+      // the row's whole group: 4 (Q4_0) or 8 (Q8_0) 16-byte loads
+      constexpr int NV = 4 * QFmt<QT>::chunks;
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(wtile + QLay<QT>::off(KB, g0, lane, 0));
+      u32x4_t v[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) v[i] = p[i];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (g0 + b < kb0 || g0 + b >= kb1) continue;   // uniform
+        if constexpr (QT == 1) {
+          block(g0 + b, u32x4_t{v[0][b], v[1][b], v[2][b], v[3][b]}, u32x4_t{0, 0, 0, 0});
+        } else {
+          // quarter q of block b: dwords 2b, 2b+1 of the 32-byte run v[2q], v[2q+1]
+          const int h = 2 * (b & 1), i = b >> 1;
+          block(g0 + b, u32x4_t{v[i][h], v[i][h + 1], v[2 + i][h], v[2 + i][h + 1]},
+                u32x4_t{v[4 + i][h], v[4 + i][h + 1], v[6 + i][h], v[6 + i][h + 1]});
+        }
+      }
+    } else {
+      for (int kb = max(g0, kb0); kb < kb1; ++kb) {
+        u32x4_t w0, w1;
+        load_block<QT>(wtile, KB, kb, lane, w0, w1);
+        block(kb, w0, w1);
+      }
     }
   }
 }
@@ -349,48 +406,46 @@ hipError_t launch_qint(const QArgs& a, int qt, int act, int sc, int grid1, int g
 //   product 16 * round(isum * dw), and the activation scale is staged as
 //   da / 16 (powers of two: the same products and roundings).
 // The activation scales of a step are staged [row][block] (one 16-byte read
-// per sub-tile and step).
+// per sub-tile and step), the weight scales of the workgroup's 64 weight rows
+// [block][row] (wave 0 loads them, 8 bytes per lane; each wave then reads the
+// 4-row quads it needs, 16 lanes to an address).
 constexpr int kQgStage = 4;                          // 32-element blocks per step
 constexpr int kQgRowStride = kQgStage * 32 + 16;     // bytes per staged row (pad spreads the banks)
 constexpr int kQgABytes = kGemmRows * kQgRowStride;  // 9216
-constexpr int kQgBufBytes = kQgABytes + kGemmRows * kQgStage * 4;   // + scales [row][block]
+constexpr int kQgDaBytes = kGemmRows * kQgStage * 4;  // activation scales [row][block] f32
+constexpr int kQgDwBytes = kQgStage * 64 * 2;         // weight scales [block][64 rows] fp16/bf16
+constexpr int kQgBufBytes = kQgABytes + kQgDaBytes + kQgDwBytes;
 // LDS: [2][kQgBufBytes] | act tile [64][kQgActStride] f32 (gate_up epilogue) | pairs [64]
 constexpr int kQgActStride = 36;   // 32 columns + pad (16-byte rows, spread banks)
 constexpr size_t kQgLds = 2 * (size_t)kQgBufBytes + kGemmRows * kQgActStride * 4 + kGemmRows * 4;
 constexpr int kQgBias = 0x4B400000;      // bits of 1.5 * 2^23
 constexpr float kQgBiasF = 12582912.0f;  // 1.5 * 2^23
 
-struct QgStage { u32x4_t v[2]; float d; };
+// one thread's share of a step's staging: a 32-byte block of its row and the
+// block's scale; in wave 0 also 4 weight scales (block lane / 16, rows
+// 4 * (lane % 16) .. +3)
+struct QgStage { u32x4_t v[2]; float d; u32x2_t dw; };
 
-// this thread's 32-byte block of its row (one of kQgStage blocks of the step)
-__device__ __forceinline__ QgStage qg_load(const int8_t* rowq, const float* rowd, int kb) {
+__device__ __forceinline__ QgStage qg_load(const int8_t* rowq, const float* rowd, int kb0, int sblk,
+                                           const uint16_t* stile, bool w0, int lane) {
   QgStage s;
-  const u32x4_t* p = reinterpret_cast<const u32x4_t*>(rowq + 32 * kb);
+  const u32x4_t* p = reinterpret_cast<const u32x4_t*>(rowq + 32 * (kb0 + sblk));
   s.v[0] = p[0];
   s.v[1] = p[1];
-  s.d = rowd[kb];
+  s.d = rowd[kb0 + sblk];
+  if (w0) s.dw = *reinterpret_cast<const u32x2_t*>(stile + (kb0 + (lane >> 4)) * 64 + 4 * (lane & 15));
   return s;
 }
 
 template <int QT>
-__device__ __forceinline__ void qg_store(unsigned char* buf, int srow, int sblk, const QgStage& s) {
+__device__ __forceinline__ void qg_store(unsigned char* buf, int srow, int sblk, const QgStage& s, bool w0,
+                                         int lane) {
   *reinterpret_cast<u32x4_t*>(buf + srow * kQgRowStride + 32 * sblk) = s.v[0];
   *reinterpret_cast<u32x4_t*>(buf + srow * kQgRowStride + 32 * sblk + 16) = s.v[1];
   reinterpret_cast<float*>(buf + kQgABytes)[srow * kQgStage + sblk] = QT == 1 ? s.d * 0.0625f : s.d;
+  if (w0) *reinterpret_cast<u32x2_t*>(buf + kQgABytes + kQgDaBytes + (lane >> 4) * 128 + 8 * (lane & 15)) = s.dw;
 }
 
-// The lane's 8 weight bytes (k = 8q..8q+7 of the block) of tile lane `tl` for
-// block kb: Q8_0 from the chunk of bytes 16*(q/2).., Q4_0 word q (elements
-// 8q+m in the low nibble of byte m, 8q+4+m in the high one).
-template <int QT>
-__device__ __forceinline__ uint64_t qg_wload(const char* tile, int kb, int tl, int q) {
-  const char* blk = tile + (size_t)kb * QFmt<QT>::block_bytes;
-  if constexpr (QT == 0) {
-    return *reinterpret_cast<const uint64_t*>(blk + (q >> 1) * 1024 + tl * 16 + 8 * (q & 1));
-  } else {
-    return *reinterpret_cast<const uint32_t*>(blk + tl * 16 + 4 * q);
-  }
-}
 // MFMA B bytes: Q8_0 as stored; Q4_0 as 16 * (n - 8), elements 8q..8q+7
 template <int QT>
 __device__ __forceinline__ long qg_wbytes(uint64_t w) {
@@ -432,10 +487,41 @@ __device__ __forceinline__ void qg_block(const unsigned char* buf, int sblk, int
   }
 }
 
+// The wave's weights of one step (kQgStage = 4 blocks, one layout group):
+// lane 16q + r takes quarter q of weight row tl = tlb + r for the 4 blocks,
+// one contiguous run (Q4_0 16 bytes, Q8_0 32 bytes).
+static_assert(kQgStage == 4, "a step is one 4-block layout group");
+template <int QT>
+struct QgWSet {
+  uint64_t w[kQgStage];
+  __device__ __forceinline__ void load(const char* wtile, int KB, int kb0, int tl, int q) {
+    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(wtile + QLay<QT>::off(KB, kb0, tl, q));
+    if constexpr (QT == 1) {
+      const u32x4_t v = p[0];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w[b] = v[b];
+    } else {
+      const u32x4_t v0 = p[0], v1 = p[1];
+      w[0] = (uint64_t)v0.x | ((uint64_t)v0.y << 32);
+      w[1] = (uint64_t)v0.z | ((uint64_t)v0.w << 32);
+      w[2] = (uint64_t)v1.x | ((uint64_t)v1.y << 32);
+      w[3] = (uint64_t)v1.z | ((uint64_t)v1.w << 32);
+    }
+  }
+};
+
 // One GEMM over K = 32*KB for the tile's NSUB*16 rows (rowq/rowd: this
 // thread's staging row) against the wave's 16 weight rows (tile lanes
 // tlb..tlb+15 of the weight tile wtile, scales stile), accumulating into acc.
-template <int QT, int SC, int NSUB>
+// Loads run D steps ahead through a ring of register sets, one batch per
+// step: the weights of step st + D and the activation rows of step
+// st + 1 + D (staged into LDS, double-buffered, one step before use).  The
+// memory counter drains in issue order, so a batch holds both kinds: waiting
+// for the rows to stage never waits for weights issued after them.  The
+// kernels use D = 1: on MI355X rings of 2 and 3 steps measured slower at
+// every tile size (small tiles are bound by load-instruction issue, not by
+// the latency a deeper ring hides).
+template <int QT, int SC, int NSUB, int D>
 __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq, const float* rowd, int KB,
                                         const char* wtile, const uint16_t* stile, int tlb, int tid,
                                         f32x4_t (&acc)[4]) {
@@ -443,48 +529,49 @@ __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq,
   const int lane = tid & 63, q = lane >> 4, r = lane & 15;
   const int srow = tid >> 2, sblk = tid & 3;   // staging: row, block within the step
   const int tl = tlb + r;
-  const uint16_t* sp = stile + tlb + 4 * q;    // scales of weight rows 4q..4q+3
+  const bool w0 = (tid >> 6) == 0;             // wave 0 also stages the weight scales
   const int NS = KB / kQgStage;                // steps (KB is a multiple of kQgStage)
-  QgStage sv = qg_load(rowq, rowd, sblk);
-  uint64_t wv[kQgStage];
-  u32x2_t dv[kQgStage];
+  // ring: weights of step j in ws[j % D], staging of step j in sv[j % D]
+  QgWSet<QT> ws[D];
+  QgStage sv[D];
 #pragma unroll
-  for (int b = 0; b < kQgStage; ++b) {
-    wv[b] = qg_wload<QT>(wtile, b, tl, q);
-    dv[b] = *reinterpret_cast<const u32x2_t*>(sp + b * 64);
+  for (int u = 0; u < D; ++u) {
+    ws[u].load(wtile, KB, min(u, NS - 1) * kQgStage, tl, q);
+    sv[u] = qg_load(rowq, rowd, min(u, NS - 1) * kQgStage, sblk, stile, w0, lane);
   }
-  if (stager) qg_store<QT>(smem, srow, sblk, sv);
+  if (stager) qg_store<QT>(smem, srow, sblk, sv[0], w0, lane);
+  sv[0] = qg_load(rowq, rowd, min(D, NS - 1) * kQgStage, sblk, stile, w0, lane);
   __syncthreads();
-  for (int st = 0; st < NS; ++st) {
-    const int bufi = st & 1;
-    const bool more = st + 1 < NS;   // uniform
-    const int kn = (more ? st + 1 : st) * kQgStage;
-    sv = qg_load(rowq, rowd, kn + sblk);
-    uint64_t wn[kQgStage];
-    u32x2_t dn[kQgStage];
+  for (int st0 = 0; st0 < NS; st0 += D) {
 #pragma unroll
-    for (int b = 0; b < kQgStage; ++b) {
-      wn[b] = qg_wload<QT>(wtile, kn + b, tl, q);
-      dn[b] = *reinterpret_cast<const u32x2_t*>(sp + (kn + b) * 64);
+    for (int u = 0; u < D; ++u) {
+      const int st = st0 + u;
+      const bool live = st < NS;       // uniform
+      const bool more = st + 1 < NS;   // uniform
+      const unsigned char* buf = smem + (st & 1) * kQgBufBytes;
+      if (live) {
+        f32x4_t dq[4];
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s)
+          dq[s] = *reinterpret_cast<const f32x4_t*>(buf + kQgABytes + (16 * s + r) * kQgStage * 4);
+#pragma unroll
+        for (int b = 0; b < kQgStage; ++b) {
+          const u32x2_t raw =
+              *reinterpret_cast<const u32x2_t*>(buf + kQgABytes + kQgDaBytes + b * 128 + (tlb + 4 * q) * 2);
+          qg_block<SC, NSUB>(buf, b, r, q, qg_wbytes<QT>(ws[u].w[b]), raw, dq, acc);
+          // keep each block's scaling next to its MFMAs: left free, the fma
+          // chains sink below all of the step's MFMAs and every MFMA result and
+          // scale of the step is live at once
+#pragma unroll
+          for (int s = 0; s < NSUB; ++s) asm volatile("" : "+v"(acc[s]));
+        }
+      }
+      const int un = (u + 1) % D;   // ring slot of step st + 1 (constant once unrolled)
+      ws[u].load(wtile, KB, min(st + D, NS - 1) * kQgStage, tl, q);
+      if (more && stager) qg_store<QT>(smem + ((st & 1) ^ 1) * kQgBufBytes, srow, sblk, sv[un], w0, lane);
+      sv[un] = qg_load(rowq, rowd, min(st + 1 + D, NS - 1) * kQgStage, sblk, stile, w0, lane);
+      __syncthreads();
     }
-    const unsigned char* buf = smem + bufi * kQgBufBytes;
-    f32x4_t dq[4];
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s)
-      dq[s] = *reinterpret_cast<const f32x4_t*>(buf + kQgABytes + (16 * s + r) * kQgStage * 4);
-#pragma unroll
-    for (int b = 0; b < kQgStage; ++b) {
-      qg_block<SC, NSUB>(buf, b, r, q, qg_wbytes<QT>(wv[b]), dv[b], dq, acc);
-      // keep each block's scaling next to its MFMAs: left free, the fma
-      // chains sink below all of the step's MFMAs and every MFMA result and
-      // scale of the step is live at once
-#pragma unroll
-      for (int s = 0; s < NSUB; ++s) asm volatile("" : "+v"(acc[s]));
-    }
-    if (more && stager) qg_store<QT>(smem + (bufi ^ 1) * kQgBufBytes, srow, sblk, sv);
-#pragma unroll
-    for (int b = 0; b < kQgStage; ++b) { wv[b] = wn[b]; dv[b] = dn[b]; }
-    __syncthreads();
   }
 }
 
@@ -520,10 +607,10 @@ __global__ __launch_bounds__(kBlock) void q_gemm13_kernel(QArgs a) {
     const uint16_t* stl = a.w13_d + tile * KB * 64;
     const int tlb = (wave & 1) * 16 + (wave >> 1) * 32;
     switch (nsub) {   // uniform
-      case 1: qg_gemm<QT, SC, 1>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
-      case 2: qg_gemm<QT, SC, 2>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
-      case 3: qg_gemm<QT, SC, 3>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
-      default: qg_gemm<QT, SC, 4>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
+      case 1: qg_gemm<QT, SC, 1, 1>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
+      case 2: qg_gemm<QT, SC, 2, 1>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
+      case 3: qg_gemm<QT, SC, 3, 1>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
+      default: qg_gemm<QT, SC, 4, 1>(smem, rq, rd, KB, wt, stl, tlb, tid, acc); break;
     }
   }
   // up waves hand their sums to the gate waves; acc[s] = tile row 16s + r,
@@ -602,10 +689,10 @@ __global__ __launch_bounds__(kBlock) void q_gemm2_kernel(QArgs a) {
     const char* wt = (const char*)a.w2 + tile * KB2 * QFmt<QT>::block_bytes;
     const uint16_t* stl = a.w2_d + tile * KB2 * 64;
     switch (nsub) {   // uniform
-      case 1: qg_gemm<QT, SC, 1>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
-      case 2: qg_gemm<QT, SC, 2>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
-      case 3: qg_gemm<QT, SC, 3>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
-      default: qg_gemm<QT, SC, 4>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
+      case 1: qg_gemm<QT, SC, 1, 1>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
+      case 2: qg_gemm<QT, SC, 2, 1>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
+      case 3: qg_gemm<QT, SC, 3, 1>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
+      default: qg_gemm<QT, SC, 4, 1>(smem, rq, rd, KB2, wt, stl, 16 * wave, tid, acc); break;
     }
   }
   // acc[s] = tile row 16s + r, output rows 64hb + 16 * wave + 4q .. +3
@@ -675,15 +762,18 @@ __global__ void q_repack_kernel(const void* __restrict__ qs, const uint16_t* __r
     row_to_tile(proj, row, I, ti, lane);
     const int tiles_per_e = proj == 0 ? I / 32 : rows / 64;
     const size_t tile = (size_t)e * tiles_per_e + ti;
-    char* dst = (char*)wdst + (tile * KB + kb) * QFmt<QT>::block_bytes + lane * 16;
+    char* dst = (char*)wdst + tile * KB * QFmt<QT>::block_bytes;
     if constexpr (QT == 0) {
       const u32x4_t* src = reinterpret_cast<const u32x4_t*>((const int8_t*)qs + er * K + kb * 32);
-      *reinterpret_cast<u32x4_t*>(dst) = src[0];
-      *reinterpret_cast<u32x4_t*>(dst + 1024) = src[1];
+      const u32x4_t a = src[0], b = src[1];
+      const u32x2_t qv[4] = {{a.x, a.y}, {a.z, a.w}, {b.x, b.y}, {b.z, b.w}};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x2_t*>(dst + QLay<0>::off(KB, kb, lane, q)) = qv[q];
     } else {
       const u32x4_t src = *reinterpret_cast<const u32x4_t*>((const uint32_t*)qs + er * (K / 8) + kb * 4);
-      *reinterpret_cast<u32x4_t*>(dst) =
-          u32x4_t{q4_to_dev(src.x), q4_to_dev(src.y), q4_to_dev(src.z), q4_to_dev(src.w)};
+      const uint32_t qv[4] = {src.x, src.y, src.z, src.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(dst + QLay<1>::off(KB, kb, lane, q)) = q4_to_dev(qv[q]);
     }
     ddst[(tile * KB + kb) * 64 + lane] = d[er * KB + kb];
   }
@@ -729,9 +819,10 @@ __global__ void q8_online_quant_kernel(const void* __restrict__ w, int N, int K,
     int8_t q[32];
     int qs;
     const float d = quant_block_q8_0(v, q, &qs);
-    char* dst = (char*)wdst + (tile * KB + kb) * QFmt<0>::block_bytes + lane * 16;
-    *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(q);
-    *reinterpret_cast<u32x4_t*>(dst + 1024) = *reinterpret_cast<const u32x4_t*>(q + 16);
+    char* dst = (char*)wdst + tile * KB * QFmt<0>::block_bytes;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+      *reinterpret_cast<u32x2_t*>(dst + QLay<0>::off(KB, kb, lane, qq)) = *reinterpret_cast<const u32x2_t*>(q + 8 * qq);
     ddst[(tile * KB + kb) * 64 + lane] = f32_to_f16(d);
   }
 }
@@ -768,10 +859,8 @@ __global__ void q_block_dots_kernel(const void* __restrict__ wbase, const int8_t
     int ti, lane;
     row_to_tile(proj, n, I, ti, lane);
     const size_t tile = (size_t)e * tiles_per_e + ti;
-    const char* wp = (const char*)wbase + (tile * KB + kb) * QFmt<QT>::block_bytes + lane * 16;
-    const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(wp);
-    u32x4_t w1 = {0, 0, 0, 0};
-    if constexpr (QT == 0) w1 = *reinterpret_cast<const u32x4_t*>(wp + 1024);
+    u32x4_t w0, w1;
+    load_block<QT>((const char*)wbase + tile * KB * QFmt<QT>::block_bytes, KB, kb, lane, w0, w1);
     int wd[8];
     unpack_w<QT>(w0, w1, wd);
     const int* xv = reinterpret_cast<const int*>(a_qs + (size_t)m * K + kb * 32);
