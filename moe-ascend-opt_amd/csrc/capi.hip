@@ -124,6 +124,7 @@ struct mi_moe_handle {
   int64_t cap_T = 0, cap_n = 0;
   DevBuf act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U, r_tiles, r_ntiles;
   DevBuf xq, xd;   // Q8_0 activations of the grouped-GEMM path
+  DevBuf r_chunk;  // per-chunk expert counts of the multi-workgroup routing
 };
 
 namespace {
@@ -161,6 +162,7 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
   HIPCHK(h->r_tok.alloc((size_t)capn * sizeof(int32_t)));
   HIPCHK(h->r_scat.alloc((size_t)capn * sizeof(int32_t)));
   HIPCHK(h->r_tiles.alloc((size_t)gemm_tiles_max(capn, (int)h->E) * 4 * sizeof(int32_t)));
+  HIPCHK(h->r_chunk.alloc((size_t)route_chunks((int)capn) * h->E * sizeof(int32_t)));
   if (h->quant != MI_MOE_W4A16) {
     HIPCHK(h->xq.alloc((size_t)capT * h->H));
     HIPCHK(h->xd.alloc((size_t)capT * (h->H / 32) * sizeof(float)));
@@ -195,6 +197,7 @@ RouteGlobal route_view(mi_moe_handle* h) {
   rg.U = (int32_t*)h->r_U.p;
   rg.tiles = (int32_t*)h->r_tiles.p;
   rg.ntiles = (int32_t*)h->r_ntiles.p;
+  rg.chunk = (int32_t*)h->r_chunk.p;
   return rg;
 }
 
@@ -317,7 +320,7 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
   DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z,
                     &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
                     &h->r_active, &h->r_tok, &h->r_scat, &h->r_U, &h->r_tiles, &h->r_ntiles,
-                    &h->xq, &h->xd};
+                    &h->xq, &h->xd, &h->r_chunk};
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
   if (h->ev1) (void)hipEventDestroy(h->ev1);
@@ -533,13 +536,16 @@ MI_API int mi_moe_route(const int32_t* ids, int64_t T, int64_t K, int64_t E, int
     return MI_MOE_OK;
   }
   if (!ids || !token_map || !scatter) return fail(MI_MOE_EINVAL, "null pointer");
-  DevBuf active, U;
+  DevBuf active, U, chunk;
   HIPCHK(active.alloc((size_t)E * sizeof(int32_t)));
   HIPCHK(U.alloc(sizeof(int32_t)));
-  RouteGlobal rg{counts, starts, (int32_t*)active.p, token_map, scatter, (int32_t*)U.p};
+  HIPCHK(chunk.alloc((size_t)route_chunks((int)(T * K)) * E * sizeof(int32_t)));
+  RouteGlobal rg{counts, starts, (int32_t*)active.p, token_map, scatter, (int32_t*)U.p, nullptr, nullptr,
+                 (int32_t*)chunk.p};
   HIPCHK(launch_route_global(ids, (int)(T * K), (int)K, (int)E, rg, st, 1));
   HIPCHK(hipStreamSynchronize(st));
   active.release();
   U.release();
+  chunk.release();
   return MI_MOE_OK;
 }

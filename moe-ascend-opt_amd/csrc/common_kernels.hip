@@ -9,115 +9,49 @@ namespace mimoe {
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / kWave;
 
-// Global routing (one workgroup of 1024 threads): the stable counting sort of
-// preprocess_moe_routing (Int8-gemm/moe_common.cpp:146-216) for any number of
-// (t,k) pairs.  Each wave owns a contiguous segment of ids; per-wave
-// per-expert counts are prefix-summed across waves so the ranks stay in
-// (t,k) order.  With tiles_out, also the row tiles of the grouped GEMMs: per
-// active expert in ascending order, its sorted rows in chunks of kGemmRows.
-// LDS: (kRouteWaves + 1) * E ints (E <= 512).
-__global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
-    const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
-    int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out,
-    int tok_div, int32_t* tiles_out, int32_t* ntiles_out) {
-  extern __shared__ int lds[];
-  int* counts = lds;            // [E]
-  int* cw = lds + E;            // [kRouteWaves][E]
-  __shared__ int s_U;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int e = tid; e < E; e += kRouteThreads) counts[e] = 0;
-  for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) cw[i] = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += kRouteThreads) {
-    const int e = ids[i];
-    if ((unsigned)e < (unsigned)E) atomicAdd(&counts[e], 1);
+// Routing: the stable counting sort of preprocess_moe_routing
+// (Int8-gemm/moe_common.cpp:146-216) for any number of (t,k) pairs, plus, with
+// tiles_out, the row tiles of the grouped GEMMs: per active expert in
+// ascending order, its sorted rows in chunks of kGemmRows.
+//   n <= kRouteMultiMin: one workgroup (route_global_kernel);
+//   above: route_count_kernel (a histogram per chunk of kRouteChunk ids),
+//   route_scan_kernel (totals, starts, tiles, and per-chunk base offsets),
+//   route_scatter_kernel (stable ranks per chunk).
+// Inside a workgroup each wave owns a contiguous segment of ids; per-wave
+// per-expert counts are prefix-summed across waves (and, across workgroups,
+// seeded with the chunk's base offsets), so ranks stay in (t,k) order.
+
+// Lanes of this wave holding the same valid expert id as this lane.
+__device__ __forceinline__ uint64_t route_match(int e, bool valid, int nbits) {
+  uint64_t m = __ballot(valid);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const uint64_t bb = __ballot(valid && ((e >> bit) & 1));
+    m &= ((e >> bit) & 1) ? bb : ~bb;
   }
-  __syncthreads();
-  if (tid < kWave) {
-    const int per = (E + kWave - 1) / kWave;
-    const int base = lane * per;
-    int s = 0, a = 0;
-    for (int i = 0; i < per; ++i) {
-      const int e = base + i;
-      if (e < E) { const int c = counts[e]; s += c; a += (c > 0); }
-    }
-    int tl = 0;   // row tiles of this lane's experts
-    for (int i = 0; i < per; ++i) {
-      const int e = base + i;
-      if (e < E) tl += (counts[e] + kGemmRows - 1) / kGemmRows;
-    }
-    int sinc = s, ainc = a, tinc = tl;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int v = __shfl_up(sinc, off);
-      const int w = __shfl_up(ainc, off);
-      const int u = __shfl_up(tinc, off);
-      if (lane >= off) { sinc += v; ainc += w; tinc += u; }
-    }
-    int sx = sinc - s, ax = ainc - a, tx = tinc - tl;
-    for (int i = 0; i < per; ++i) {
-      const int e = base + i;
-      if (e < E) {
-        const int c = counts[e];
-        counts_out[e] = c;
-        starts_out[e] = sx;
-        counts[e] = sx;  // counts[] now holds starts
-        if (c > 0) active_out[ax++] = e;
-        if (tiles_out)
-          for (int r0 = 0; r0 < c; r0 += kGemmRows, ++tx) {
-            tiles_out[4 * tx + 0] = e;
-            tiles_out[4 * tx + 1] = sx + r0;
-            tiles_out[4 * tx + 2] = min(kGemmRows, c - r0);
-            tiles_out[4 * tx + 3] = 0;
-          }
-        sx += c;
-      }
-    }
-    if (lane == kWave - 1) {
-      starts_out[E] = sinc; *U_out = ainc; s_U = ainc;
-      if (ntiles_out) *ntiles_out = tinc;
-    }
-  }
-  __syncthreads();
-  int nbits = 0;
-  while ((1 << nbits) < E) ++nbits;
-  const int seg = ((n + kRouteWaves - 1) / kRouteWaves + kWave - 1) / kWave * kWave;
-  const int lo = wave * seg, hi = min(n, lo + seg);
-  int* mine = cw + wave * E;
-  // pass A: per-wave counts
+  return m;
+}
+
+// One wave: per-expert counts of ids[lo, hi) added into mine[E].
+__device__ void route_wave_count(const int32_t* __restrict__ ids, int lo, int hi, int E, int nbits,
+                                 int lane, int* mine) {
   for (int b0 = lo; b0 < hi; b0 += kWave) {
     const int i = b0 + lane;
     const int e = (i < hi) ? ids[i] : -1;
     const bool valid = (i < hi) && ((unsigned)e < (unsigned)E);
-    uint64_t m = __ballot(valid);
-    for (int bit = 0; bit < nbits; ++bit) {
-      const uint64_t bb = __ballot(valid && ((e >> bit) & 1));
-      m &= ((e >> bit) & 1) ? bb : ~bb;
-    }
+    const uint64_t m = route_match(e, valid, nbits);
     if (valid && __ffsll((long long)m) - 1 == lane) mine[e] += __popcll(m);
     __builtin_amdgcn_wave_barrier();
   }
-  __syncthreads();
-  // prefix over waves, seeded with starts
-  for (int e = tid; e < E; e += kRouteThreads) {
-    int run = counts[e];
-    for (int w = 0; w < kRouteWaves; ++w) {
-      const int c = cw[w * E + e];
-      cw[w * E + e] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
-  // pass B: ranks
+}
+
+// One wave: ranks of ids[lo, hi) from the running bases mine[E].
+__device__ void route_wave_rank(const int32_t* __restrict__ ids, int lo, int hi, int K, int E, int nbits,
+                                int lane, int* mine, int32_t* tok, int32_t* scat, int tok_div) {
   for (int b0 = lo; b0 < hi; b0 += kWave) {
     const int i = b0 + lane;
     const int e = (i < hi) ? ids[i] : -1;
     const bool valid = (i < hi) && ((unsigned)e < (unsigned)E);
-    uint64_t m = __ballot(valid);
-    for (int bit = 0; bit < nbits; ++bit) {
-      const uint64_t bb = __ballot(valid && ((e >> bit) & 1));
-      m &= ((e >> bit) & 1) ? bb : ~bb;
-    }
+    const uint64_t m = route_match(e, valid, nbits);
     int add = 0;
     if (valid) {
       const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
@@ -134,9 +68,186 @@ __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
   }
 }
 
+// Wave 0: per-expert totals counts[E] (LDS) -> counts_out, starts_out, the
+// active list, U and the row tiles; counts[] becomes the starts.
+__device__ void route_finish(int* counts, int E, int lane, int32_t* counts_out, int32_t* starts_out,
+                             int32_t* active_out, int32_t* U_out, int32_t* tiles_out, int32_t* ntiles_out) {
+  const int per = (E + kWave - 1) / kWave;
+  const int base = lane * per;
+  int s = 0, a = 0, tl = 0;   // rows, active experts and row tiles of this lane's experts
+  for (int i = 0; i < per; ++i) {
+    const int e = base + i;
+    if (e < E) {
+      const int c = counts[e];
+      s += c; a += (c > 0); tl += (c + kGemmRows - 1) / kGemmRows;
+    }
+  }
+  int sinc = s, ainc = a, tinc = tl;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int v = __shfl_up(sinc, off);
+    const int w = __shfl_up(ainc, off);
+    const int u = __shfl_up(tinc, off);
+    if (lane >= off) { sinc += v; ainc += w; tinc += u; }
+  }
+  int sx = sinc - s, ax = ainc - a, tx = tinc - tl;
+  for (int i = 0; i < per; ++i) {
+    const int e = base + i;
+    if (e < E) {
+      const int c = counts[e];
+      counts_out[e] = c;
+      starts_out[e] = sx;
+      counts[e] = sx;
+      if (c > 0) active_out[ax++] = e;
+      if (tiles_out)
+        for (int r0 = 0; r0 < c; r0 += kGemmRows, ++tx) {
+          tiles_out[4 * tx + 0] = e;
+          tiles_out[4 * tx + 1] = sx + r0;
+          tiles_out[4 * tx + 2] = min(kGemmRows, c - r0);
+          tiles_out[4 * tx + 3] = 0;
+        }
+      sx += c;
+    }
+  }
+  if (lane == kWave - 1) {
+    starts_out[E] = sinc;
+    *U_out = ainc;
+    if (ntiles_out) *ntiles_out = tinc;
+  }
+}
+
+__device__ __forceinline__ int route_bits(int E) {
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  return nbits;
+}
+
+// One workgroup for all n ids.  LDS: (kRouteWaves + 1) * E ints (E <= 512).
+__global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
+    const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
+    int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out,
+    int tok_div, int32_t* tiles_out, int32_t* ntiles_out) {
+  extern __shared__ int lds[];
+  int* counts = lds;            // [E]
+  int* cw = lds + E;            // [kRouteWaves][E]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int e = tid; e < E; e += kRouteThreads) counts[e] = 0;
+  for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) cw[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += kRouteThreads) {
+    const int e = ids[i];
+    if ((unsigned)e < (unsigned)E) atomicAdd(&counts[e], 1);
+  }
+  __syncthreads();
+  if (tid < kWave) route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out);
+  __syncthreads();
+  const int nbits = route_bits(E);
+  const int seg = ((n + kRouteWaves - 1) / kRouteWaves + kWave - 1) / kWave * kWave;
+  const int lo = wave * seg, hi = min(n, lo + seg);
+  int* mine = cw + wave * E;
+  route_wave_count(ids, lo, hi, E, nbits, lane, mine);
+  __syncthreads();
+  // prefix over waves, seeded with starts
+  for (int e = tid; e < E; e += kRouteThreads) {
+    int run = counts[e];
+    for (int w = 0; w < kRouteWaves; ++w) {
+      const int c = cw[w * E + e];
+      cw[w * E + e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  route_wave_rank(ids, lo, hi, K, E, nbits, lane, mine, tok, scat, tok_div);
+}
+
+// Multi-workgroup routing, step 1: the expert histogram of one chunk of ids.
+constexpr int kRouteCountThreads = 256;
+__global__ __launch_bounds__(kRouteCountThreads) void route_count_kernel(const int32_t* __restrict__ ids, int n,
+                                                                         int E, int32_t* chunk_counts) {
+  extern __shared__ int hist[];   // [E]
+  const int tid = threadIdx.x, c = blockIdx.x;
+  for (int e = tid; e < E; e += kRouteCountThreads) hist[e] = 0;
+  __syncthreads();
+  const int lo = c * kRouteChunk, hi = min(n, lo + kRouteChunk);
+  for (int i = lo + tid; i < hi; i += kRouteCountThreads) {
+    const int e = ids[i];
+    if ((unsigned)e < (unsigned)E) atomicAdd(&hist[e], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kRouteCountThreads) chunk_counts[(size_t)c * E + e] = hist[e];
+}
+
+// Step 2 (one workgroup): totals over the C chunks, the outputs of
+// route_finish, and chunk_counts[c][e] replaced by the sorted position of
+// chunk c's first row of expert e.
+__global__ __launch_bounds__(kRouteThreads) void route_scan_kernel(int32_t* chunk_counts, int C, int E,
+                                                                   int32_t* counts_out, int32_t* starts_out,
+                                                                   int32_t* active_out, int32_t* U_out,
+                                                                   int32_t* tiles_out, int32_t* ntiles_out) {
+  extern __shared__ int counts[];   // [E]
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int e = tid; e < E; e += kRouteThreads) {
+    int s = 0;
+    for (int c = 0; c < C; ++c) s += chunk_counts[(size_t)c * E + e];
+    counts[e] = s;
+  }
+  __syncthreads();
+  if (tid < kWave) route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out);
+  __syncthreads();
+  for (int e = tid; e < E; e += kRouteThreads) {
+    int run = counts[e];
+    for (int c = 0; c < C; ++c) {
+      const int v = chunk_counts[(size_t)c * E + e];
+      chunk_counts[(size_t)c * E + e] = run;
+      run += v;
+    }
+  }
+}
+
+// Step 3: stable ranks of one chunk, each wave kRouteChunk / kRouteWaves ids.
+// LDS: kRouteWaves * E ints.
+__global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(const int32_t* __restrict__ ids, int n,
+                                                                      int K, int E, const int32_t* chunk_base,
+                                                                      int32_t* tok, int32_t* scat, int tok_div) {
+  extern __shared__ int cw[];   // [kRouteWaves][E]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = blockIdx.x;
+  for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) cw[i] = 0;
+  __syncthreads();
+  const int nbits = route_bits(E);
+  constexpr int seg = kRouteChunk / kRouteWaves;
+  const int lo = min(n, c * kRouteChunk + wave * seg), hi = min(n, lo + seg);
+  int* mine = cw + wave * E;
+  route_wave_count(ids, lo, hi, E, nbits, lane, mine);
+  __syncthreads();
+  for (int e = tid; e < E; e += kRouteThreads) {
+    int run = chunk_base[(size_t)c * E + e];
+    for (int w = 0; w < kRouteWaves; ++w) {
+      const int v = cw[w * E + e];
+      cw[w * E + e] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  route_wave_rank(ids, lo, hi, K, E, nbits, lane, mine, tok, scat, tok_div);
+}
+
 // tok_div = 0: tok[] holds pair indices t*K+k (fused kernels); 1: token ids.
 hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const RouteGlobal& rg,
                                hipStream_t st, int tok_div) {
+  if (n > kRouteMultiMin && rg.chunk) {
+    const int C = (n + kRouteChunk - 1) / kRouteChunk;
+    hipLaunchKernelGGL(route_count_kernel, dim3(C), dim3(kRouteCountThreads), (size_t)E * sizeof(int), st, ids,
+                       n, E, rg.chunk);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kRouteThreads), (size_t)E * sizeof(int), st, rg.chunk,
+                       C, E, rg.counts, rg.starts, rg.active, rg.U, rg.tiles, rg.ntiles);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(route_scatter_kernel, dim3(C), dim3(kRouteThreads), (size_t)kRouteWaves * E * sizeof(int),
+                       st, ids, n, K, E, rg.chunk, rg.tok, rg.scat, tok_div);
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)(kRouteWaves + 1) * E * sizeof(int);
   hipLaunchKernelGGL(route_global_kernel, dim3(1), dim3(kRouteThreads), lds, st, ids, n, K, E,
                      rg.counts, rg.starts, rg.active, rg.tok, rg.scat, rg.U, tok_div, rg.tiles,

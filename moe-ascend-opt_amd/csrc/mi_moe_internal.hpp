@@ -22,7 +22,14 @@ struct RouteGlobal {
   int32_t* U;        // [1]
   int32_t* tiles;    // [n/kGemmRows + E][4]: expert, first sorted row, rows (<= kGemmRows), 0; or null
   int32_t* ntiles;   // [1]
+  int32_t* chunk;    // [ceil(n / kRouteChunk)][E] scratch of the multi-workgroup routing, or null
 };
+
+// Routing: one workgroup up to kRouteMultiMin pairs, three launches over
+// chunks of kRouteChunk ids above.
+constexpr int kRouteChunk = 2048;
+constexpr int kRouteMultiMin = 4096;
+__host__ __device__ constexpr int route_chunks(int n) { return (n + kRouteChunk - 1) / kRouteChunk; }
 
 // Row tile of the grouped GEMMs of the sorted path: routed rows of one expert.
 constexpr int kGemmRows = 64;

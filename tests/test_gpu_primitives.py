@@ -21,7 +21,10 @@ def _ptr(t):
 
 @pytest.mark.parametrize("T,K,E,seed", [(1, 8, 128, 0), (8, 8, 128, 1), (128, 8, 128, 2),
                                         (4096, 8, 128, 3), (512, 8, 256, 4), (300, 10, 64, 5),
-                                        (77, 1, 16, 6), (0, 8, 128, 7)])
+                                        (77, 1, 16, 6), (0, 8, 128, 7),
+                                        # multi-workgroup routing (> 4096 pairs): ragged last
+                                        # chunk, and the largest expert count
+                                        (700, 8, 128, 8), (1100, 10, 512, 9)])
 def test_route_bit_exact(cuda, T, K, E, seed):
     rng = np.random.default_rng(seed)
     ids = rng.integers(-1, E + 1, size=(T, K)).astype(np.int32)
