@@ -407,17 +407,23 @@ hipError_t launch_qint(const QArgs& a, int qt, int act, int sc, int grid1, int g
 //   da / 16 (powers of two: the same products and roundings).
 // The activation scales of a step are staged [row][block] (one 16-byte read
 // per sub-tile and step), the weight scales of the workgroup's 64 weight rows
-// [block][row] (wave 0 loads them, 8 bytes per lane; each wave then reads the
-// 4-row quads it needs, 16 lanes to an address).
+// [block][row]: wave 0 loads them, 8 bytes per lane, and each wave reads the
+// 4-row quads it needs, 16 lanes to an address.  Tiles of 3-4 sub-tiles
+// (CONV) stage them as fp32 pairs (dw, -1.5 * 2^23 * dw), converted once by
+// wave 0, which saves each lane 8 VALU ops per block; smaller tiles stage the
+// fp16/bf16 bits and convert per lane, keeping wave 0's staging short (a
+// small tile's step is short and waits on it).
 constexpr int kQgStage = 4;                          // 32-element blocks per step
 constexpr int kQgRowStride = kQgStage * 32 + 16;     // bytes per staged row (pad spreads the banks)
 constexpr int kQgABytes = kGemmRows * kQgRowStride;  // 9216
 constexpr int kQgDaBytes = kGemmRows * kQgStage * 4;  // activation scales [row][block] f32
-constexpr int kQgDwBytes = kQgStage * 64 * 2;         // weight scales [block][64 rows] fp16/bf16
+constexpr int kQgDwBytes = kQgStage * 64 * 8;         // weight scales [block][64 rows] (dw, nb) f32 or bits
 constexpr int kQgBufBytes = kQgABytes + kQgDaBytes + kQgDwBytes;
-// LDS: [2][kQgBufBytes] | act tile [64][kQgActStride] f32 (gate_up epilogue) | pairs [64]
+// LDS: [2][kQgBufBytes] staging (after the K loop, the gate_up epilogue's act
+// tile [64][kQgActStride] f32 reuses it) | pairs [64]
 constexpr int kQgActStride = 36;   // 32 columns + pad (16-byte rows, spread banks)
-constexpr size_t kQgLds = 2 * (size_t)kQgBufBytes + kGemmRows * kQgActStride * 4 + kGemmRows * 4;
+static_assert(kGemmRows * kQgActStride * 4 <= 2 * kQgBufBytes, "act tile fits the staging buffers");
+constexpr size_t kQgLds = 2 * (size_t)kQgBufBytes + kGemmRows * 4;
 constexpr int kQgBias = 0x4B400000;      // bits of 1.5 * 2^23
 constexpr float kQgBiasF = 12582912.0f;  // 1.5 * 2^23
 
@@ -437,13 +443,21 @@ __device__ __forceinline__ QgStage qg_load(const int8_t* rowq, const float* rowd
   return s;
 }
 
-template <int QT>
+template <int QT, int SC, bool CONV>
 __device__ __forceinline__ void qg_store(unsigned char* buf, int srow, int sblk, const QgStage& s, bool w0,
                                          int lane) {
   *reinterpret_cast<u32x4_t*>(buf + srow * kQgRowStride + 32 * sblk) = s.v[0];
   *reinterpret_cast<u32x4_t*>(buf + srow * kQgRowStride + 32 * sblk + 16) = s.v[1];
   reinterpret_cast<float*>(buf + kQgABytes)[srow * kQgStage + sblk] = QT == 1 ? s.d * 0.0625f : s.d;
-  if (w0) *reinterpret_cast<u32x2_t*>(buf + kQgABytes + kQgDaBytes + (lane >> 4) * 128 + 8 * (lane & 15)) = s.dw;
+  if (w0 && !CONV) {
+    *reinterpret_cast<u32x2_t*>(buf + kQgABytes + kQgDaBytes + (lane >> 4) * 128 + 8 * (lane & 15)) = s.dw;
+  } else if (w0) {
+    const float d0 = to_f32<SC>(s.dw.x & 0xffffu), d1 = to_f32<SC>(s.dw.x >> 16);
+    const float d2 = to_f32<SC>(s.dw.y & 0xffffu), d3 = to_f32<SC>(s.dw.y >> 16);
+    f32x4_t* o = reinterpret_cast<f32x4_t*>(buf + kQgABytes + kQgDaBytes + (lane >> 4) * 512 + 32 * (lane & 15));
+    o[0] = f32x4_t{d0, -kQgBiasF * d0, d1, -kQgBiasF * d1};
+    o[1] = f32x4_t{d2, -kQgBiasF * d2, d3, -kQgBiasF * d3};
+  }
 }
 
 // MFMA B bytes: Q8_0 as stored; Q4_0 as 16 * (n - 8), elements 8q..8q+7
@@ -458,19 +472,13 @@ __device__ __forceinline__ long qg_wbytes(uint64_t w) {
 }
 
 // acc[s] += round(isum * dw) * da (fused) for block `sblk` of the step and the
-// NSUB sub-tiles.  raw = the fp16/bf16 scales of weight rows 4q..4q+3;
+// NSUB sub-tiles, given dw and nb = -1.5 * 2^23 * dw of weight rows 4q..4q+3;
 // dq[s] = the staged activation scales of tile row 16s + r for the step's
 // blocks.
-template <int SC, int NSUB>
+template <int NSUB>
 __device__ __forceinline__ void qg_block(const unsigned char* buf, int sblk, int r, int q, long wb,
-                                         u32x2_t raw, const f32x4_t (&dq)[4], f32x4_t (&acc)[4]) {
-  const uint32_t rw[4] = {raw.x & 0xffffu, raw.x >> 16, raw.y & 0xffffu, raw.y >> 16};
-  float dws[4], nb[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    dws[i] = to_f32<SC>(rw[i]);
-    nb[i] = -kQgBiasF * dws[i];
-  }
+                                         const float (&dws)[4], const float (&nb)[4], const f32x4_t (&dq)[4],
+                                         f32x4_t (&acc)[4]) {
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) {
     const long av = *reinterpret_cast<const long*>(buf + (16 * s + r) * kQgRowStride + 32 * sblk + 8 * q);
@@ -525,6 +533,7 @@ template <int QT, int SC, int NSUB, int D>
 __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq, const float* rowd, int KB,
                                         const char* wtile, const uint16_t* stile, int tlb, int tid,
                                         f32x4_t (&acc)[4]) {
+  constexpr bool CONV = NSUB >= 3;         // weight scales staged as fp32 pairs
   const bool stager = (tid >> 6) < NSUB;   // waves holding the tile's rows
   const int lane = tid & 63, q = lane >> 4, r = lane & 15;
   const int srow = tid >> 2, sblk = tid & 3;   // staging: row, block within the step
@@ -539,7 +548,7 @@ __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq,
     ws[u].load(wtile, KB, min(u, NS - 1) * kQgStage, tl, q);
     sv[u] = qg_load(rowq, rowd, min(u, NS - 1) * kQgStage, sblk, stile, w0, lane);
   }
-  if (stager) qg_store<QT>(smem, srow, sblk, sv[0], w0, lane);
+  if (stager) qg_store<QT, SC, CONV>(smem, srow, sblk, sv[0], w0, lane);
   sv[0] = qg_load(rowq, rowd, min(D, NS - 1) * kQgStage, sblk, stile, w0, lane);
   __syncthreads();
   for (int st0 = 0; st0 < NS; st0 += D) {
@@ -556,9 +565,24 @@ __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq,
           dq[s] = *reinterpret_cast<const f32x4_t*>(buf + kQgABytes + (16 * s + r) * kQgStage * 4);
 #pragma unroll
         for (int b = 0; b < kQgStage; ++b) {
-          const u32x2_t raw =
-              *reinterpret_cast<const u32x2_t*>(buf + kQgABytes + kQgDaBytes + b * 128 + (tlb + 4 * q) * 2);
-          qg_block<SC, NSUB>(buf, b, r, q, qg_wbytes<QT>(ws[u].w[b]), raw, dq, acc);
+          float dws[4], nb[4];
+          if constexpr (CONV) {
+            const f32x4_t* scp =
+                reinterpret_cast<const f32x4_t*>(buf + kQgABytes + kQgDaBytes + b * 512 + (tlb + 4 * q) * 8);
+            const f32x4_t s0 = scp[0], s1 = scp[1];
+            dws[0] = s0.x; nb[0] = s0.y; dws[1] = s0.z; nb[1] = s0.w;
+            dws[2] = s1.x; nb[2] = s1.y; dws[3] = s1.z; nb[3] = s1.w;
+          } else {
+            const u32x2_t raw =
+                *reinterpret_cast<const u32x2_t*>(buf + kQgABytes + kQgDaBytes + b * 128 + (tlb + 4 * q) * 2);
+            const uint32_t rw[4] = {raw.x & 0xffffu, raw.x >> 16, raw.y & 0xffffu, raw.y >> 16};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              dws[i] = to_f32<SC>(rw[i]);
+              nb[i] = -kQgBiasF * dws[i];
+            }
+          }
+          qg_block<NSUB>(buf, b, r, q, qg_wbytes<QT>(ws[u].w[b]), dws, nb, dq, acc);
           // keep each block's scaling next to its MFMAs: left free, the fma
           // chains sink below all of the step's MFMAs and every MFMA result and
           // scale of the step is live at once
@@ -568,7 +592,7 @@ __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq,
       }
       const int un = (u + 1) % D;   // ring slot of step st + 1 (constant once unrolled)
       ws[u].load(wtile, KB, min(st + D, NS - 1) * kQgStage, tl, q);
-      if (more && stager) qg_store<QT>(smem + ((st & 1) ^ 1) * kQgBufBytes, srow, sblk, sv[un], w0, lane);
+      if (more && stager) qg_store<QT, SC, CONV>(smem + ((st & 1) ^ 1) * kQgBufBytes, srow, sblk, sv[un], w0, lane);
       sv[un] = qg_load(rowq, rowd, min(st + 1 + D, NS - 1) * kQgStage, sblk, stile, w0, lane);
       __syncthreads();
     }
@@ -593,8 +617,8 @@ __global__ __launch_bounds__(kBlock) void q_gemm13_kernel(QArgs a) {
   const int srow = tid >> 2;
   const int spair = c.rg.tok[row0 + min(srow, rows - 1)];
   const int tok = spair / c.K;
-  float* actt = reinterpret_cast<float*>(smem + 2 * kQgBufBytes);   // [64 rows][kQgActStride]
-  int* pairs = reinterpret_cast<int*>(actt + kGemmRows * kQgActStride);
+  float* actt = reinterpret_cast<float*>(smem);   // [64 rows][kQgActStride], after the K loop
+  int* pairs = reinterpret_cast<int*>(smem + 2 * kQgBufBytes);
   if ((tid & 3) == 0) pairs[srow] = spair;
   const size_t tile = (size_t)e * S + sl;
   f32x4_t acc[4];
@@ -677,7 +701,7 @@ __global__ __launch_bounds__(kBlock) void q_gemm2_kernel(QArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   const int srow = tid >> 2;
   const int spair = c.rg.tok[row0 + min(srow, rows - 1)];
-  int* pairs = reinterpret_cast<int*>(smem + 2 * kQgBufBytes + kGemmRows * kQgActStride * 4);
+  int* pairs = reinterpret_cast<int*>(smem + 2 * kQgBufBytes);
   if ((tid & 3) == 0) pairs[srow] = spair;
   const size_t tile = (size_t)e * HB + hb;
   f32x4_t acc[4];
