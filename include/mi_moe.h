@@ -33,9 +33,11 @@ extern "C" {
 #define MI_MOE_Q4_0 1
 #define MI_MOE_W4A16 2
 
-/* dtype codes for activations and scales */
+/* dtype codes for activations and scales (and router logits, which may also
+ * be MI_MOE_F32) */
 #define MI_MOE_F16 0
 #define MI_MOE_BF16 1
+#define MI_MOE_F32 2
 
 typedef struct mi_moe_handle mi_moe_handle;
 
@@ -155,6 +157,31 @@ int mi_moe_route(const int32_t* topk_ids, int64_t T, int64_t K, int64_t E,
 int mi_moe_block_dots(mi_moe_handle* h, int64_t expert, int proj,
                       const int8_t* a_qs, int64_t M, int32_t* isum,
                       void* stream);
+
+/* Router top-k + softmax: logits [T,E] (fp16, bf16 or fp32, device) ->
+ * topk_ids [T,K] int32 and topk_w [T,K] fp32 (device), the K largest logits
+ * of each token in descending order (equal logits: the lower expert id first)
+ * with weights softmax over the K values (renormalize != 0) or the softmax
+ * over all E gathered at the ids.  Replaces make_topk_from_logits_cpu
+ * (Int8-gemm/test/fused_moe_cpu.py:20-37), the step the reference harness
+ * runs before moe_forward.  E <= 512, 1 <= K <= min(E, 64).  Stream-ordered. */
+int mi_moe_topk_softmax(const void* logits, int logits_dtype, int64_t T,
+                        int64_t E, int64_t K, int renormalize,
+                        int32_t* topk_ids, float* topk_w, void* stream);
+
+/* Router top-k + softmax followed by mi_moe_forward on the same stream:
+ * router_logits [T,E] with E the handle's expert count.  The picks go to
+ * topk_ids_out / topk_w_out ([T,K], device) when both are given, else to a
+ * buffer the handle owns (grown on demand; growth synchronizes the stream).
+ * The reference composes make_topk_from_logits_cpu
+ * (Int8-gemm/test/fused_moe_cpu.py:20-37) with moe_forward
+ * (Int8-gemm/nanovllm_ops.cpp:219-236) in Python; here it is one call.  The
+ * handle's timer (mi_moe_get_last_run_time_ms) covers the forward only. */
+int mi_moe_forward_logits(mi_moe_handle* h, const void* x, void* y,
+                          const void* router_logits, int logits_dtype,
+                          int64_t T, int64_t K, int renormalize,
+                          int act_dtype, int32_t* topk_ids_out,
+                          float* topk_w_out, void* stream);
 
 #ifdef __cplusplus
 }

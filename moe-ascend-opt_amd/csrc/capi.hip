@@ -39,6 +39,7 @@ hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, hipStream_t
 hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, hipStream_t);
 hipError_t launch_qint_gemm(const QArgs&, int, int, int, hipStream_t);
+hipError_t launch_topk_softmax(const void*, int, int, int, int, int, int32_t*, float*, hipStream_t);
 hipError_t launch_q_repack(int, const void*, const uint16_t*, void*, uint16_t*, int, int, int, int,
                            int, hipStream_t);
 hipError_t launch_q8_online_quant(const void*, int, int, int, int, int, int, void*, uint16_t*,
@@ -125,6 +126,8 @@ struct mi_moe_handle {
   DevBuf act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U, r_tiles, r_ntiles;
   DevBuf xq, xd;   // Q8_0 activations of the grouped-GEMM path
   DevBuf r_chunk;  // per-chunk expert counts of the multi-workgroup routing
+  DevBuf r_rids, r_rw;   // router top-k ids / weights of mi_moe_forward_logits
+  int64_t cap_r = 0;     // capacity of r_rids / r_rw in (t, k) entries
 };
 
 namespace {
@@ -320,7 +323,7 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
   DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z,
                     &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
                     &h->r_active, &h->r_tok, &h->r_scat, &h->r_U, &h->r_tiles, &h->r_ntiles,
-                    &h->xq, &h->xd, &h->r_chunk};
+                    &h->xq, &h->xd, &h->r_chunk, &h->r_rids, &h->r_rw};
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
   if (h->ev1) (void)hipEventDestroy(h->ev1);
@@ -492,6 +495,50 @@ MI_API int mi_moe_forward(mi_moe_handle* h, const void* x, void* y, const float*
     h->timed_once = true;
   }
   return MI_MOE_OK;
+}
+
+MI_API int mi_moe_topk_softmax(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,
+                               int renormalize, int32_t* topk_ids, float* topk_w, void* stream) {
+  if (logits_dtype != MI_MOE_F16 && logits_dtype != MI_MOE_BF16 && logits_dtype != MI_MOE_F32)
+    return fail(MI_MOE_EINVAL, "logits dtype must be fp16, bf16 or fp32");
+  if (T < 0 || E < 1 || E > 512) return fail(MI_MOE_EINVAL, "bad T=%lld / E=%lld (E <= 512)", (long long)T, (long long)E);
+  if (K < 1 || K > E || K > 64) return fail(MI_MOE_EINVAL, "top_k=%lld must be in [1, min(E, 64)]", (long long)K);
+  if (T > ((int64_t)1 << 24)) return fail(MI_MOE_EINVAL, "T too large");
+  if (T == 0) return MI_MOE_OK;
+  if (!logits || !topk_ids || !topk_w) return fail(MI_MOE_EINVAL, "null pointer");
+  HIPCHK(launch_topk_softmax(logits, logits_dtype, (int)T, (int)E, (int)K, renormalize ? 1 : 0, topk_ids, topk_w,
+                             (hipStream_t)stream));
+  return MI_MOE_OK;
+}
+
+MI_API int mi_moe_forward_logits(mi_moe_handle* h, const void* x, void* y, const void* router_logits,
+                                 int logits_dtype, int64_t T, int64_t K, int renormalize, int act_dtype,
+                                 int32_t* topk_ids_out, float* topk_w_out, void* stream) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  if (T < 0 || K < 1 || K > 64) return fail(MI_MOE_EINVAL, "bad T=%lld / top_k=%lld", (long long)T, (long long)K);
+  if (T == 0) return MI_MOE_OK;
+  if ((topk_ids_out == nullptr) != (topk_w_out == nullptr))
+    return fail(MI_MOE_EINVAL, "topk_ids_out and topk_w_out must both be given or both be null");
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* ids = topk_ids_out;
+  float* w = topk_w_out;
+  if (!ids) {
+    const int64_t need = T * K;
+    if (need > h->cap_r) {
+      int64_t cap = h->cap_r ? h->cap_r : 1024;
+      while (cap < need) cap *= 2;
+      HIPCHK(hipStreamSynchronize(st));   // the buffers may be in use by queued work
+      HIPCHK(h->r_rids.alloc((size_t)cap * sizeof(int32_t)));
+      HIPCHK(h->r_rw.alloc((size_t)cap * sizeof(float)));
+      h->cap_r = cap;
+    }
+    ids = (int32_t*)h->r_rids.p;
+    w = (float*)h->r_rw.p;
+  }
+  rc = mi_moe_topk_softmax(router_logits, logits_dtype, T, h->E, K, renormalize, ids, w, stream);
+  if (rc) return rc;
+  return mi_moe_forward(h, x, y, w, ids, T, K, act_dtype, stream);
 }
 
 MI_API int mi_moe_get_last_phase_times_ms(mi_moe_handle* h, double* ms, int max_phases) {

@@ -361,4 +361,95 @@ hipError_t launch_quant_act(const void* x, int act, int64_t T, int64_t H, int8_t
   return hipGetLastError();
 }
 
+// Router top-k + softmax (make_topk_from_logits_cpu,
+// Int8-gemm/test/fused_moe_cpu.py:20-37): one wave per token.  Lane l holds
+// logits l, l+64, ... (E <= kTopkMaxE).  K rounds of a wave arg-max (the
+// larger logit, then the lower id: a total order, so every lane agrees);
+// lane k keeps pick k.  Softmax over the K picks (renorm) or over all E
+// gathered at the picks, with mi_expf and the sum taken in k (or e) order by
+// lane 0 through LDS, w = e / s: the arithmetic of orc_topk_softmax.
+constexpr int kTopkWaves = 4;
+constexpr int kTopkMaxE = 512;
+constexpr int kTopkMaxK = 64;
+template <int LDT>  // logits: 0 fp16, 1 bf16, 2 fp32
+__global__ __launch_bounds__(kTopkWaves * kWave) void topk_softmax_kernel(const void* __restrict__ logits,
+                                                                          int T, int E, int K, int renorm,
+                                                                          int32_t* __restrict__ ids_out,
+                                                                          float* __restrict__ w_out) {
+  __shared__ float ex[kTopkWaves][kTopkMaxE];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kTopkWaves + wave;
+  if (t >= T) return;   // whole wave; no workgroup barrier follows
+  constexpr int NJ = kTopkMaxE / kWave;
+  float v[NJ];
+  bool live[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = lane + kWave * j;
+    live[j] = e < E;
+    const size_t off = (size_t)t * E + (live[j] ? e : 0);
+    if constexpr (LDT == 2) v[j] = reinterpret_cast<const float*>(logits)[off];
+    else v[j] = to_f32<LDT>(reinterpret_cast<const uint16_t*>(logits)[off]);
+  }
+  float myv = 0.0f;
+  int myid = 0;
+  for (int k = 0; k < K; ++k) {
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;   // no candidate: loses to any real one
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (live[j] && (bi == 0x7fffffff || v[j] > bv)) { bv = v[j]; bi = lane + kWave * j; }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off);
+      const int oi = __shfl_xor(bi, off);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (bi == lane + kWave * j) live[j] = false;
+    if (lane == k) { myv = bv; myid = bi; }
+  }
+  const float m = __shfl(myv, 0);
+  float* exw = ex[wave];
+  float e_k = 0.0f;
+  if (renorm) {
+    if (lane < K) {
+      e_k = mi_expf(myv - m);
+      exw[lane] = e_k;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int e = lane + kWave * j;
+      if (e < E) exw[e] = mi_expf(v[j] - m);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  float s = 0.0f;
+  if (lane == 0) {
+    const int cnt = renorm ? K : E;
+    for (int i = 0; i < cnt; ++i) s = s + exw[i];
+  }
+  s = __shfl(s, 0);
+  if (lane < K) {
+    if (!renorm) e_k = exw[myid];
+    ids_out[(size_t)t * K + lane] = myid;
+    w_out[(size_t)t * K + lane] = e_k / s;
+  }
+}
+
+hipError_t launch_topk_softmax(const void* logits, int ldt, int T, int E, int K, int renorm, int32_t* ids,
+                               float* w, hipStream_t st) {
+  if (T == 0) return hipSuccess;
+  const dim3 grid((T + kTopkWaves - 1) / kTopkWaves), block(kTopkWaves * kWave);
+  if (ldt == 2)
+    hipLaunchKernelGGL(topk_softmax_kernel<2>, grid, block, 0, st, logits, T, E, K, renorm, ids, w);
+  else if (ldt == 1)
+    hipLaunchKernelGGL(topk_softmax_kernel<1>, grid, block, 0, st, logits, T, E, K, renorm, ids, w);
+  else
+    hipLaunchKernelGGL(topk_softmax_kernel<0>, grid, block, 0, st, logits, T, E, K, renorm, ids, w);
+  return hipGetLastError();
+}
+
 }  // namespace mimoe

@@ -2,11 +2,14 @@
 // the reference extension (Int8-gemm/nanovllm_ops.cpp:349-412):
 //   torch.classes.nanovllm.MoEInfer(E, H, I, quant_type)
 //   torch.ops.nanovllm.moe_forward(hidden, topk_ids, topk_w, moe) -> Tensor
-// plus the build-defined W4A16 loader store_awq_repack and the out variant
-// moe_forward_out.  Only this file sees torch types; it calls the C ABI of
+// plus the build-defined W4A16 loader store_awq_repack, the out variant
+// moe_forward_out, and the router step the reference runs in its Python
+// harness (make_topk_from_logits_cpu, Int8-gemm/test/fused_moe_cpu.py:20-37)
+// as moe_topk_softmax / moe_forward_logits.  Only this file sees torch types; it calls the C ABI of
 // include/mi_moe.h on the current HIP stream.
 #include <c10/hip/HIPStream.h>
 #include <torch/custom_class.h>
+#include <tuple>
 #include <vector>
 #include <torch/library.h>
 #include <ATen/ATen.h>
@@ -100,6 +103,53 @@ void moe_forward_out_hip(const at::Tensor& hidden, const at::Tensor& topk_ids,
                          const at::Tensor& topk_w, const c10::intrusive_ptr<MoEInferHandle>& moe,
                          at::Tensor out) {
   forward_into(hidden, topk_ids, topk_w, moe, out);
+}
+
+int logits_code(const at::Tensor& t) {
+  if (t.scalar_type() == at::kFloat) return MI_MOE_F32;
+  if (t.scalar_type() == at::kBFloat16) return MI_MOE_BF16;
+  TORCH_CHECK(t.scalar_type() == at::kHalf, "router logits must be float32, bfloat16 or float16");
+  return MI_MOE_F16;
+}
+
+std::tuple<at::Tensor, at::Tensor> moe_topk_softmax_hip(const at::Tensor& logits, int64_t top_k,
+                                                        bool renormalize) {
+  TORCH_CHECK(logits.is_cuda() && logits.dim() == 2, "moe_topk_softmax: logits must be a [T,E] HIP tensor");
+  at::Tensor x = contig(logits);
+  const int64_t T = x.size(0), E = x.size(1);
+  at::Tensor ids = at::empty({T, top_k}, x.options().dtype(at::kInt));
+  at::Tensor w = at::empty({T, top_k}, x.options().dtype(at::kFloat));
+  check_status(mi_moe_topk_softmax(x.data_ptr(), logits_code(x), T, E, top_k, renormalize ? 1 : 0,
+                                   ids.data_ptr<int32_t>(), w.data_ptr<float>(), stream_of(x)),
+               "moe_topk_softmax");
+  return {ids, w};
+}
+
+std::tuple<at::Tensor, at::Tensor> moe_topk_softmax_cpu_reject(const at::Tensor&, int64_t, bool) {
+  TORCH_CHECK(false, "nanovllm::moe_topk_softmax: this MI355X build runs on HIP tensors only");
+}
+
+at::Tensor moe_forward_logits_hip(const at::Tensor& hidden, const at::Tensor& router_logits, int64_t top_k,
+                                  bool renormalize, const c10::intrusive_ptr<MoEInferHandle>& moe) {
+  TORCH_CHECK(hidden.is_cuda() && router_logits.is_cuda() && hidden.device() == router_logits.device(),
+              "moe_forward_logits: hidden and router_logits must be HIP tensors on one device");
+  TORCH_CHECK(hidden.dim() == 2 && router_logits.dim() == 2 && router_logits.size(0) == hidden.size(0),
+              "moe_forward_logits: expected hidden [T,H], router_logits [T,E]");
+  TORCH_CHECK(router_logits.size(1) == moe->info(0), "router_logits has ", router_logits.size(1),
+              " experts, handle has ", moe->info(0));
+  TORCH_CHECK(hidden.size(1) == moe->info(1), "hidden size ", hidden.size(1), " != handle H ", moe->info(1));
+  at::Tensor x = contig(hidden), g = contig(router_logits);
+  at::Tensor out = at::empty_like(x);
+  check_status(mi_moe_forward_logits(moe->h, x.data_ptr(), out.data_ptr(), g.data_ptr(), logits_code(g),
+                                     x.size(0), top_k, renormalize ? 1 : 0, act_code(x), nullptr, nullptr,
+                                     stream_of(x)),
+               "moe_forward_logits");
+  return out;
+}
+
+at::Tensor moe_forward_logits_cpu_reject(const at::Tensor&, const at::Tensor&, int64_t, bool,
+                                         const c10::intrusive_ptr<MoEInferHandle>&) {
+  TORCH_CHECK(false, "nanovllm::moe_forward_logits: this MI355X build runs on HIP tensors only");
 }
 
 int scale_code(const at::Tensor& d) {
@@ -234,13 +284,20 @@ TORCH_LIBRARY_FRAGMENT(nanovllm, m) {
         "__torch__.torch.classes.nanovllm.MoEInfer moe) -> Tensor");
   m.def("moe_forward_out(Tensor hidden, Tensor topk_ids, Tensor topk_w, "
         "__torch__.torch.classes.nanovllm.MoEInfer moe, Tensor(a!) out) -> ()");
+  m.def("moe_topk_softmax(Tensor logits, int top_k, bool renormalize=True) -> (Tensor, Tensor)");
+  m.def("moe_forward_logits(Tensor hidden, Tensor router_logits, int top_k, bool renormalize, "
+        "__torch__.torch.classes.nanovllm.MoEInfer moe) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(nanovllm, CUDA, m) {
   m.impl("moe_forward", &moe_forward_hip);
   m.impl("moe_forward_out", &moe_forward_out_hip);
+  m.impl("moe_topk_softmax", &moe_topk_softmax_hip);
+  m.impl("moe_forward_logits", &moe_forward_logits_hip);
 }
 
 TORCH_LIBRARY_IMPL(nanovllm, CPU, m) {
   m.impl("moe_forward", &moe_forward_cpu_reject);
+  m.impl("moe_topk_softmax", &moe_topk_softmax_cpu_reject);
+  m.impl("moe_forward_logits", &moe_forward_logits_cpu_reject);
 }

@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(PKG_DIR, "libmimoe.so")
 SHIM_PATH = os.path.join(PKG_DIR, "libnanovllm_shim.so")
 
 Q8_0, Q4_0, W4A16 = 0, 1, 2
-F16, BF16 = 0, 1
+F16, BF16, F32 = 0, 1, 2   # dtype codes (F32: router logits only)
 
 _loaded = False
 _capi = None
@@ -35,7 +35,7 @@ C_SYMBOLS = (
     "mi_moe_get_info", "mi_moe_store_quantized", "mi_moe_quantize_and_store_expert",
     "mi_moe_store_awq", "mi_moe_forward", "mi_moe_get_last_run_time_ms",
     "mi_moe_set_timing", "mi_moe_quantize_act_q8_0", "mi_moe_route", "mi_moe_block_dots",
-    "mi_moe_get_last_phase_times_ms",
+    "mi_moe_get_last_phase_times_ms", "mi_moe_topk_softmax", "mi_moe_forward_logits",
 )
 
 
@@ -85,6 +85,8 @@ def capi():
     L.mi_moe_quantize_act_q8_0.argtypes = [P, I, I64, I64, P, P, P]
     L.mi_moe_route.argtypes = [P, I64, I64, I64, P, P, P, P, P]
     L.mi_moe_block_dots.argtypes = [P, I64, I, P, I64, P, P]
+    L.mi_moe_topk_softmax.argtypes = [P, I, I64, I64, I64, I, P, P, P]
+    L.mi_moe_forward_logits.argtypes = [P, P, P, P, I, I64, I64, I, I, P, P, P]
     for name in C_SYMBOLS:
         fn = getattr(L, name)
         if fn.restype is ctypes.c_int or fn.restype is None:

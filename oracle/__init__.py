@@ -18,6 +18,9 @@ Parity status per function (how each is pinned; see tests/test_oracle_*.py):
                         (Int8-gemm/test/fused_moe_cpu.py:40-95, loose).
   awq_dequant           known-answer packed words + pack/unpack round trip.
   moe_forward_w4a16     dense float64 torch formula over dequantized weights.
+  topk_softmax          the reference's own formula (torch.topk + torch.softmax,
+                        Int8-gemm/test/fused_moe_cpu.py:20-37): ids exact, weights
+                        within a few ulp; ties, K = E, -inf logits, float64 softmax.
 The exact fp32 bits of the ARM build (``-ffast-math``, ggml's exp polynomial)
 are not reproducible off-ARM: those bits are "parity unpinned" and are
 compared at tolerance.
@@ -196,6 +199,21 @@ def awq_dequant(qweight, qzeros, scales_bits, scale_dtype, group):
                           _p(np.ascontiguousarray(scales_bits, dtype=np.uint16)),
                           ctypes.c_int(scale_dtype), _i64(K), _i64(N), _i64(group), _p(w))
     return w
+
+
+def topk_softmax(logits: np.ndarray, K: int, renormalize: bool = True):
+    """Router top-k + softmax (make_topk_from_logits_cpu,
+    Int8-gemm/test/fused_moe_cpu.py:20-37): logits [T, E] float32 ->
+    (ids [T, K] int32, w [T, K] float32); equal logits: lower id first."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = x.shape
+    ids = np.zeros((T, K), np.int32)
+    w = np.zeros((T, K), np.float32)
+    rc = lib().orc_topk_softmax(_p(x), _i64(T), _i64(E), _i64(K), ctypes.c_int(1 if renormalize else 0),
+                                _p(ids), _p(w))
+    if rc != 0:
+        raise ValueError("orc_topk_softmax: bad sizes")
+    return ids, w
 
 
 def moe_forward_w4a16(act_dtype, scale_dtype, x_bits, topk_w, topk_ids,

@@ -474,3 +474,54 @@ int orc_moe_forward_w4a16(int act_dtype, int scale_dtype, const uint16_t* x,
   free(counts); free(starts); free(tmap); free(scat); free(xf); free(expert_out);
   return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* Router top-k + softmax -- make_topk_from_logits_cpu                  */
+/* (Int8-gemm/test/fused_moe_cpu.py:20-37)                              */
+/* ------------------------------------------------------------------ */
+/* Per token: the K largest of the E fp32 logits in descending order
+ * (torch.topk(largest=True, sorted=True); equal logits: the lower expert id
+ * first, a rule torch leaves open), then
+ *   renormalize: w_k = exp(v_k - v_0) / sum_{j<K} exp(v_j - v_0)   (softmax
+ *                of the K values; v_0 is their max), sum in k order;
+ *   otherwise:   w_k = exp(v_k - v_0) / sum_{e<E} exp(x_e - v_0)  (softmax
+ *                over all E gathered at the ids; v_0 is the max logit),
+ *                sum in e order.
+ * exp is orc_expf; NaN logits are not supported.  Returns -1 on bad sizes. */
+int orc_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t K, int renormalize,
+                     int32_t* ids, float* w) {
+  if (T < 0 || E < 1 || K < 1 || K > E) return -1;
+  unsigned char* taken = (unsigned char*)malloc((size_t)E);
+  float* ex = (float*)malloc(sizeof(float) * (size_t)(E > K ? E : K));
+  for (int64_t t = 0; t < T; ++t) {
+    const float* x = logits + t * E;
+    memset(taken, 0, (size_t)E);
+    for (int64_t k = 0; k < K; ++k) {
+      int64_t best = -1;
+      for (int64_t e = 0; e < E; ++e) {
+        if (taken[e]) continue;
+        if (best < 0 || x[e] > x[best]) best = e;   /* strict: ties keep the lower id */
+      }
+      taken[best] = 1;
+      ids[t * K + k] = (int32_t)best;
+    }
+    const float m = x[ids[t * K]];
+    float s = 0.0f;
+    if (renormalize) {
+      for (int64_t k = 0; k < K; ++k) {
+        ex[k] = orc_expf(x[ids[t * K + k]] - m);
+        s = s + ex[k];
+      }
+      for (int64_t k = 0; k < K; ++k) w[t * K + k] = ex[k] / s;
+    } else {
+      for (int64_t e = 0; e < E; ++e) {
+        ex[e] = orc_expf(x[e] - m);
+        s = s + ex[e];
+      }
+      for (int64_t k = 0; k < K; ++k) w[t * K + k] = ex[ids[t * K + k]] / s;
+    }
+  }
+  free(taken);
+  free(ex);
+  return 0;
+}

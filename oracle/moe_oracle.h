@@ -124,6 +124,10 @@ int orc_moe_forward_w4a16(int act_dtype, int scale_dtype, const uint16_t* x,
                           int64_t E, int64_t I, int64_t K, int64_t group,
                           int nthreads);
 
+/* Router top-k + softmax (Int8-gemm/test/fused_moe_cpu.py:20-37). */
+int orc_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t K,
+                     int renormalize, int32_t* ids, float* w);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,8 @@ def test_shim_registers_reference_schema():
     assert schema.startswith("nanovllm::moe_forward(Tensor hidden, Tensor topk_ids, Tensor topk_w, "
                              "__torch__.torch.classes.nanovllm.MoEInfer moe) -> Tensor")
     assert "Tensor(a!) out" in str(torch.ops.nanovllm.moe_forward_out.default._schema)
+    assert "(Tensor, Tensor)" in str(torch.ops.nanovllm.moe_topk_softmax.default._schema)
+    assert "router_logits" in str(torch.ops.nanovllm.moe_forward_logits.default._schema)
     methods = {str(s).split("(")[0] for s in torch._C._jit_get_custom_class_schemas()
                if "nanovllm.MoEInfer" in str(s)}
     for m in ("__init__", "quantize_and_store_expert", "store_quantized_repack", "store_awq_repack",
@@ -59,5 +61,12 @@ def test_argument_errors_are_status_codes():
     assert b"null handle" in L.mi_moe_last_error()
     assert L.mi_moe_route(None, -1, 8, 128, None, None, None, None, None) == 1
     assert L.mi_moe_quantize_act_q8_0(None, 1, 1, 33, None, None, None) == 1
+    assert L.mi_moe_topk_softmax(None, 3, 1, 128, 8, 1, None, None, None) == 1      # dtype
+    assert L.mi_moe_topk_softmax(None, 2, 1, 600, 8, 1, None, None, None) == 1      # E > 512
+    assert L.mi_moe_topk_softmax(None, 2, 1, 8, 9, 1, None, None, None) == 1        # K > E
+    assert b"top_k" in L.mi_moe_last_error()
+    assert L.mi_moe_topk_softmax(None, 2, 0, 128, 8, 1, None, None, None) == 0      # T = 0: nothing
+    assert L.mi_moe_forward_logits(None, None, None, None, 2, 1, 8, 1, 1, None, None, None) == 1
+    assert b"null handle" in L.mi_moe_last_error()
     assert L.mi_moe_destroy(None) == 0
     assert L.mi_moe_get_last_run_time_ms(None) < 0
