@@ -252,6 +252,81 @@ def run_config(cfg, steps, warmup):
                       "per_T": per}), flush=True)
 
 
+def time_closures(torch, fns, warmup):
+    """Mean µs per closure of `fns` replayed from one HIP graph, after eager
+    warmup calls (which also grow any on-demand buffers)."""
+    for i in range(max(warmup, 2)):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for f in fns:
+            f()
+    gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / len(fns)
+
+
+def run_router(steps, warmup):
+    """Router top-k + softmax ahead of dispatch (the step the reference runs in
+    its harness, make_topk_from_logits_cpu, Int8-gemm/test/fused_moe_cpu.py:
+    20-37) on the headline shape: the top-k kernel alone, the W4A16 decode
+    layer from precomputed ids, and the layer from router logits
+    (moe_forward_logits = top-k then the layer), bs 1/2/4/8, graph replay."""
+    import torch
+    import nanovllm_moe
+    nanovllm_moe.load()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rint32(*shape):
+        v = torch.randint(0, 2**32, shape, generator=g, dtype=torch.int64, device=dev)
+        return torch.where(v >= 2**31, v - 2**32, v).to(torch.int32)
+
+    E_, H_, I_, K_, copies = 128, 2048, 768, 8, 4
+    handles = []
+    for _ in range(copies):
+        h = torch.classes.nanovllm.MoEInfer(E_, H_, I_, 2)
+        s13 = (torch.rand(E_, H_ // GROUP, 2 * I_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
+        s2 = (torch.rand(E_, I_ // GROUP, H_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
+        h.store_awq_repack(rint32(E_, H_, 2 * I_ // 8), rint32(E_, H_ // GROUP, 2 * I_ // 8), s13,
+                           rint32(E_, I_, H_ // 8), rint32(E_, I_ // GROUP, H_ // 8), s2, GROUP)
+        h.set_timing(False)
+        handles.append(h)
+    topk = torch.ops.nanovllm.moe_topk_softmax
+    fwd_out = torch.ops.nanovllm.moe_forward_out
+    fwd_logits = torch.ops.nanovllm.moe_forward_logits
+    per = {}
+    n = max(steps // 4, 8)
+    for bs in BATCHES:
+        xs, gs, ids, ws = [], [], [], []
+        for i in range(8):
+            gg = torch.Generator().manual_seed(9000 + 10 * bs + i)
+            xs.append(torch.randn(bs, H_, generator=gg).to(torch.bfloat16).to(dev))
+            gs.append(torch.randn(bs, E_, generator=gg).to(dev))
+            a, b = topk(gs[-1], K_, True)
+            ids.append(a)
+            ws.append(b)
+        out = torch.empty(bs, H_, dtype=torch.bfloat16, device=dev)
+        t_topk = time_closures(torch, [lambda i=i: topk(gs[i % 8], K_, True) for i in range(n)], warmup)
+        t_ids = time_closures(torch, [lambda i=i: fwd_out(xs[i % 8], ids[i % 8], ws[i % 8], handles[i % copies], out)
+                                      for i in range(n)], warmup)
+        t_log = time_closures(torch, [lambda i=i: fwd_logits(xs[i % 8], gs[i % 8], K_, True, handles[i % copies])
+                                      for i in range(n)], warmup)
+        per[str(bs)] = {"topk_us": round(t_topk, 2), "layer_from_ids_us": round(t_ids, 2),
+                        "layer_from_logits_us": round(t_log, 2)}
+        log(f"[bench router] bs={bs}: top-k {t_topk:.2f} us, layer {t_ids:.2f} us, from logits {t_log:.2f} us")
+    print(json.dumps({"workload": "router top-k + softmax (renormalize) ahead of the W4A16 decode layer, "
+                                  "Qwen3-30B-A3B shape (H=2048, I=768, E=128, top-8)",
+                      "unit": "us per call", "timing": "HIP-graph replay", "weight_copies": copies,
+                      "per_bs": per}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -269,6 +344,8 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="BASELINE configuration: 2 (default) is the headline line; 3/4/5 print a "
                          "measurement line for Q4_0 prefill / MiniMax / Zipf routing")
+    ap.add_argument("--router", action="store_true",
+                    help="measure the router top-k kernel and the layer from router logits instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -277,6 +354,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.router:
+        run_router(args.steps, args.warmup)
         return
     if args.config != 2:
         run_config(args.config, args.steps, args.warmup)

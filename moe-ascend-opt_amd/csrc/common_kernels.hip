@@ -364,13 +364,47 @@ hipError_t launch_quant_act(const void* x, int act, int64_t T, int64_t H, int8_t
 // Router top-k + softmax (make_topk_from_logits_cpu,
 // Int8-gemm/test/fused_moe_cpu.py:20-37): one wave per token.  Lane l holds
 // logits l, l+64, ... (E <= kTopkMaxE).  K rounds of a wave arg-max (the
-// larger logit, then the lower id: a total order, so every lane agrees);
+// larger logit, then the lower id: a total order, so every lane agrees; DPP
+// inside rows, readlane across them);
 // lane k keeps pick k.  Softmax over the K picks (renorm) or over all E
 // gathered at the picks, with mi_expf and the sum taken in k (or e) order by
 // lane 0 through LDS, w = e / s: the arithmetic of orc_topk_softmax.
 constexpr int kTopkWaves = 4;
 constexpr int kTopkMaxE = 512;
 constexpr int kTopkMaxK = 64;
+
+// (v, i) beats (bv, bi): the larger logit, then the lower id
+__device__ __forceinline__ bool topk_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+template <int CTRL>
+__device__ __forceinline__ void topk_dpp_step(float& bv, int& bi) {
+  const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), CTRL, 0xf, 0xf, false));
+  const int oi = __builtin_amdgcn_mov_dpp(bi, CTRL, 0xf, 0xf, false);
+  if (topk_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+}
+
+// Wave arg-max of (bv, bi) under topk_better; the result in every lane.
+// Inside each 16-lane row: row_mirror (i <-> 15-i), row_half_mirror
+// (i <-> 7-i in each half), quad_perm [2,3,0,1] and [1,0,3,2] leave every
+// lane with the row's best; then the four rows through readlane.
+__device__ __forceinline__ void topk_wave_argmax(float& bv, int& bi) {
+  topk_dpp_step<0x140>(bv, bi);   // row_mirror
+  topk_dpp_step<0x141>(bv, bi);   // row_half_mirror
+  topk_dpp_step<0x4e>(bv, bi);    // quad_perm [2,3,0,1]
+  topk_dpp_step<0xb1>(bv, bi);    // quad_perm [1,0,3,2]
+  float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 0));
+  int ri = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+  for (int row = 1; row < 4; ++row) {
+    const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 16 * row));
+    const int i = __builtin_amdgcn_readlane(bi, 16 * row);
+    if (topk_better(v, i, rv, ri)) { rv = v; ri = i; }
+  }
+  bv = rv;
+  bi = ri;
+}
 template <int LDT>  // logits: 0 fp16, 1 bf16, 2 fp32
 __global__ __launch_bounds__(kTopkWaves * kWave) void topk_softmax_kernel(const void* __restrict__ logits,
                                                                           int T, int E, int K, int renorm,
@@ -399,18 +433,13 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_softmax_kernel(const 
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
       if (live[j] && (bi == 0x7fffffff || v[j] > bv)) { bv = v[j]; bi = lane + kWave * j; }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
+    topk_wave_argmax(bv, bi);
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
       if (bi == lane + kWave * j) live[j] = false;
     if (lane == k) { myv = bv; myid = bi; }
   }
-  const float m = __shfl(myv, 0);
+  const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), 0));
   float* exw = ex[wave];
   float e_k = 0.0f;
   if (renorm) {
@@ -431,7 +460,7 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_softmax_kernel(const 
     const int cnt = renorm ? K : E;
     for (int i = 0; i < cnt; ++i) s = s + exw[i];
   }
-  s = __shfl(s, 0);
+  s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
   if (lane < K) {
     if (!renorm) e_k = exw[myid];
     ids_out[(size_t)t * K + lane] = myid;
