@@ -27,10 +27,12 @@ HIP_SOURCES = ["capi.hip", "common_kernels.hip", "w4a16.hip", "qint.hip"]
 # Packed-FP32 instructions are disabled for all device code (only scalar /
 # float2 source is written; the compiler must not form v_pk_* fp32 ops).
 NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-# Per-file device flags.  The int8 grouped GEMMs read every MFMA result with
-# VALU ops (the per-block fp32 scaling); the VGPR form of the MFMA saves a
-# v_accvgpr_read per element.
-FILE_FLAGS = {"qint.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-file device flags.  The grouped GEMMs read every MFMA result with VALU
+# ops (the per-block fp32 scaling, the W4A16 zero/scale fold); the VGPR form
+# of the MFMA saves a v_accvgpr_read per result register.  The W4A16 decode
+# kernels compile to the same code either way.
+FILE_FLAGS = {"qint.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+              "w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd):

@@ -115,7 +115,7 @@ def test_gemm_path_tiles_and_invalid_ids(cuda, qt):
 
 
 @pytest.mark.parametrize("qt", [0, 1])
-@pytest.mark.parametrize("bs", [1, 8])
+@pytest.mark.parametrize("bs", [1, 8, 64])   # 64: 512 pairs, the int8 grouped-GEMM path
 def test_qwen_shape(cuda, qt, bs):
     E, H, I = 128, 2048, 768
     w = _weights(qt, E, H, I, seed=99)
