@@ -84,6 +84,7 @@ __host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) 
 struct W4Plan {
   int nb1, s1;    // phase 1: groups per load batch, 16-row slices per workgroup
   int nb2, rt2;   // down: groups per load batch, 16-row tiles per wave
+  int wide2;      // down: 8 waves per SIMD (grids beyond one resident round at 6)
 };
 
 // Q8_0 / Q4_0 fused kernel (qint.hip).

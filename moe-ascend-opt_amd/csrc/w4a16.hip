@@ -378,8 +378,8 @@ __device__ __forceinline__ void down_tiles(const char* wb, const uint16_t* arow,
 // y = 0 (Int8-gemm/q8_gemm.cpp:329-332).  No workspace traffic besides act,
 // no cross-workgroup communication.
 // LDS: act rows [K][I] | metadata [K][RT][SEC] | outputs [K][16 RT] f32 | valid [K].
-template <int ACT, int NB, int RT>
-__global__ __launch_bounds__(kDownMaxK * 64) __attribute__((amdgpu_waves_per_eu(kDownWavesPerEU)))
+template <int ACT, int NB, int RT, int WPE = kDownWavesPerEU>
+__global__ __launch_bounds__(kDownMaxK * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void w4a16_down_token_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -819,15 +819,19 @@ static hipError_t dispatch_p1(const W4Args& a, int nb, int s, int grid, size_t l
 
 // (NB, RT) pairs instantiated for the down kernel.  RT > 1 (2-4 tiles per
 // wave) measured no faster on the decode shapes, so only RT = 1 is built.
+// The wide variants (8 waves per SIMD, 64 VGPRs: 1- or 2-group batches, the
+// larger batches spill there) serve grids larger than one round of resident
+// workgroups at 6 waves per SIMD.
 template <int ACT>
-static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int grid, size_t lds, hipStream_t st) {
-#define P2_CASE(NB_, RT_)                                                                           \
-  if (nb == NB_ && rt == RT_) {                                                                     \
-    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3(grid), dim3(64 * a.c.K), lds, \
-                       st, a);                                                                      \
-    return hipGetLastError();                                                                       \
+static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int wide, int grid, size_t lds, hipStream_t st) {
+#define P2_CASE(NB_, RT_, WPE_)                                                                           \
+  if (nb == NB_ && rt == RT_ && (WPE_ == 8) == (wide != 0)) {                                             \
+    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_, WPE_>), dim3(grid), dim3(64 * a.c.K), lds, \
+                       st, a);                                                                            \
+    return hipGetLastError();                                                                             \
   }
-  P2_CASE(1, 1) P2_CASE(2, 1) P2_CASE(3, 1) P2_CASE(4, 1) P2_CASE(6, 1) P2_CASE(8, 1)
+  P2_CASE(1, 1, 6) P2_CASE(2, 1, 6) P2_CASE(3, 1, 6) P2_CASE(4, 1, 6) P2_CASE(6, 1, 6) P2_CASE(8, 1, 6)
+  P2_CASE(1, 1, 8) P2_CASE(2, 1, 8)
 #undef P2_CASE
   return hipErrorInvalidValue;
 }
@@ -844,14 +848,21 @@ static int pick_div(const int* sizes, int count, int need) {
 // counts (S slices per phase-1 workgroup and RT row tiles per down wave are 1:
 // larger values measured no faster on the decode shapes).  The token-major
 // down kernel spills at NB = 12 within its 6-waves-per-SIMD register budget,
-// so NB <= 8 there.
-W4Plan w4a16_plan(int H, int I) {
+// so NB <= 8 there.  A down grid larger than one round of resident
+// workgroups at 6 waves per SIMD (bs 8 at Qwen3: 1024 workgroups of 8 waves
+// against 768) runs the wide variant at 8 waves per SIMD with 2-group
+// batches: 13.9 -> 12.6 us at bs 8; below that, the single-batch NB is
+// faster (bs 1: 6.0 against 6.5 us).
+W4Plan w4a16_plan(int H, int I, int K, int grid2, int num_cu) {
   static const int nb1[] = {1, 2, 3, 4, 6, 8}, nb2[] = {1, 2, 3, 4, 6, 8};
   W4Plan p;
   p.nb1 = pick_div(nb1, 6, H / 512);
   p.s1 = 1;
-  p.nb2 = pick_div(nb2, 6, I / 128);
   p.rt2 = 1;
+  // down kernel: K waves per workgroup; 4 SIMDs per CU
+  const int resident6 = num_cu * ((4 * kDownWavesPerEU) / K);
+  p.wide2 = grid2 > resident6 ? 1 : 0;
+  p.nb2 = p.wide2 ? ((I / 128) % 2 == 0 ? 2 : 1) : pick_div(nb2, 6, I / 128);
   return p;
 }
 
@@ -863,7 +874,7 @@ static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int g
   hipError_t err = dispatch_p1<ACT>(a, p.nb1, p.s1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
-  return dispatch_p2<ACT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
+  return dispatch_p2<ACT>(a, p.nb2, p.rt2, p.wide2, grid2 / p.rt2, lds2, st);
 }
 
 // Decode path (T*K <= 64, K <= kDownMaxK): grid1 = T*K * I/16 (phase 1),
