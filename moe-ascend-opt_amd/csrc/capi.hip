@@ -22,7 +22,6 @@
 #define MI_API extern "C" __attribute__((visibility("default")))
 
 namespace mimoe {
-constexpr size_t kMaxLds = 65536;   // dynamic LDS a fused-kernel launch may ask for
 constexpr size_t kXAllBytes = 16384; // hidden rows phase 1 copies whole on the decode path
 constexpr int kDecodeCols = 4;       // phase-1 pass width on the decode path
 
@@ -34,7 +33,7 @@ hipError_t launch_awq_repack_all(const int32_t*, const int32_t*, const uint16_t*
                                  const int32_t*, const uint16_t*, void*, unsigned char*, void*,
                                  unsigned char*, int, int, int, hipStream_t);
 hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*, hipStream_t);
-W4Plan w4a16_plan(int, int, int, int, int);
+W4Plan w4a16_plan(int, int);
 hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, hipStream_t);
@@ -226,7 +225,7 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
     // keeps the LDS small (occupancy), extra columns take another pass
     a.p1_cols = (int)(T < kDecodeCols ? T : kDecodeCols);
     while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1) > kMaxLds) --a.p1_cols;
-    const W4Plan plan = w4a16_plan((int)h->H, (int)h->I, (int)K, (int)(T * (h->H / 16)), h->num_cu);
+    const W4Plan plan = w4a16_plan((int)h->H, (int)h->I);
     HIPCHK(launch_w4a16(a, plan, act, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st, mid));
     h->mid_recorded = mid != nullptr;
     return MI_MOE_OK;

@@ -67,6 +67,7 @@ struct W4Args {
 // Bytes of the w2 metadata of one 16-row tile: G2 = I/128 groups of 16 u16
 // scales and 8 bytes of zero nibbles, rounded up to 16 bytes.
 __host__ __device__ inline int w2_meta_sec_bytes(int G2) { return (40 * G2 + 15) & ~15; }
+constexpr size_t kMaxLds = 65536;   // dynamic LDS a kernel launch may ask for
 
 // The decode down kernel runs a wave per routed expert of a token.
 constexpr int kDownMaxK = 8;
@@ -84,7 +85,6 @@ __host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) 
 struct W4Plan {
   int nb1, s1;    // phase 1: groups per load batch, 16-row slices per workgroup
   int nb2, rt2;   // down: groups per load batch, 16-row tiles per wave
-  int wide2;      // down: 8 waves per SIMD (grids beyond one resident round at 6)
 };
 
 // Q8_0 / Q4_0 fused kernel (qint.hip).

@@ -378,8 +378,8 @@ __device__ __forceinline__ void down_tiles(const char* wb, const uint16_t* arow,
 // y = 0 (Int8-gemm/q8_gemm.cpp:329-332).  No workspace traffic besides act,
 // no cross-workgroup communication.
 // LDS: act rows [K][I] | metadata [K][RT][SEC] | outputs [K][16 RT] f32 | valid [K].
-template <int ACT, int NB, int RT, int WPE = kDownWavesPerEU>
-__global__ __launch_bounds__(kDownMaxK * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+template <int ACT, int NB, int RT>
+__global__ __launch_bounds__(kDownMaxK * 64) __attribute__((amdgpu_waves_per_eu(kDownWavesPerEU)))
 void w4a16_down_token_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -428,8 +428,10 @@ void w4a16_down_token_kernel(W4Args a) {
 // Per 128-k group the workgroup stages the tile's activation rows (bf16, row
 // stride kGemmRowStride) and their sums into LDS, double-buffered with one
 // barrier per group; each wave holds its 16 weight rows of the group (16 B per
-// lane) and the lane's scale and zero in registers, and the next group's
-// loads are issued before the current group is computed.  The MFMA A operand
+// lane) in registers, and the next group's loads are issued before the
+// current group is computed.  The workgroup's scales and zeros for all of K
+// (contiguous in the metadata layout) are copied into LDS once at the start,
+// so a step issues no per-lane metadata loads.  The MFMA A operand
 // is 16 rows of the tile (sub-tiles of 16 rows; only the sub-tiles holding
 // rows are computed), B the dequantized weights:
 //   acc += s * (sum_k x (magic + q) - (offset + z) * sum_k x)   per group,
@@ -441,7 +443,16 @@ void w4a16_down_token_kernel(W4Args a) {
 constexpr int kGemmRowStride = 272;   // 256 B of a row + 16 B that spread the rows over the LDS banks
 constexpr int kGemmABytes = kGemmRows * kGemmRowStride;
 // LDS: staged rows [2][kGemmABytes] | row sums [2][kGemmRows] f32 | pair of each row [kGemmRows]
+// | the workgroup's metadata (gemm13: 4 slice blocks of 80*G1 B; gemm2: 4
+// sections of w2_meta_sec_bytes(G2) B)
 constexpr size_t kGemmLds = 2 * (size_t)kGemmABytes + 3 * kGemmRows * sizeof(float);
+
+// Copy nbytes (a multiple of 16) from global to LDS with the workgroup's
+// threads; the caller's barrier makes them visible.
+__device__ __forceinline__ void gemm_copy_meta(unsigned char* dst, const unsigned char* src, int nbytes, int tid) {
+  for (int k = tid; k < (nbytes >> 4); k += kBlock)
+    *reinterpret_cast<u32x4_t*>(dst + 16 * k) = ldg16(src + 16 * k);
+}
 
 // The staging thread's 32 values of its row (4 x 16 B) and their sum over the
 // row's 128 values (v_dot2 with (1, 1), then the row's 4 threads, which are
@@ -521,11 +532,13 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
   const uint16_t* xsrc = c.x + (size_t)(spair / c.K) * H + 32 * spart;
   const size_t blk = (size_t)e * NI1 + j;
   const char* wg = (const char*)a.w13 + blk * 2 * G1 * 1024 + lane * 16;
-  const unsigned char* mb = a.w13_m + blk * 80 * G1;
-  const uint32_t* msc = reinterpret_cast<const uint32_t*>(mb) + r * G1;
-  const unsigned char* mz = mb + 64 * G1 + r * G1;
   float* sums0 = reinterpret_cast<float*>(smem + 2 * kGemmABytes);
   int* pairs = reinterpret_cast<int*>(sums0 + 2 * kGemmRows);   // the tile's pair indices
+  unsigned char* meta = smem + kGemmLds;                         // [4 slices][80 * G1]
+  gemm_copy_meta(meta, a.w13_m + ((size_t)e * NI1 + 4 * sb) * 80 * G1, 4 * 80 * G1, tid);
+  const unsigned char* mb = meta + wave * 80 * G1;
+  const uint32_t* msc = reinterpret_cast<const uint32_t*>(mb) + r * G1;
+  const unsigned char* mz = mb + 64 * G1 + r * G1;
   constexpr float off = W4Consts<ACT>::offset;
 
   // only the waves of the sub-tiles holding rows store staged activations
@@ -535,7 +548,6 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) sv[i] = ldg16(xsrc + 8 * i);
   u32x4_t wgc = ldg16(wg), wuc = ldg16(wg + (size_t)G1 * 1024);
-  uint32_t scc = msc[0], zzc = mz[0];
   if (spart == 0) pairs[srow] = spair;
   if (stager) gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
   __syncthreads();
@@ -550,8 +562,8 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = ldg16(xsrc + 128 * gn + 8 * i);
     const u32x4_t wgn = ldg16(wg + (size_t)gn * 1024), wun = ldg16(wg + (size_t)(G1 + gn) * 1024);
-    const uint32_t scn = msc[gn], zzn = mz[gn];
     {
+      const uint32_t scc = msc[g], zzc = mz[g];
       const uint32_t wg4[4] = {wgc.x, wgc.y, wgc.z, wgc.w}, wu4[4] = {wuc.x, wuc.y, wuc.z, wuc.w};
       u32x4_t B[2][4];
 #pragma unroll
@@ -566,7 +578,7 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
     if (more && stager)
       gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
                        gemm_row_sum<ACT>(sv));
-    wgc = wgn; wuc = wun; scc = scn; zzc = zzn;
+    wgc = wgn; wuc = wun;
     __syncthreads();
   }
 #pragma unroll
@@ -603,9 +615,11 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
   const uint16_t* asrc = a.act + (size_t)spair * I + 32 * spart;
   const size_t tile = ((size_t)e * MQ + m) * 4 + wave;
   const char* wb = (const char*)a.w2 + tile * G2 * 1024 + lane * 16;
-  const unsigned char* sec = a.w2_m + tile * SEC;
   float* sums0 = reinterpret_cast<float*>(smem + 2 * kGemmABytes);
   int* pairs = reinterpret_cast<int*>(sums0 + 2 * kGemmRows);
+  unsigned char* meta = smem + kGemmLds;   // [4 tiles][SEC]
+  gemm_copy_meta(meta, a.w2_m + ((size_t)e * MQ + m) * 4 * SEC, 4 * SEC, tid);
+  const unsigned char* sec = meta + wave * SEC;
   constexpr float off = W4Consts<ACT>::offset;
 
   const bool stager = wave < nsub;
@@ -613,7 +627,6 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) sv[i] = ldg16(asrc + 8 * i);
   u32x4_t wc = ldg16(wb);
-  float sc = w2_scale(sec, 0, r, a.sdt), zc = w2_zero(sec, G2, 0, r);
   if (spart == 0) pairs[srow] = spair;
   if (stager) gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
   __syncthreads();
@@ -627,8 +640,8 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = ldg16(asrc + 128 * gn + 8 * i);
     const u32x4_t wn = ldg16(wb + (size_t)gn * 1024);
-    const float sn = w2_scale(sec, gn, r, a.sdt), zn = w2_zero(sec, G2, gn, r);
     {
+      const float sc = w2_scale(sec, g2, r, a.sdt), zc = w2_zero(sec, G2, g2, r);
       const uint32_t w4[4] = {wc.x, wc.y, wc.z, wc.w};
       u32x4_t B[1][4];
 #pragma unroll
@@ -639,7 +652,7 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
     if (more && stager)
       gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
                        gemm_row_sum<ACT>(sv));
-    wc = wn; sc = sn; zc = zn;
+    wc = wn;
     __syncthreads();
   }
 #pragma unroll
@@ -657,17 +670,20 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
 
 hipError_t launch_w4a16_gemm(const W4Args& a, int act, int tiles_max, hipStream_t st, hipEvent_t mid) {
   const int g13 = tiles_max * (a.c.I / 64), g2 = tiles_max * (a.c.H / 64);
+  const size_t lds13 = kGemmLds + (size_t)4 * 80 * (a.c.H / 128);
+  const size_t lds2 = kGemmLds + (size_t)4 * w2_meta_sec_bytes(a.c.I / 128);
+  if (lds13 > kMaxLds || lds2 > kMaxLds) return hipErrorInvalidValue;
   if (act == 1)
-    hipLaunchKernelGGL((w4a16_gemm13_kernel<1>), dim3(g13), dim3(kBlock), kGemmLds, st, a);
+    hipLaunchKernelGGL((w4a16_gemm13_kernel<1>), dim3(g13), dim3(kBlock), lds13, st, a);
   else
-    hipLaunchKernelGGL((w4a16_gemm13_kernel<0>), dim3(g13), dim3(kBlock), kGemmLds, st, a);
+    hipLaunchKernelGGL((w4a16_gemm13_kernel<0>), dim3(g13), dim3(kBlock), lds13, st, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
   if (act == 1)
-    hipLaunchKernelGGL((w4a16_gemm2_kernel<1>), dim3(g2), dim3(kBlock), kGemmLds, st, a);
+    hipLaunchKernelGGL((w4a16_gemm2_kernel<1>), dim3(g2), dim3(kBlock), lds2, st, a);
   else
-    hipLaunchKernelGGL((w4a16_gemm2_kernel<0>), dim3(g2), dim3(kBlock), kGemmLds, st, a);
+    hipLaunchKernelGGL((w4a16_gemm2_kernel<0>), dim3(g2), dim3(kBlock), lds2, st, a);
   return hipGetLastError();
 }
 
@@ -819,19 +835,15 @@ static hipError_t dispatch_p1(const W4Args& a, int nb, int s, int grid, size_t l
 
 // (NB, RT) pairs instantiated for the down kernel.  RT > 1 (2-4 tiles per
 // wave) measured no faster on the decode shapes, so only RT = 1 is built.
-// The wide variants (8 waves per SIMD, 64 VGPRs: 1- or 2-group batches, the
-// larger batches spill there) serve grids larger than one round of resident
-// workgroups at 6 waves per SIMD.
 template <int ACT>
-static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int wide, int grid, size_t lds, hipStream_t st) {
-#define P2_CASE(NB_, RT_, WPE_)                                                                           \
-  if (nb == NB_ && rt == RT_ && (WPE_ == 8) == (wide != 0)) {                                             \
-    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_, WPE_>), dim3(grid), dim3(64 * a.c.K), lds, \
-                       st, a);                                                                            \
-    return hipGetLastError();                                                                             \
+static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int grid, size_t lds, hipStream_t st) {
+#define P2_CASE(NB_, RT_)                                                                           \
+  if (nb == NB_ && rt == RT_) {                                                                     \
+    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3(grid), dim3(64 * a.c.K), lds, \
+                       st, a);                                                                      \
+    return hipGetLastError();                                                                       \
   }
-  P2_CASE(1, 1, 6) P2_CASE(2, 1, 6) P2_CASE(3, 1, 6) P2_CASE(4, 1, 6) P2_CASE(6, 1, 6) P2_CASE(8, 1, 6)
-  P2_CASE(1, 1, 8) P2_CASE(2, 1, 8)
+  P2_CASE(1, 1) P2_CASE(2, 1) P2_CASE(3, 1) P2_CASE(4, 1) P2_CASE(6, 1) P2_CASE(8, 1)
 #undef P2_CASE
   return hipErrorInvalidValue;
 }
@@ -848,21 +860,14 @@ static int pick_div(const int* sizes, int count, int need) {
 // counts (S slices per phase-1 workgroup and RT row tiles per down wave are 1:
 // larger values measured no faster on the decode shapes).  The token-major
 // down kernel spills at NB = 12 within its 6-waves-per-SIMD register budget,
-// so NB <= 8 there.  A down grid larger than one round of resident
-// workgroups at 6 waves per SIMD (bs 8 at Qwen3: 1024 workgroups of 8 waves
-// against 768) runs the wide variant at 8 waves per SIMD with 2-group
-// batches: 13.9 -> 12.6 us at bs 8; below that, the single-batch NB is
-// faster (bs 1: 6.0 against 6.5 us).
-W4Plan w4a16_plan(int H, int I, int K, int grid2, int num_cu) {
+// so NB <= 8 there.
+W4Plan w4a16_plan(int H, int I) {
   static const int nb1[] = {1, 2, 3, 4, 6, 8}, nb2[] = {1, 2, 3, 4, 6, 8};
   W4Plan p;
   p.nb1 = pick_div(nb1, 6, H / 512);
   p.s1 = 1;
+  p.nb2 = pick_div(nb2, 6, I / 128);
   p.rt2 = 1;
-  // down kernel: K waves per workgroup; 4 SIMDs per CU
-  const int resident6 = num_cu * ((4 * kDownWavesPerEU) / K);
-  p.wide2 = grid2 > resident6 ? 1 : 0;
-  p.nb2 = p.wide2 ? ((I / 128) % 2 == 0 ? 2 : 1) : pick_div(nb2, 6, I / 128);
   return p;
 }
 
@@ -874,7 +879,7 @@ static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int g
   hipError_t err = dispatch_p1<ACT>(a, p.nb1, p.s1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
-  return dispatch_p2<ACT>(a, p.nb2, p.rt2, p.wide2, grid2 / p.rt2, lds2, st);
+  return dispatch_p2<ACT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
 }
 
 // Decode path (T*K <= 64, K <= kDownMaxK): grid1 = T*K * I/16 (phase 1),
