@@ -593,7 +593,8 @@ __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq,
       const int un = (u + 1) % D;   // ring slot of step st + 1 (constant once unrolled)
       ws[u].load(wtile, KB, min(st + D, NS - 1) * kQgStage, tl, q);
       if (more && stager) qg_store<QT, SC, CONV>(smem + ((st & 1) ^ 1) * kQgBufBytes, srow, sblk, sv[un], w0, lane);
-      sv[un] = qg_load(rowq, rowd, min(st + 1 + D, NS - 1) * kQgStage, sblk, stile, w0, lane);
+      if (stager)   // uniform per wave
+        sv[un] = qg_load(rowq, rowd, min(st + 1 + D, NS - 1) * kQgStage, sblk, stile, w0, lane);
       __syncthreads();
     }
   }
