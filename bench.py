@@ -171,7 +171,23 @@ def time_graph(torch, op_out, calls, out, warmup):
     return e0.elapsed_time(e1) * 1e3 / len(calls)
 
 
-def run_config(cfg, steps, warmup):
+def time_eager(torch, op_out, calls, out, warmup):
+    """Mean µs per call of `calls` issued eagerly (profiler counter runs,
+    which cannot collect inside a captured graph)."""
+    for i in range(max(warmup, 2)):
+        x, ids, w, h = calls[i % len(calls)]
+        op_out(x, ids, w, h, out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for x, ids, w, h in calls:
+        op_out(x, ids, w, h, out)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / len(calls)
+
+
+def run_config(cfg, steps, warmup, eager=False):
     """The other BASELINE configurations, as one JSON line each (not the
     headline line): 3 = Q4_0 prefill, Qwen3 shape, T 32..4096; 4 = MiniMax-M2
     W4A16, bs 1/8/64; 5 = Zipf-skewed routing (p ~ r^-1.2), T = 512, Qwen3
@@ -232,7 +248,7 @@ def run_config(cfg, steps, warmup):
             calls.append((x, ids_c.to(dev), w.to(torch.float32).to(dev), handles[i % copies]))
         seq = [calls[i % nroutes] for i in range(max(steps // 4, nroutes))]
         out = torch.empty(T, H_, dtype=torch.bfloat16, device=dev)
-        us = time_graph(torch, op_out, seq, out, warmup)
+        us = (time_eager if eager else time_graph)(torch, op_out, seq, out, warmup)
         byts = sum(nbytes[i % nroutes] for i in range(len(seq))) / len(seq)
         flops = 6 * T * K_ * H_ * I_
         per[str(T)] = {"us_per_layer": round(us, 2), "GB_per_s": round(byts / (us * 1e-6) / 1e9, 1),
@@ -248,7 +264,7 @@ def run_config(cfg, steps, warmup):
              4: "W4A16, MiniMax-M2 shape (H=3072, I=1536, E=256, top-8, group 128)",
              5: "W4A16, Qwen3-30B-A3B shape, Zipf-skewed routing (p ~ r^-1.2, distinct top-8)"}
     print(json.dumps({"config_id": cfg, "workload": names[cfg], "unit": "us/layer and GB/s",
-                      "timing": "HIP-graph replay", "weight_copies": copies, "routings": nroutes,
+                      "timing": "eager calls" if eager else "HIP-graph replay", "weight_copies": copies, "routings": nroutes,
                       "per_T": per}), flush=True)
 
 
@@ -359,7 +375,7 @@ def main():
         run_router(args.steps, args.warmup)
         return
     if args.config != 2:
-        run_config(args.config, args.steps, args.warmup)
+        run_config(args.config, args.steps, args.warmup, args.eager)
         return
     batches = tuple(int(b) for b in args.batches.split(","))
 

@@ -514,31 +514,40 @@ __device__ __forceinline__ void gemm_group(const unsigned char* buf, const float
   }
 }
 
-// gate_up + SiLU*mul: work item (row tile, block of 4 slices = 64 gate and 64
-// up rows); wave w owns slice 4*sb + w.  act[pair] gets the slice's 16 values.
+// gate_up + SiLU*mul: work item (row tile, kGemm13Blocks consecutive blocks of
+// 4 slices, a slice = 16 gate and 16 up rows); wave w owns slice w of each
+// block, so a staged activation row serves 2 * kGemm13Blocks weight tiles per
+// wave.  act[pair] gets the slices' 16 values each.
+constexpr int kGemm13Blocks = 2;
 template <int ACT>
 __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
+  constexpr int NB = kGemm13Blocks;
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, NI1 = c.I >> 4, G1 = H >> 7, NSB = NI1 >> 2;
+  const int H = c.H, NI1 = c.I >> 4, G1 = H >> 7, NSB = NI1 / (4 * NB);
   const int ti = blockIdx.x / NSB, sb = blockIdx.x - ti * NSB;
   if (ti >= *c.rg.ntiles) return;   // uniform
   const int4 tl = reinterpret_cast<const int4*>(c.rg.tiles)[ti];
   const int e = tl.x, row0 = tl.y, rows = tl.z, nsub = (rows + 15) >> 4;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
-  const int j = 4 * sb + wave;
   const int srow = tid >> 2, spart = tid & 3;
   const int spair = c.rg.tok[row0 + min(srow, rows - 1)];
   const uint16_t* xsrc = c.x + (size_t)(spair / c.K) * H + 32 * spart;
-  const size_t blk = (size_t)e * NI1 + j;
-  const char* wg = (const char*)a.w13 + blk * 2 * G1 * 1024 + lane * 16;
   float* sums0 = reinterpret_cast<float*>(smem + 2 * kGemmABytes);
   int* pairs = reinterpret_cast<int*>(sums0 + 2 * kGemmRows);   // the tile's pair indices
-  unsigned char* meta = smem + kGemmLds;                         // [4 slices][80 * G1]
-  gemm_copy_meta(meta, a.w13_m + ((size_t)e * NI1 + 4 * sb) * 80 * G1, 4 * 80 * G1, tid);
-  const unsigned char* mb = meta + wave * 80 * G1;
-  const uint32_t* msc = reinterpret_cast<const uint32_t*>(mb) + r * G1;
-  const unsigned char* mz = mb + 64 * G1 + r * G1;
+  unsigned char* meta = smem + kGemmLds;                         // [4 * NB slices][80 * G1]
+  gemm_copy_meta(meta, a.w13_m + ((size_t)e * NI1 + 4 * NB * sb) * 80 * G1, 4 * NB * 80 * G1, tid);
+  const char* wg[NB];
+  const uint32_t* msc[NB];
+  const unsigned char* mz[NB];
+#pragma unroll
+  for (int p = 0; p < NB; ++p) {
+    const int jl = 4 * p + wave;   // slice within the workgroup's blocks
+    wg[p] = (const char*)a.w13 + ((size_t)e * NI1 + 4 * NB * sb + jl) * 2 * G1 * 1024 + lane * 16;
+    const unsigned char* mb = meta + jl * 80 * G1;
+    msc[p] = reinterpret_cast<const uint32_t*>(mb) + r * G1;
+    mz[p] = mb + 64 * G1 + r * G1;
+  }
   constexpr float off = W4Consts<ACT>::offset;
 
   // only the waves of the sub-tiles holding rows store staged activations
@@ -547,13 +556,20 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
   u32x4_t sv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sv[i] = ldg16(xsrc + 8 * i);
-  u32x4_t wgc = ldg16(wg), wuc = ldg16(wg + (size_t)G1 * 1024);
+  u32x4_t wc[2 * NB];
+#pragma unroll
+  for (int p = 0; p < NB; ++p) {
+    wc[2 * p] = ldg16(wg[p]);
+    wc[2 * p + 1] = ldg16(wg[p] + (size_t)G1 * 1024);
+  }
   if (spart == 0) pairs[srow] = spair;
   if (stager) gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
   __syncthreads();
-  f32x4_t acc[2][4];
+  f32x4_t acc[2 * NB][4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) acc[0][s] = acc[1][s] = f32x4_t{0, 0, 0, 0};
+  for (int p = 0; p < 2 * NB; ++p)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[p][s] = f32x4_t{0, 0, 0, 0};
   for (int g = 0; g < G1; ++g) {
     const int b = g & 1;
     const bool more = g + 1 < G1;   // uniform
@@ -561,51 +577,69 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
     // next group: issued before this one is computed
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = ldg16(xsrc + 128 * gn + 8 * i);
-    const u32x4_t wgn = ldg16(wg + (size_t)gn * 1024), wun = ldg16(wg + (size_t)(G1 + gn) * 1024);
-    {
-      const uint32_t scc = msc[g], zzc = mz[g];
-      const uint32_t wg4[4] = {wgc.x, wgc.y, wgc.z, wgc.w}, wu4[4] = {wuc.x, wuc.y, wuc.z, wuc.w};
-      u32x4_t B[2][4];
+    u32x4_t wn[2 * NB];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        B[0][i] = deq4<ACT>(wg4[i]);
-        B[1][i] = deq4<ACT>(wu4[i]);
+    for (int p = 0; p < NB; ++p) {
+      wn[2 * p] = ldg16(wg[p] + (size_t)gn * 1024);
+      wn[2 * p + 1] = ldg16(wg[p] + (size_t)(G1 + gn) * 1024);
+    }
+    {
+      u32x4_t B[2 * NB][4];
+      float sc[2 * NB], cz[2 * NB];
+#pragma unroll
+      for (int p = 0; p < 2 * NB; ++p) {
+        const uint32_t w4[4] = {wc[p].x, wc[p].y, wc[p].z, wc[p].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) B[p][i] = deq4<ACT>(w4[i]);
       }
-      const float sc2[2] = {scale_f32(scc & 0xffffu, a.sdt), scale_f32(scc >> 16, a.sdt)};
-      const float cz2[2] = {off + (float)(zzc & 0xfu), off + (float)((zzc >> 4) & 0xfu)};
-      gemm_group<ACT, 2, true>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, sc2, cz2, acc);
+#pragma unroll
+      for (int p = 0; p < NB; ++p) {
+        const uint32_t scc = msc[p][g], zzc = mz[p][g];
+        sc[2 * p] = scale_f32(scc & 0xffffu, a.sdt);
+        sc[2 * p + 1] = scale_f32(scc >> 16, a.sdt);
+        cz[2 * p] = off + (float)(zzc & 0xfu);
+        cz[2 * p + 1] = off + (float)((zzc >> 4) & 0xfu);
+      }
+      gemm_group<ACT, 2 * NB, true>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, sc, cz, acc);
     }
     if (more && stager)
       gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
                        gemm_row_sum<ACT>(sv));
-    wgc = wgn; wuc = wun;
+#pragma unroll
+    for (int p = 0; p < 2 * NB; ++p) wc[p] = wn[p];
     __syncthreads();
   }
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    if (s < nsub) {
-      const float gv[4] = {acc[0][s].x, acc[0][s].y, acc[0][s].z, acc[0][s].w};
-      const float uv[4] = {acc[1][s].x, acc[1][s].y, acc[1][s].z, acc[1][s].w};
+  for (int p = 0; p < NB; ++p)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 16 * s + 4 * q + v;
-        if (row < rows)
-          a.act[(size_t)pairs[row] * c.I + 16 * j + r] = from_f32<ACT>(silu_mul_fast(gv[v], uv[v]));
+    for (int s = 0; s < 4; ++s) {
+      if (s < nsub) {
+        const float gv[4] = {acc[2 * p][s].x, acc[2 * p][s].y, acc[2 * p][s].z, acc[2 * p][s].w};
+        const float uv[4] = {acc[2 * p + 1][s].x, acc[2 * p + 1][s].y, acc[2 * p + 1][s].z, acc[2 * p + 1][s].w};
+        const int j = 4 * NB * sb + 4 * p + wave;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = 16 * s + 4 * q + v;
+          if (row < rows)
+            a.act[(size_t)pairs[row] * c.I + 16 * j + r] = from_f32<ACT>(silu_mul_fast(gv[v], uv[v]));
+        }
       }
     }
-  }
 }
 
-// down: work item (row tile, quad m = rows 64m..64m+63 of H); wave w owns the
-// 16-row tile 64m + 16w.  eout[pair] gets the tile's 16 fp32 values; the
-// combine kernel sums over k.
+// down: work item (row tile, kGemm2Quads consecutive quads m.. of H, a quad =
+// 64 rows); wave w owns the 16-row tile 64m + 16w of each quad, so a staged
+// activation row serves kGemm2Quads weight tiles (the rows are re-staged by
+// every workgroup of the tile: 2 quads halve that traffic).  eout[pair] gets
+// the tiles' fp32 values; the combine kernel sums over k.
+constexpr int kGemm2Quads = 4;
 template <int ACT>
 __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, I = c.I, G2 = I >> 7, MQ = H >> 6;
+  const int H = c.H, I = c.I, G2 = I >> 7, MQ = H >> 6, NMB = MQ / kGemm2Quads;
   const int SEC = w2_meta_sec_bytes(G2);
-  const int ti = blockIdx.x / MQ, m = blockIdx.x - ti * MQ;
+  const int ti = blockIdx.x / NMB, m0 = (blockIdx.x - ti * NMB) * kGemm2Quads;
   if (ti >= *c.rg.ntiles) return;   // uniform
   const int4 tl = reinterpret_cast<const int4*>(c.rg.tiles)[ti];
   const int e = tl.x, row0 = tl.y, rows = tl.z, nsub = (rows + 15) >> 4;
@@ -613,65 +647,85 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
   const int srow = tid >> 2, spart = tid & 3;
   const int spair = c.rg.tok[row0 + min(srow, rows - 1)];
   const uint16_t* asrc = a.act + (size_t)spair * I + 32 * spart;
-  const size_t tile = ((size_t)e * MQ + m) * 4 + wave;
-  const char* wb = (const char*)a.w2 + tile * G2 * 1024 + lane * 16;
+  const char* wb[kGemm2Quads];
+  const unsigned char* sec[kGemm2Quads];
   float* sums0 = reinterpret_cast<float*>(smem + 2 * kGemmABytes);
   int* pairs = reinterpret_cast<int*>(sums0 + 2 * kGemmRows);
-  unsigned char* meta = smem + kGemmLds;   // [4 tiles][SEC]
-  gemm_copy_meta(meta, a.w2_m + ((size_t)e * MQ + m) * 4 * SEC, 4 * SEC, tid);
-  const unsigned char* sec = meta + wave * SEC;
+  unsigned char* meta = smem + kGemmLds;   // [kGemm2Quads quads][4 tiles][SEC], contiguous in HBM
+  gemm_copy_meta(meta, a.w2_m + ((size_t)e * MQ + m0) * 4 * SEC, kGemm2Quads * 4 * SEC, tid);
+#pragma unroll
+  for (int p = 0; p < kGemm2Quads; ++p) {
+    const size_t tile = ((size_t)e * MQ + m0 + p) * 4 + wave;
+    wb[p] = (const char*)a.w2 + tile * G2 * 1024 + lane * 16;
+    sec[p] = meta + (p * 4 + wave) * SEC;
+  }
   constexpr float off = W4Consts<ACT>::offset;
 
   const bool stager = wave < nsub;
   u32x4_t sv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sv[i] = ldg16(asrc + 8 * i);
-  u32x4_t wc = ldg16(wb);
+  u32x4_t wc[kGemm2Quads];
+#pragma unroll
+  for (int p = 0; p < kGemm2Quads; ++p) wc[p] = ldg16(wb[p]);
   if (spart == 0) pairs[srow] = spair;
   if (stager) gemm_stage_store(smem, sums0, srow, spart, sv, gemm_row_sum<ACT>(sv));
   __syncthreads();
-  f32x4_t acc[1][4];
+  f32x4_t acc[kGemm2Quads][4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) acc[0][s] = f32x4_t{0, 0, 0, 0};
+  for (int p = 0; p < kGemm2Quads; ++p)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[p][s] = f32x4_t{0, 0, 0, 0};
   for (int g2 = 0; g2 < G2; ++g2) {
     const int b = g2 & 1;
     const bool more = g2 + 1 < G2;   // uniform
     const int gn = more ? g2 + 1 : g2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = ldg16(asrc + 128 * gn + 8 * i);
-    const u32x4_t wn = ldg16(wb + (size_t)gn * 1024);
-    {
-      const float sc = w2_scale(sec, g2, r, a.sdt), zc = w2_zero(sec, G2, g2, r);
-      const uint32_t w4[4] = {wc.x, wc.y, wc.z, wc.w};
-      u32x4_t B[1][4];
+    u32x4_t wn[kGemm2Quads];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) B[0][i] = deq4<ACT>(w4[i]);
-      const float sc1[1] = {sc}, cz1[1] = {off + zc};
-      gemm_group<ACT, 1, false>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, sc1, cz1, acc);
+    for (int p = 0; p < kGemm2Quads; ++p) wn[p] = ldg16(wb[p] + (size_t)gn * 1024);
+    {
+      u32x4_t B[kGemm2Quads][4];
+      float scp[kGemm2Quads], czp[kGemm2Quads];
+#pragma unroll
+      for (int p = 0; p < kGemm2Quads; ++p) {
+        const uint32_t w4[4] = {wc[p].x, wc[p].y, wc[p].z, wc[p].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) B[p][i] = deq4<ACT>(w4[i]);
+        scp[p] = w2_scale(sec[p], g2, r, a.sdt);
+        czp[p] = off + w2_zero(sec[p], G2, g2, r);
+      }
+      gemm_group<ACT, kGemm2Quads, false>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, scp,
+                                           czp, acc);
     }
     if (more && stager)
       gemm_stage_store(smem + (b ^ 1) * kGemmABytes, sums0 + (b ^ 1) * kGemmRows, srow, spart, sv,
                        gemm_row_sum<ACT>(sv));
-    wc = wn;
+#pragma unroll
+    for (int p = 0; p < kGemm2Quads; ++p) wc[p] = wn[p];
     __syncthreads();
   }
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    if (s < nsub) {
-      const float vv[4] = {acc[0][s].x, acc[0][s].y, acc[0][s].z, acc[0][s].w};
+  for (int p = 0; p < kGemm2Quads; ++p)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 16 * s + 4 * q + v;
-        if (row < rows) c.eout[(size_t)pairs[row] * H + 64 * m + 16 * wave + r] = vv[v];
+    for (int s = 0; s < 4; ++s) {
+      if (s < nsub) {
+        const float vv[4] = {acc[p][s].x, acc[p][s].y, acc[p][s].z, acc[p][s].w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = 16 * s + 4 * q + v;
+          if (row < rows) c.eout[(size_t)pairs[row] * H + 64 * (m0 + p) + 16 * wave + r] = vv[v];
+        }
       }
     }
-  }
 }
 
 hipError_t launch_w4a16_gemm(const W4Args& a, int act, int tiles_max, hipStream_t st, hipEvent_t mid) {
-  const int g13 = tiles_max * (a.c.I / 64), g2 = tiles_max * (a.c.H / 64);
-  const size_t lds13 = kGemmLds + (size_t)4 * 80 * (a.c.H / 128);
-  const size_t lds2 = kGemmLds + (size_t)4 * w2_meta_sec_bytes(a.c.I / 128);
+  const int g13 = tiles_max * (a.c.I / 64 / kGemm13Blocks), g2 = tiles_max * (a.c.H / 64 / kGemm2Quads);
+  const size_t lds13 = kGemmLds + (size_t)4 * kGemm13Blocks * 80 * (a.c.H / 128);
+  const size_t lds2 = kGemmLds + (size_t)kGemm2Quads * 4 * w2_meta_sec_bytes(a.c.I / 128);
+  if ((a.c.H / 64) % kGemm2Quads || (a.c.I / 64) % kGemm13Blocks) return hipErrorInvalidValue;
   if (lds13 > kMaxLds || lds2 > kMaxLds) return hipErrorInvalidValue;
   if (act == 1)
     hipLaunchKernelGGL((w4a16_gemm13_kernel<1>), dim3(g13), dim3(kBlock), lds13, st, a);
