@@ -183,6 +183,67 @@ int mi_moe_forward_logits(mi_moe_handle* h, const void* x, void* y,
                           int act_dtype, int32_t* topk_ids_out,
                           float* topk_w_out, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Hybrid CPU-offload executor.  The reference's NPU op runs the whole layer
+ * in a host callback between device->host and host->device copies
+ * (moe_forward_npu_stream, Int8-gemm/nanovllm_ops.cpp:244-305); its roadmap
+ * keeps hot experts in device memory and runs cold ones on the CPU
+ * (README.md:124-134).  Here experts with host_mask[e] != 0 ("cold") keep
+ * their wire-format weights in host memory and run on a pool of host
+ * threads; the others are stored compacted in a device handle, so device
+ * memory holds only them.  A forward overlaps the two halves (see
+ * mi_moe_hybrid_forward). */
+typedef struct mi_moe_hybrid mi_moe_hybrid;
+
+/* num_threads host threads (0: the hardware threads, at most 16).  Shape rules
+ * as mi_moe_create.  Without a HIP device only an all-cold handle can be made
+ * (usable through mi_moe_hybrid_host_forward). */
+int mi_moe_hybrid_create(int64_t num_experts, int64_t hidden, int64_t intermediate,
+                         int quant_type, const uint8_t* host_mask, int num_threads,
+                         mi_moe_hybrid** out);
+
+int mi_moe_hybrid_destroy(mi_moe_hybrid* hh);
+
+/* Same arrays and layouts as mi_moe_store_quantized / mi_moe_store_awq,
+ * covering all E experts; each expert's slices go to the device handle or to
+ * host memory according to the mask. */
+int mi_moe_hybrid_store_quantized(mi_moe_hybrid* hh, const void* gate_up_qs,
+                                  const void* gate_up_d, const void* down_qs,
+                                  const void* down_d, int scale_dtype,
+                                  int src_on_device, void* stream);
+int mi_moe_hybrid_store_awq(mi_moe_hybrid* hh, const int32_t* w13_qweight,
+                            const int32_t* w13_qzeros, const void* w13_scales,
+                            const int32_t* w2_qweight, const int32_t* w2_qzeros,
+                            const void* w2_scales, int64_t group, int scale_dtype,
+                            int src_on_device, void* stream);
+
+/* The fused MoE layer over all E experts, arguments as mi_moe_forward (device
+ * pointers, stream-ordered).  On `stream`: the ids of cold experts are
+ * remapped to -1 and the device handle runs the hot ones into y; meanwhile a
+ * side stream of the handle copies x, ids and topk_w to pinned host memory
+ * and runs the cold experts in a stream host callback; the fp32 partial is
+ * copied back and y = round(y_hot + y_cold), with y_hot already rounded to
+ * the activation dtype.  Calls that overlap on one handle race, as for
+ * mi_moe_forward.  Growing the staging buffers synchronizes the streams, so
+ * the call is not for graph capture. */
+int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y,
+                          const float* topk_w, const int32_t* topk_ids,
+                          int64_t T, int64_t K, int act_dtype, void* stream);
+
+/* The cold experts' partial alone, synchronously, on host memory: y_part
+ * [T,H] fp32 = per token, sum over k in order of topk_w * expert(x) over the
+ * pairs routed to cold experts (0 elsewhere).  x_host [T,H] fp16/bf16. */
+int mi_moe_hybrid_host_forward(mi_moe_hybrid* hh, const void* x_host,
+                               const float* topk_w_host,
+                               const int32_t* topk_ids_host, int64_t T,
+                               int64_t K, int act_dtype, float* y_part_host);
+
+/* Expert split, host weight bytes, and the last host pass (ms, routed pairs;
+ * valid once the stream of that call has been synchronized). */
+int mi_moe_hybrid_get_stats(mi_moe_hybrid* hh, int64_t* device_experts,
+                            int64_t* host_experts, int64_t* host_weight_bytes,
+                            double* last_host_ms, int64_t* last_host_pairs);
+
 #ifdef __cplusplus
 }
 #endif

@@ -290,9 +290,13 @@ MI_API const char* mi_moe_last_error(void) { return g_err.c_str(); }
 
 MI_API int mi_moe_version(void) { return 100; }
 
-MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe_handle** out) {
-  if (!out) return fail(MI_MOE_EINVAL, "out is null");
-  *out = nullptr;
+namespace mimoe {
+int api_fail(int code, const char* msg) {
+  g_err = msg;
+  return code;
+}
+
+int check_dims(int64_t E, int64_t H, int64_t I, int quant_type) {
   if (E <= 0 || H <= 0 || I <= 0) return fail(MI_MOE_EINVAL, "E, H, I must be positive");
   if (quant_type < 0 || quant_type > 2) return fail(MI_MOE_EINVAL, "quant_type must be 0, 1 or 2");
   if (H % 32 != 0) return fail(MI_MOE_EINVAL, "hidden_size must be multiple of 32");
@@ -302,6 +306,15 @@ MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe
   if (quant_type == MI_MOE_W4A16 && (H % 512 != 0 || I % 128 != 0))
     return fail(MI_MOE_EINVAL, "W4A16 needs hidden_size %% 512 == 0 and intermediate_size %% 128 == 0");
   if (E > 512) return fail(MI_MOE_EUNSUPPORTED, "at most 512 experts");
+  return MI_MOE_OK;
+}
+}  // namespace mimoe
+
+MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe_handle** out) {
+  if (!out) return fail(MI_MOE_EINVAL, "out is null");
+  *out = nullptr;
+  const int rc = check_dims(E, H, I, quant_type);
+  if (rc) return rc;
   mi_moe_handle* h = new (std::nothrow) mi_moe_handle();
   if (!h) return fail(MI_MOE_EINVAL, "out of host memory");
   h->E = E; h->H = H; h->I = I; h->quant = quant_type;

@@ -1,0 +1,351 @@
+// host_experts.cpp -- host executor of the hybrid offload path (see
+// host_experts.hpp).  Work is split into tasks of (cold expert, block of
+// output rows) so every weight byte a call needs is read once per call, by
+// one thread, for all the routed rows of its expert.
+#include "host_experts.hpp"
+
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+
+namespace mimoe_host {
+
+// ---------------------------------------------------------------- pool
+Pool::Pool(int nthreads) {
+  if (nthreads < 1) nthreads = 1;
+  for (int i = 1; i < nthreads; ++i) th_.emplace_back([this] { work(); });
+}
+
+Pool::~Pool() {
+  {
+    std::lock_guard<std::mutex> lk(m_);
+    stop_ = true;
+  }
+  cv_.notify_all();
+  for (auto& t : th_) t.join();
+}
+
+void Pool::run(int64_t n, const std::function<void(int64_t)>& f) {
+  if (n <= 0) return;
+  if (th_.empty() || n == 1) {
+    for (int64_t i = 0; i < n; ++i) f(i);
+    return;
+  }
+  std::unique_lock<std::mutex> lk(m_);
+  fn_ = &f;
+  n_ = n;
+  next_.store(0);
+  busy_ = (int)th_.size();
+  ++gen_;
+  lk.unlock();
+  cv_.notify_all();
+  for (int64_t i; (i = next_.fetch_add(1)) < n;) f(i);
+  lk.lock();
+  done_.wait(lk, [&] { return busy_ == 0; });   // every worker has left this generation
+  fn_ = nullptr;
+}
+
+void Pool::work() {
+  uint64_t seen = 0;
+  for (;;) {
+    std::unique_lock<std::mutex> lk(m_);
+    cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+    if (stop_) return;
+    seen = gen_;
+    const std::function<void(int64_t)>* f = fn_;
+    const int64_t n = n_;
+    lk.unlock();
+    for (int64_t i; (i = next_.fetch_add(1)) < n;) (*f)(i);
+    lk.lock();
+    if (--busy_ == 0) done_.notify_one();
+  }
+}
+
+// ---------------------------------------------------------------- formats
+int num_arrays(int quant) { return quant == 2 ? 6 : 4; }
+
+size_t expert_bytes(int quant, int64_t H, int64_t I, int idx) {
+  const int64_t N13 = 2 * I;
+  if (quant == 2) {   // AWQ, group 128
+    switch (idx) {
+      case 0: return (size_t)H * (N13 / 8) * 4;
+      case 1: return (size_t)(H / 128) * (N13 / 8) * 4;
+      case 2: return (size_t)(H / 128) * N13 * 2;
+      case 3: return (size_t)I * (H / 8) * 4;
+      case 4: return (size_t)(I / 128) * (H / 8) * 4;
+      case 5: return (size_t)(I / 128) * H * 2;
+      default: return 0;
+    }
+  }
+  const size_t qdiv = quant == 1 ? 2 : 1;
+  switch (idx) {
+    case 0: return (size_t)N13 * H / qdiv;
+    case 1: return (size_t)N13 * (H / 32) * 2;
+    case 2: return (size_t)H * I / qdiv;
+    case 3: return (size_t)H * (I / 32) * 2;
+    default: return 0;
+  }
+}
+
+namespace {
+
+constexpr int kTokBlock = 256;    // tokens per pass (bounds the per-pair buffers)
+constexpr int kQRows = 32;        // output rows per Q task
+constexpr int kAwqWords = 8;      // packed words (64 columns) per W4A16 task
+constexpr int kAwqOrder[8] = {0, 2, 4, 6, 1, 3, 5, 7};   // nibble slot s -> column 8j + order[s]
+
+float bits_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+float f16_f32(uint16_t h) {
+  const uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) {
+    const float v = (float)m * 5.9604644775390625e-8f;   // m * 2^-24 (exact)
+    return s ? -v : v;
+  }
+  if (e == 31) return bits_f32(s | 0x7f800000u | (m << 13));
+  return bits_f32(s | ((e + 112u) << 23) | (m << 13));
+}
+
+inline float half_f32(uint16_t v, int dt) { return dt == 1 ? bits_f32((uint32_t)v << 16) : f16_f32(v); }
+
+// Q8_0 of n values (n % 32 == 0): d = amax / 127, q = sat8(RNE(x / d))
+// (quantize_block_q8_0, Int8-gemm/gemm_kernels.cpp:37-57); d kept as fp32.
+void quant_q8_0(const float* x, int64_t n, int8_t* q, float* d) {
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const float* v = x + 32 * b;
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) amax = std::max(amax, fabsf(v[i]));
+    const float dd = amax / 127.0f, id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    d[b] = dd;
+    for (int i = 0; i < 32; ++i) {
+      const float r = std::min(std::max(nearbyintf(v[i] * id), -128.0f), 127.0f);
+      q[32 * b + i] = (int8_t)r;
+    }
+  }
+}
+
+__attribute__((target_clones("avx2", "default")))
+int32_t dot32(const int8_t* a, const int8_t* b) {
+  int32_t s = 0;
+  for (int i = 0; i < 32; ++i) s += (int32_t)a[i] * (int32_t)b[i];
+  return s;
+}
+
+// Rows [n0, n1) of a Q8_0 / Q4_0 matrix ([N][K] wire rows, scales [N][K/32])
+// against the Q8_0 rows of P routed pairs: out[p][n] = sum_kb (isum*dw)*da.
+void q_rows(int quant, int sdt, const uint8_t* wq, const uint16_t* wd, int64_t K, int64_t n0, int64_t n1,
+            const int8_t* const* aq, const float* const* ad, int64_t P, float* const* out) {
+  const int64_t KB = K / 32;
+  std::vector<int8_t> row(quant == 1 ? (size_t)K : 0);
+  std::vector<float> dw((size_t)KB);
+  for (int64_t n = n0; n < n1; ++n) {
+    const int8_t* w;
+    if (quant == 0) {
+      w = reinterpret_cast<const int8_t*>(wq) + n * K;
+    } else {   // element k in u32[k/8] bits 4(k%8), value nibble - 8
+      const uint32_t* u = reinterpret_cast<const uint32_t*>(wq) + n * (K / 8);
+      for (int64_t k = 0; k < K; ++k) row[k] = (int8_t)((int)((u[k >> 3] >> (4 * (k & 7))) & 15u) - 8);
+      w = row.data();
+    }
+    for (int64_t kb = 0; kb < KB; ++kb) dw[kb] = half_f32(wd[n * KB + kb], sdt);
+    for (int64_t p = 0; p < P; ++p) {
+      float c = 0.0f;
+      for (int64_t kb = 0; kb < KB; ++kb) {
+        const float t = (float)dot32(aq[p] + 32 * kb, w + 32 * kb) * dw[kb];
+        c = c + t * ad[p][kb];
+      }
+      out[p][n] = c;
+    }
+  }
+}
+
+__attribute__((target_clones("avx2", "default")))
+void axpy(float* __restrict__ y, const float* __restrict__ v, float a, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] += a * v[i];
+}
+
+// Columns [8*j0, 8*j1) of an AWQ matrix (qweight [K][N/8], qzeros [K/128][N/8],
+// scales [K/128][N]) against P fp32 rows xf[p] [K] with group sums xs[p]
+// [K/128]: out[p][n] = sum_g s * (sum_k x_k q_kn - z * xs_g).
+void awq_cols(const int32_t* q, const int32_t* z, const uint16_t* s, int sdt, int64_t K, int64_t N, int64_t j0,
+              int64_t j1, const float* const* xf, const float* const* xs, int64_t P, float* const* out) {
+  const int64_t NW = N / 8, G = K / 128, nc = (j1 - j0) * 8;
+  std::vector<float> acc((size_t)(P * nc), 0.0f), accg((size_t)(P * nc)), v((size_t)nc), sf((size_t)nc),
+      zf((size_t)nc);
+  for (int64_t g = 0; g < G; ++g) {
+    std::fill(accg.begin(), accg.end(), 0.0f);
+    for (int64_t k = 128 * g; k < 128 * g + 128; ++k) {
+      const int32_t* wr = q + k * NW;
+      for (int64_t j = j0; j < j1; ++j) {
+        const uint32_t u = (uint32_t)wr[j];
+        for (int sl = 0; sl < 8; ++sl) v[(j - j0) * 8 + kAwqOrder[sl]] = (float)((u >> (4 * sl)) & 15u);
+      }
+      for (int64_t p = 0; p < P; ++p) axpy(&accg[p * nc], v.data(), xf[p][k], nc);
+    }
+    for (int64_t j = j0; j < j1; ++j) {
+      const uint32_t u = (uint32_t)z[g * NW + j];
+      for (int sl = 0; sl < 8; ++sl) {
+        const int64_t col = 8 * j + kAwqOrder[sl], i = col - 8 * j0;
+        zf[i] = (float)((u >> (4 * sl)) & 15u);
+        sf[i] = half_f32(s[g * N + col], sdt);
+      }
+    }
+    for (int64_t p = 0; p < P; ++p) {
+      float* a = &acc[p * nc];
+      const float* b = &accg[p * nc];
+      const float x = xs[p][g];
+      for (int64_t i = 0; i < nc; ++i) a[i] += sf[i] * (b[i] - zf[i] * x);
+    }
+  }
+  for (int64_t p = 0; p < P; ++p) memcpy(out[p] + 8 * j0, &acc[p * nc], sizeof(float) * (size_t)nc);
+}
+
+float silu_mul(float g, float u) { return u * (g / (1.0f + expf(-g))); }
+
+}  // namespace
+
+int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype, const int32_t* ids,
+                const float* topk_w, int64_t T, int64_t K, float* y_part) {
+  const int64_t H = cs.H, I = cs.I, N13 = 2 * I, E = cs.E, Ec = cs.Ec;
+  const bool awq = cs.quant == 2;
+  memset(y_part, 0, sizeof(float) * (size_t)(T * H));
+  if (Ec == 0 || T == 0) return 0;
+  size_t eb[6];
+  for (int a = 0; a < 6; ++a) eb[a] = expert_bytes(cs.quant, H, I, a);
+  int64_t total = 0;
+  for (int64_t t0 = 0; t0 < T; t0 += kTokBlock) {
+    const int64_t t1 = std::min(T, t0 + kTokBlock), nT = t1 - t0;
+    // cold pairs of the block grouped by cold expert, pair order kept
+    std::vector<int64_t> start((size_t)Ec + 1, 0);
+    std::vector<int32_t> cold((size_t)(nT * K), -1);
+    for (int64_t i = 0; i < nT * K; ++i) {
+      const int32_t e = ids[t0 * K + i];
+      if (e >= 0 && e < E && cs.cold_of[e] >= 0) {
+        cold[i] = cs.cold_of[e];
+        ++start[cold[i] + 1];
+      }
+    }
+    for (int64_t c = 0; c < Ec; ++c) start[c + 1] += start[c];
+    const int64_t P = start[Ec];
+    if (P == 0) continue;
+    total += P;
+    std::vector<int64_t> pair_of((size_t)P), pos_of((size_t)(nT * K), -1), fill(start.begin(), start.end() - 1);
+    for (int64_t i = 0; i < nT * K; ++i)
+      if (cold[i] >= 0) {
+        const int64_t pos = fill[cold[i]]++;
+        pair_of[pos] = i;
+        pos_of[i] = pos;
+      }
+    // activations of the block's tokens
+    std::vector<float> xf((size_t)(nT * H));
+    for (int64_t i = 0; i < nT * H; ++i) xf[i] = half_f32(x[t0 * H + i], act_dtype);
+    std::vector<float> gu((size_t)(P * N13)), out((size_t)(P * H));
+    std::vector<const float*> pxf((size_t)P), pxs((size_t)P);
+    std::vector<const int8_t*> paq((size_t)P);
+    std::vector<const float*> pad((size_t)P);
+    std::vector<float*> pgu((size_t)P), pout((size_t)P);
+    std::vector<float> xs, act;
+    std::vector<int8_t> xq, aq;
+    std::vector<float> xd, ad;
+    const int64_t G1 = H / 128, G2 = I / 128;
+    if (awq) {
+      xs.resize((size_t)(nT * G1));
+      for (int64_t t = 0; t < nT; ++t)
+        for (int64_t g = 0; g < G1; ++g) {
+          float sum = 0.0f;
+          for (int64_t k = 0; k < 128; ++k) sum += xf[t * H + 128 * g + k];
+          xs[t * G1 + g] = sum;
+        }
+    } else {
+      xq.resize((size_t)(nT * H));
+      xd.resize((size_t)(nT * (H / 32)));
+      pool.run(nT, [&](int64_t t) { quant_q8_0(&xf[t * H], H, &xq[t * H], &xd[t * (H / 32)]); });
+    }
+    for (int64_t p = 0; p < P; ++p) {
+      const int64_t t = pair_of[p] / K;
+      pxf[p] = &xf[t * H];
+      if (awq) pxs[p] = &xs[t * G1];
+      else { paq[p] = &xq[t * H]; pad[p] = &xd[t * (H / 32)]; }
+      pgu[p] = &gu[p * N13];
+      pout[p] = &out[p * H];
+    }
+    // gate_up: tasks of (cold expert with pairs, row block)
+    std::vector<int64_t> task_c;
+    const int64_t blk13 = awq ? (N13 / 8) / kAwqWords : N13 / kQRows;
+    const int64_t blk2 = awq ? (H / 8) / kAwqWords : H / kQRows;
+    for (int64_t c = 0; c < Ec; ++c)
+      if (start[c + 1] > start[c]) task_c.push_back(c);
+    const int64_t nc = (int64_t)task_c.size();
+    pool.run(nc * blk13, [&](int64_t task) {
+      const int64_t c = task_c[task / blk13], b = task % blk13, p0 = start[c], np = start[c + 1] - p0;
+      if (awq) {
+        awq_cols(reinterpret_cast<const int32_t*>(cs.arr[0].data() + c * eb[0]),
+                 reinterpret_cast<const int32_t*>(cs.arr[1].data() + c * eb[1]),
+                 reinterpret_cast<const uint16_t*>(cs.arr[2].data() + c * eb[2]), cs.scale_dtype, H, N13,
+                 b * kAwqWords, (b + 1) * kAwqWords, &pxf[p0], &pxs[p0], np, &pgu[p0]);
+      } else {
+        q_rows(cs.quant, cs.scale_dtype, cs.arr[0].data() + c * eb[0],
+               reinterpret_cast<const uint16_t*>(cs.arr[1].data() + c * eb[1]), H, b * kQRows, (b + 1) * kQRows,
+               &paq[p0], &pad[p0], np, &pgu[p0]);
+      }
+    });
+    // SiLU(gate) * up, then the down projection's input rows
+    act.resize((size_t)(P * I));
+    if (awq) xs.assign((size_t)(P * G2), 0.0f);
+    else { aq.resize((size_t)(P * I)); ad.resize((size_t)(P * (I / 32))); }
+    pool.run(P, [&](int64_t p) {
+      float* a = &act[p * I];
+      const float* g = &gu[p * N13];
+      for (int64_t j = 0; j < I; ++j) a[j] = silu_mul(g[j], g[I + j]);
+      if (awq) {
+        for (int64_t gg = 0; gg < G2; ++gg) {
+          float sum = 0.0f;
+          for (int64_t k = 0; k < 128; ++k) sum += a[128 * gg + k];
+          xs[p * G2 + gg] = sum;
+        }
+      } else {
+        quant_q8_0(a, I, &aq[p * I], &ad[p * (I / 32)]);
+      }
+    });
+    for (int64_t p = 0; p < P; ++p) {
+      pxf[p] = &act[p * I];
+      if (awq) pxs[p] = &xs[p * G2];
+      else { paq[p] = &aq[p * I]; pad[p] = &ad[p * (I / 32)]; }
+    }
+    pool.run(nc * blk2, [&](int64_t task) {
+      const int64_t c = task_c[task / blk2], b = task % blk2, p0 = start[c], np = start[c + 1] - p0;
+      if (awq) {
+        awq_cols(reinterpret_cast<const int32_t*>(cs.arr[3].data() + c * eb[3]),
+                 reinterpret_cast<const int32_t*>(cs.arr[4].data() + c * eb[4]),
+                 reinterpret_cast<const uint16_t*>(cs.arr[5].data() + c * eb[5]), cs.scale_dtype, I, H,
+                 b * kAwqWords, (b + 1) * kAwqWords, &pxf[p0], &pxs[p0], np, &pout[p0]);
+      } else {
+        q_rows(cs.quant, cs.scale_dtype, cs.arr[2].data() + c * eb[2],
+               reinterpret_cast<const uint16_t*>(cs.arr[3].data() + c * eb[3]), I, b * kQRows, (b + 1) * kQRows,
+               &paq[p0], &pad[p0], np, &pout[p0]);
+      }
+    });
+    // weighted sum over k in ascending order
+    pool.run(nT, [&](int64_t t) {
+      float* yr = y_part + (t0 + t) * H;
+      for (int64_t k = 0; k < K; ++k) {
+        const int64_t pos = pos_of[t * K + k];
+        if (pos < 0) continue;
+        const float w = topk_w[(t0 + t) * K + k];
+        const float* o = &out[pos * H];
+        for (int64_t h = 0; h < H; ++h) {
+          const float prod = w * o[h];
+          yr[h] = yr[h] + prod;
+        }
+      }
+    });
+  }
+  return total;
+}
+
+}  // namespace mimoe_host

@@ -1,0 +1,74 @@
+// host_experts.hpp -- the host (CPU) half of the hybrid offload executor:
+// experts whose weights stay in host memory ("cold" experts) run here, on a
+// fixed pool of host threads, from the wire-format bytes the caller stored.
+//
+// Arithmetic per format (the reference CPU algorithm for Q8_0 / Q4_0,
+// Int8-gemm/q8_gemm.cpp:276-646, with tp = 1):
+//   Q8_0 / Q4_0  x rows -> Q8_0 blocks (fp32 d); gate_up rows c += (isum*dw)*da
+//                over the 32-blocks in order; SiLU(gate)*up; the intermediate
+//                -> Q8_0; down rows likewise; weighted sum over k in order.
+//   W4A16        fp32: y = sum_g s[g,n] * (sum_{k in g} x_k q_kn - z[g,n] sum_{k in g} x_k)
+//                per 128-group, SiLU(gate)*up in fp32, down likewise.
+// No HIP calls: this file is plain C++ and runs inside a stream host callback.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#include <atomic>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+namespace mimoe_host {
+
+// A fixed set of worker threads.  run(n, f) calls f(i) for every i in [0, n)
+// on the workers and the calling thread and returns when all calls are done.
+// One run at a time per pool.
+class Pool {
+ public:
+  explicit Pool(int nthreads);
+  ~Pool();
+  Pool(const Pool&) = delete;
+  Pool& operator=(const Pool&) = delete;
+  int size() const { return (int)th_.size() + 1; }
+  void run(int64_t n, const std::function<void(int64_t)>& f);
+
+ private:
+  void work();
+  std::vector<std::thread> th_;
+  std::mutex m_;
+  std::condition_variable cv_, done_;
+  const std::function<void(int64_t)>* fn_ = nullptr;
+  int64_t n_ = 0;
+  std::atomic<int64_t> next_{0};
+  int busy_ = 0;
+  uint64_t gen_ = 0;
+  bool stop_ = false;
+};
+
+// Number of weight arrays of a format (Q8_0 / Q4_0: gate_up_qs, gate_up_d,
+// down_qs, down_d; W4A16: w13_q, w13_z, w13_s, w2_q, w2_z, w2_s) and the
+// bytes one expert takes in array idx of the wire layout.
+int num_arrays(int quant);
+size_t expert_bytes(int quant, int64_t H, int64_t I, int idx);
+
+// Wire-format weights of the cold experts: arr[a] holds array a of cold
+// expert c at c * expert_bytes(quant, H, I, a).
+struct ColdSet {
+  int quant = 0;        // 0 Q8_0, 1 Q4_0, 2 W4A16 (group 128)
+  int scale_dtype = 0;  // 0 fp16, 1 bf16
+  int64_t E = 0, H = 0, I = 0, Ec = 0;
+  std::vector<int32_t> cold_of;   // [E]: cold index of expert e, or -1
+  std::vector<uint8_t> arr[6];
+};
+
+// y_part [T,H] fp32: per token, the sum over k in ascending order of
+// topk_w[t,k] * expert(x[t]) over the pairs whose id is a cold expert (rows
+// of tokens without such a pair are 0).  x [T,H] fp16/bf16 bits (act_dtype
+// 0/1).  Returns the number of cold pairs.
+int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype, const int32_t* ids,
+                const float* topk_w, int64_t T, int64_t K, float* y_part);
+
+}  // namespace mimoe_host

@@ -39,6 +39,12 @@ __host__ __device__ inline int64_t gemm_tiles_max(int64_t n, int E) {
   return n / kGemmRows + (n < E ? n : E);
 }
 
+// Error reporting and shape rules shared by the C-ABI translation units:
+// api_fail records msg as the thread's last error and returns code;
+// check_dims applies the handle shape rules of mi_moe_create.
+int api_fail(int code, const char* msg);
+int check_dims(int64_t E, int64_t H, int64_t I, int quant_type);
+
 // Arguments every fused kernel shares (routing, schedule, combine).
 struct SchedArgs {
   const uint16_t* x;       // [T,H] act dtype bits

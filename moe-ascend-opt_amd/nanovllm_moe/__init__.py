@@ -18,6 +18,7 @@ import ctypes
 import os
 
 from . import formats  # noqa: F401
+from .hybrid import HybridMoE  # noqa: F401
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libmimoe.so")
@@ -36,6 +37,9 @@ C_SYMBOLS = (
     "mi_moe_store_awq", "mi_moe_forward", "mi_moe_get_last_run_time_ms",
     "mi_moe_set_timing", "mi_moe_quantize_act_q8_0", "mi_moe_route", "mi_moe_block_dots",
     "mi_moe_get_last_phase_times_ms", "mi_moe_topk_softmax", "mi_moe_forward_logits",
+    "mi_moe_hybrid_create", "mi_moe_hybrid_destroy", "mi_moe_hybrid_store_quantized",
+    "mi_moe_hybrid_store_awq", "mi_moe_hybrid_forward", "mi_moe_hybrid_host_forward",
+    "mi_moe_hybrid_get_stats",
 )
 
 
@@ -87,6 +91,13 @@ def capi():
     L.mi_moe_block_dots.argtypes = [P, I64, I, P, I64, P, P]
     L.mi_moe_topk_softmax.argtypes = [P, I, I64, I64, I64, I, P, P, P]
     L.mi_moe_forward_logits.argtypes = [P, P, P, P, I, I64, I64, I, I, P, P, P]
+    L.mi_moe_hybrid_create.argtypes = [I64, I64, I64, I, P, I, ctypes.POINTER(P)]
+    L.mi_moe_hybrid_destroy.argtypes = [P]
+    L.mi_moe_hybrid_store_quantized.argtypes = [P, P, P, P, P, I, I, P]
+    L.mi_moe_hybrid_store_awq.argtypes = [P, P, P, P, P, P, P, I64, I, I, P]
+    L.mi_moe_hybrid_forward.argtypes = [P, P, P, P, P, I64, I64, I, P]
+    L.mi_moe_hybrid_host_forward.argtypes = [P, P, P, P, I64, I64, I, P]
+    L.mi_moe_hybrid_get_stats.argtypes = [P, P, P, P, P, P]
     for name in C_SYMBOLS:
         fn = getattr(L, name)
         if fn.restype is ctypes.c_int or fn.restype is None:

@@ -23,7 +23,13 @@ SHIM = os.path.join(PKG_DIR, "libnanovllm_shim.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["capi.hip", "common_kernels.hip", "w4a16.hip", "qint.hip"]
+HIP_SOURCES = ["capi.hip", "common_kernels.hip", "w4a16.hip", "qint.hip", "hybrid.hip"]
+# Host-only C++ (no HIP): the host executor of the hybrid offload path.  Its
+# inner loops are compiled for AVX2 and baseline x86-64 and picked at
+# load time (target_clones); -ffp-contract=off keeps the stated fp32 order.
+CXX = os.environ.get("CXX", "g++")
+CPP_SOURCES = ["host_experts.cpp"]
+CPP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-ffp-contract=off", "-fvisibility=hidden"]
 # Packed-FP32 instructions are disabled for all device code (only scalar /
 # float2 source is written; the compiler must not form v_pk_* fp32 ops).
 NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -57,10 +63,17 @@ def build_lib(verbose: bool = False) -> str:
                *FILE_FLAGS.get(src, []), os.path.join(CSRC, src), "-o", obj]
         return obj, _run(cmd)
 
+    def compile_cpp(src):
+        obj = os.path.join(objdir, src.replace(".cpp", ".o"))
+        cmd = [CXX, *CPP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", os.path.join(CSRC, src), "-o", obj]
+        return obj, _run(cmd)
+
+    cpp = [s for s in CPP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
     with ThreadPoolExecutor(max_workers=4) as ex:
-        results = list(ex.map(compile_one, srcs))
+        results = list(ex.map(compile_one, srcs)) + list(ex.map(compile_cpp, cpp))
     tmp = LIB + ".tmp"
-    out = _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for o, _ in results], "-o", tmp])
+    out = _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for o, _ in results], "-o", tmp,
+                "-pthread"])
     text = "\n".join(t for _, t in results if t.strip()) + out
     if verbose and text.strip():
         print(text)
