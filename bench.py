@@ -343,6 +343,96 @@ def run_router(steps, warmup):
                       "per_bs": per}), flush=True)
 
 
+def run_offload(steps, warmup, ncold=16, threads=0):
+    """Hybrid CPU-offload executor (mi_moe_hybrid_forward) on the headline
+    W4A16 shape: experts E-ncold..E-1 stay in host memory and run on host
+    threads, the others on the device; seeded uniform top-8 routing.  Per batch
+    size: the hybrid call (wall clock around synchronized calls, since its host
+    half runs on host threads), the all-device call on the same inputs, and
+    the host pass alone (its own timer) with the cold experts' weight bytes it
+    streams.  The reference runs the whole layer on the host in such a callback
+    (moe_forward_npu_stream, Int8-gemm/nanovllm_ops.cpp:244-305)."""
+    import torch
+    import nanovllm_moe
+    from nanovllm_moe import HybridMoE, formats
+    nanovllm_moe.load()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rint32(*shape):
+        v = torch.randint(0, 2**32, shape, generator=g, dtype=torch.int64, device=dev)
+        return torch.where(v >= 2**31, v - 2**32, v).to(torch.int32)
+
+    E_, H_, I_, K_ = 128, 2048, 768, 8
+    s13 = (torch.rand(E_, H_ // GROUP, 2 * I_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
+    s2 = (torch.rand(E_, I_ // GROUP, H_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
+    ws = (rint32(E_, H_, 2 * I_ // 8), rint32(E_, H_ // GROUP, 2 * I_ // 8), s13,
+          rint32(E_, I_, H_ // 8), rint32(E_, I_ // GROUP, H_ // 8), s2)
+    cold = list(range(E_ - ncold, E_))
+    hm = HybridMoE(E_, H_, I_, nanovllm_moe.W4A16, host_experts=cold, num_threads=threads)
+    hm.store_awq(*ws)
+    h = torch.classes.nanovllm.MoEInfer(E_, H_, I_, 2)
+    h.store_awq_repack(*ws, GROUP)
+    h.set_timing(False)
+    del ws
+    torch.cuda.synchronize()
+    per_expert = formats.bytes_per_expert(2, H_, I_)
+    st0 = hm.stats()
+    per = {}
+    n = max(steps // 8, 8)
+    for bs in (1, 8, 64):
+        calls = []
+        for i in range(8):
+            gg = torch.Generator().manual_seed(7000 + 10 * bs + i)
+            logits = torch.randn(bs, E_, generator=gg)
+            ids = torch.topk(logits, K_, dim=-1).indices.to(torch.int32)
+            w = torch.softmax(torch.topk(logits, K_, dim=-1).values, dim=-1)
+            calls.append((torch.randn(bs, H_, generator=gg).to(torch.bfloat16).to(dev), ids.to(dev),
+                          w.to(dev), ids))
+        for i in range(max(warmup, 2)):
+            x, ids, w, _ = calls[i % 8]
+            hm.forward(x, ids, w)
+            torch.ops.nanovllm.moe_forward(x, ids, w, h)
+        torch.cuda.synchronize()
+
+        def wall(fn):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(n):
+                fn(i)
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e6 / n
+
+        t_h = wall(lambda i: hm.forward(*calls[i % 8][:3]))
+        t_d = wall(lambda i: torch.ops.nanovllm.moe_forward(*calls[i % 8][:3], h))
+        host_ms, queue_ms, pairs, cold_bytes = [], [], [], []
+        for i in range(8):
+            x, ids, w, ids_cpu = calls[i]
+            hm.forward(x, ids, w)
+            torch.cuda.synchronize()
+            s = hm.stats()
+            host_ms.append(s["last_host_ms"])
+            queue_ms.append(s["last_queue_ms"])
+            pairs.append(s["last_host_pairs"])
+            used = set(int(e) for e in ids_cpu.reshape(-1).tolist()) & set(cold)
+            cold_bytes.append(len(used) * per_expert)
+        hms = sum(host_ms) / len(host_ms)
+        gbs = sum(cold_bytes) / len(cold_bytes) / (hms * 1e-3) / 1e9 if hms > 0 else None
+        per[str(bs)] = {"hybrid_us_per_call": round(t_h, 1), "device_only_us_per_call": round(t_d, 1),
+                        "host_pass_ms": round(hms, 3), "callback_queue_ms": round(sum(queue_ms) / len(queue_ms), 3),
+                        "cold_pairs_per_call": sum(pairs) / len(pairs),
+                        "cold_weight_MB_per_call": round(sum(cold_bytes) / len(cold_bytes) / 1e6, 2),
+                        "host_weight_GB_per_s": round(gbs, 2) if gbs else None}
+        log(f"[bench offload] bs={bs}: hybrid {t_h:.1f} us, device-only {t_d:.1f} us, host pass {hms:.3f} ms "
+            f"({sum(pairs) / len(pairs):.1f} cold pairs, {per[str(bs)]['host_weight_GB_per_s']} GB/s of host weights)")
+    print(json.dumps({"workload": f"hybrid CPU-offload W4A16 layer, Qwen3-30B-A3B shape (H=2048, I=768, E=128, "
+                                  f"top-8), {ncold} experts on the host", "unit": "us per call",
+                      "timing": "wall clock around synchronized eager calls",
+                      "host_threads": threads or "default (hardware threads, at most 16)",
+                      "device_experts": st0["device_experts"], "host_experts": st0["host_experts"],
+                      "host_weight_bytes": st0["host_weight_bytes"], "per_bs": per}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -360,6 +450,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="BASELINE configuration: 2 (default) is the headline line; 3/4/5 print a "
                          "measurement line for Q4_0 prefill / MiniMax / Zipf routing")
+    ap.add_argument("--offload", type=int, default=0, metavar="NCOLD",
+                    help="hybrid CPU-offload executor with NCOLD experts on the host (one JSON line)")
+    ap.add_argument("--host-threads", type=int, default=0)
     ap.add_argument("--router", action="store_true",
                     help="measure the router top-k kernel and the layer from router logits instead")
     args = ap.parse_args()
@@ -373,6 +466,9 @@ def main():
         return
     if args.router:
         run_router(args.steps, args.warmup)
+        return
+    if args.offload:
+        run_offload(args.steps, args.warmup, args.offload, args.host_threads)
         return
     if args.config != 2:
         run_config(args.config, args.steps, args.warmup, args.eager)

@@ -221,9 +221,9 @@ int mi_moe_hybrid_store_awq(mi_moe_hybrid* hh, const int32_t* w13_qweight,
  * pointers, stream-ordered).  On `stream`: the ids of cold experts are
  * remapped to -1 and the device handle runs the hot ones into y; meanwhile a
  * side stream of the handle copies x, ids and topk_w to pinned host memory
- * and runs the cold experts in a stream host callback; the fp32 partial is
- * copied back and y = round(y_hot + y_cold), with y_hot already rounded to
- * the activation dtype.  Calls that overlap on one handle race, as for
+ * and runs the cold experts in a stream host callback into a pinned fp32
+ * partial, which a device kernel then reads: y = round(y_hot + y_cold), with
+ * y_hot already rounded to the activation dtype.  Calls that overlap on one handle race, as for
  * mi_moe_forward.  Growing the staging buffers synchronizes the streams, so
  * the call is not for graph capture. */
 int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y,
@@ -238,11 +238,14 @@ int mi_moe_hybrid_host_forward(mi_moe_hybrid* hh, const void* x_host,
                                const int32_t* topk_ids_host, int64_t T,
                                int64_t K, int act_dtype, float* y_part_host);
 
-/* Expert split, host weight bytes, and the last host pass (ms, routed pairs;
- * valid once the stream of that call has been synchronized). */
+/* Expert split, host weight bytes, and the last host pass: its duration and
+ * routed pairs, and the delay from the mi_moe_hybrid_forward call to the start
+ * of its host callback (ms; valid once that call's stream has been
+ * synchronized).  Any output pointer may be NULL. */
 int mi_moe_hybrid_get_stats(mi_moe_hybrid* hh, int64_t* device_experts,
                             int64_t* host_experts, int64_t* host_weight_bytes,
-                            double* last_host_ms, int64_t* last_host_pairs);
+                            double* last_host_ms, int64_t* last_host_pairs,
+                            double* last_queue_ms);
 
 #ifdef __cplusplus
 }

@@ -92,7 +92,7 @@ namespace {
 
 constexpr int kTokBlock = 256;    // tokens per pass (bounds the per-pair buffers)
 constexpr int kQRows = 32;        // output rows per Q task
-constexpr int kAwqWords = 8;      // packed words (64 columns) per W4A16 task
+constexpr int kAwqWordsMax = 8;   // packed words (64 columns) per W4A16 task, at most
 constexpr int kAwqOrder[8] = {0, 2, 4, 6, 1, 3, 5, 7};   // nibble slot s -> column 8j + order[s]
 
 float bits_f32(uint32_t u) {
@@ -129,11 +129,28 @@ void quant_q8_0(const float* x, int64_t n, int8_t* q, float* d) {
   }
 }
 
+// Q4_0 wire row -> int8 values: element k in u32[k/8] bits 4(k%8), value nibble - 8.
 __attribute__((target_clones("avx2", "default")))
-int32_t dot32(const int8_t* a, const int8_t* b) {
-  int32_t s = 0;
-  for (int i = 0; i < 32; ++i) s += (int32_t)a[i] * (int32_t)b[i];
-  return s;
+void unpack_q4_0(const uint32_t* __restrict__ u, int8_t* __restrict__ row, int64_t nwords) {
+  for (int64_t j = 0; j < nwords; ++j) {
+    const uint32_t w = u[j];
+    for (int i = 0; i < 8; ++i) row[8 * j + i] = (int8_t)((int)((w >> (4 * i)) & 15u) - 8);
+  }
+}
+
+// One output of a Q8_0 / Q4_0 row: c = sum over the 32-blocks in order of
+// ((float)isum_kb * dw[kb]) * da[kb], isum the exact int32 block dot.
+__attribute__((target_clones("avx2", "default")))
+float q_row_dot(const int8_t* __restrict__ a, const int8_t* __restrict__ w, const float* __restrict__ dw,
+                const float* __restrict__ da, int64_t KB) {
+  float c = 0.0f;
+  for (int64_t kb = 0; kb < KB; ++kb) {
+    int32_t is = 0;
+    for (int i = 0; i < 32; ++i) is += (int32_t)a[32 * kb + i] * (int32_t)w[32 * kb + i];
+    const float t = (float)is * dw[kb];
+    c = c + t * da[kb];
+  }
+  return c;
 }
 
 // Rows [n0, n1) of a Q8_0 / Q4_0 matrix ([N][K] wire rows, scales [N][K/32])
@@ -147,20 +164,22 @@ void q_rows(int quant, int sdt, const uint8_t* wq, const uint16_t* wd, int64_t K
     const int8_t* w;
     if (quant == 0) {
       w = reinterpret_cast<const int8_t*>(wq) + n * K;
-    } else {   // element k in u32[k/8] bits 4(k%8), value nibble - 8
-      const uint32_t* u = reinterpret_cast<const uint32_t*>(wq) + n * (K / 8);
-      for (int64_t k = 0; k < K; ++k) row[k] = (int8_t)((int)((u[k >> 3] >> (4 * (k & 7))) & 15u) - 8);
+    } else {
+      unpack_q4_0(reinterpret_cast<const uint32_t*>(wq) + n * (K / 8), row.data(), K / 8);
       w = row.data();
     }
     for (int64_t kb = 0; kb < KB; ++kb) dw[kb] = half_f32(wd[n * KB + kb], sdt);
-    for (int64_t p = 0; p < P; ++p) {
-      float c = 0.0f;
-      for (int64_t kb = 0; kb < KB; ++kb) {
-        const float t = (float)dot32(aq[p] + 32 * kb, w + 32 * kb) * dw[kb];
-        c = c + t * ad[p][kb];
-      }
-      out[p][n] = c;
-    }
+    for (int64_t p = 0; p < P; ++p) out[p][n] = q_row_dot(aq[p], w, dw.data(), ad[p], KB);
+  }
+}
+
+// v[8*jj + sl] = nibble sl of w[jj] for nw packed words (packed-slot order:
+// column 8j + kAwqOrder[sl] of a word sits at slot sl).
+__attribute__((target_clones("avx2", "default")))
+void unpack_nibbles(const int32_t* __restrict__ w, float* __restrict__ v, int64_t nw) {
+  for (int64_t jj = 0; jj < nw; ++jj) {
+    const uint32_t u = (uint32_t)w[jj];
+    for (int sl = 0; sl < 8; ++sl) v[8 * jj + sl] = (float)((u >> (4 * sl)) & 15u);
   }
 }
 
@@ -174,25 +193,22 @@ void axpy(float* __restrict__ y, const float* __restrict__ v, float a, int64_t n
 // [K/128]: out[p][n] = sum_g s * (sum_k x_k q_kn - z * xs_g).
 void awq_cols(const int32_t* q, const int32_t* z, const uint16_t* s, int sdt, int64_t K, int64_t N, int64_t j0,
               int64_t j1, const float* const* xf, const float* const* xs, int64_t P, float* const* out) {
-  const int64_t NW = N / 8, G = K / 128, nc = (j1 - j0) * 8;
-  std::vector<float> acc((size_t)(P * nc), 0.0f), accg((size_t)(P * nc)), v((size_t)nc), sf((size_t)nc),
-      zf((size_t)nc);
+  const int64_t NW = N / 8, G = K / 128, nw = j1 - j0, nc = nw * 8;
+  // acc / accg / sf / zf in packed-slot order: index 8*(j-j0) + sl
+  std::vector<float> acc((size_t)(P * nc), 0.0f), accg((size_t)(P * nc)), sf((size_t)nc), zf((size_t)nc),
+      v((size_t)nc);
   for (int64_t g = 0; g < G; ++g) {
     std::fill(accg.begin(), accg.end(), 0.0f);
     for (int64_t k = 128 * g; k < 128 * g + 128; ++k) {
-      const int32_t* wr = q + k * NW;
-      for (int64_t j = j0; j < j1; ++j) {
-        const uint32_t u = (uint32_t)wr[j];
-        for (int sl = 0; sl < 8; ++sl) v[(j - j0) * 8 + kAwqOrder[sl]] = (float)((u >> (4 * sl)) & 15u);
-      }
+      unpack_nibbles(q + k * NW + j0, v.data(), nw);
       for (int64_t p = 0; p < P; ++p) axpy(&accg[p * nc], v.data(), xf[p][k], nc);
     }
     for (int64_t j = j0; j < j1; ++j) {
       const uint32_t u = (uint32_t)z[g * NW + j];
       for (int sl = 0; sl < 8; ++sl) {
-        const int64_t col = 8 * j + kAwqOrder[sl], i = col - 8 * j0;
+        const int64_t i = 8 * (j - j0) + sl;
         zf[i] = (float)((u >> (4 * sl)) & 15u);
-        sf[i] = half_f32(s[g * N + col], sdt);
+        sf[i] = half_f32(s[g * N + 8 * j + kAwqOrder[sl]], sdt);
       }
     }
     for (int64_t p = 0; p < P; ++p) {
@@ -202,7 +218,9 @@ void awq_cols(const int32_t* q, const int32_t* z, const uint16_t* s, int sdt, in
       for (int64_t i = 0; i < nc; ++i) a[i] += sf[i] * (b[i] - zf[i] * x);
     }
   }
-  for (int64_t p = 0; p < P; ++p) memcpy(out[p] + 8 * j0, &acc[p * nc], sizeof(float) * (size_t)nc);
+  for (int64_t p = 0; p < P; ++p)
+    for (int64_t j = j0; j < j1; ++j)
+      for (int sl = 0; sl < 8; ++sl) out[p][8 * j + kAwqOrder[sl]] = acc[p * nc + 8 * (j - j0) + sl];
 }
 
 float silu_mul(float g, float u) { return u * (g / (1.0f + expf(-g))); }
@@ -274,20 +292,23 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
       pgu[p] = &gu[p * N13];
       pout[p] = &out[p * H];
     }
-    // gate_up: tasks of (cold expert with pairs, row block)
+    // gate_up: tasks of (cold expert with pairs, row block); W4A16 blocks of
+    // aw packed words, the widest that still gives every thread 2 tasks
     std::vector<int64_t> task_c;
-    const int64_t blk13 = awq ? (N13 / 8) / kAwqWords : N13 / kQRows;
-    const int64_t blk2 = awq ? (H / 8) / kAwqWords : H / kQRows;
     for (int64_t c = 0; c < Ec; ++c)
       if (start[c + 1] > start[c]) task_c.push_back(c);
     const int64_t nc = (int64_t)task_c.size();
+    int aw = kAwqWordsMax;
+    while (aw > 2 && nc * ((N13 / 8) / aw) < 2 * (int64_t)pool.size()) aw /= 2;
+    const int64_t blk13 = awq ? (N13 / 8) / aw : N13 / kQRows;
+    const int64_t blk2 = awq ? (H / 8) / aw : H / kQRows;
     pool.run(nc * blk13, [&](int64_t task) {
       const int64_t c = task_c[task / blk13], b = task % blk13, p0 = start[c], np = start[c + 1] - p0;
       if (awq) {
         awq_cols(reinterpret_cast<const int32_t*>(cs.arr[0].data() + c * eb[0]),
                  reinterpret_cast<const int32_t*>(cs.arr[1].data() + c * eb[1]),
                  reinterpret_cast<const uint16_t*>(cs.arr[2].data() + c * eb[2]), cs.scale_dtype, H, N13,
-                 b * kAwqWords, (b + 1) * kAwqWords, &pxf[p0], &pxs[p0], np, &pgu[p0]);
+                 b * aw, (b + 1) * aw, &pxf[p0], &pxs[p0], np, &pgu[p0]);
       } else {
         q_rows(cs.quant, cs.scale_dtype, cs.arr[0].data() + c * eb[0],
                reinterpret_cast<const uint16_t*>(cs.arr[1].data() + c * eb[1]), H, b * kQRows, (b + 1) * kQRows,
@@ -323,7 +344,7 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
         awq_cols(reinterpret_cast<const int32_t*>(cs.arr[3].data() + c * eb[3]),
                  reinterpret_cast<const int32_t*>(cs.arr[4].data() + c * eb[4]),
                  reinterpret_cast<const uint16_t*>(cs.arr[5].data() + c * eb[5]), cs.scale_dtype, I, H,
-                 b * kAwqWords, (b + 1) * kAwqWords, &pxf[p0], &pxs[p0], np, &pout[p0]);
+                 b * aw, (b + 1) * aw, &pxf[p0], &pxs[p0], np, &pout[p0]);
       } else {
         q_rows(cs.quant, cs.scale_dtype, cs.arr[2].data() + c * eb[2],
                reinterpret_cast<const uint16_t*>(cs.arr[3].data() + c * eb[3]), I, b * kQRows, (b + 1) * kQRows,

@@ -8,9 +8,10 @@
 //   S: event "in" ............ remap ids (cold -> -1, hot -> slot) -> device
 //      forward of the hot experts into y ............ wait "part" -> y += part
 //   D: wait "in" -> copy x, ids, topk_w to pinned host buffers -> host
-//      callback: cold experts on the host pool -> copy the fp32 partial to the
-//      device -> event "part"
-// so the host experts overlap the device kernels.  The reference's NPU op
+//      callback: cold experts on the host pool, fp32 partial into pinned host
+//      memory -> event "part"
+// so the host experts overlap the device kernels; the add kernel reads the
+// partial from the pinned buffer (no copy command).  The reference's NPU op
 // does the whole layer in such a callback (moe_forward_npu_stream,
 // Int8-gemm/nanovllm_ops.cpp:244-305); the per-expert split is its roadmap
 // (README.md:124-134: hot experts resident in device memory, cold ones on the
@@ -96,7 +97,8 @@ __global__ void remap_ids_kernel(const int32_t* __restrict__ ids, const int32_t*
   }
 }
 
-// y = round(y + part) (has_dev) or round(part): 4 values per thread (H % 32 == 0)
+// y = round(y + part) (has_dev) or round(part): 4 values per thread (H % 32 == 0);
+// part is pinned host memory written by the host callback before event "part".
 template <int ACT>
 __global__ void add_partial_kernel(uint16_t* __restrict__ y, const float* __restrict__ part, int64_t n4,
                                    int has_dev) {
@@ -133,12 +135,13 @@ struct mi_moe_hybrid {
   mimoe_host::ColdSet cold;
   std::unique_ptr<mimoe_host::Pool> pool;
   std::mutex host_mu;                // host forwards run one at a time
-  DBuf slot_dev, ids_dev, part_dev;
+  DBuf slot_dev, ids_dev;
   PinBuf x_h, ids_h, w_h, part_h;
   int64_t cap_T = 0, cap_n = 0;
   hipStream_t side = nullptr;
   hipEvent_t ev_in = nullptr, ev_part = nullptr;
   std::atomic<double> last_host_ms{-1.0};
+  std::atomic<double> last_queue_ms{-1.0};   // forward call -> start of its host callback
   std::atomic<int64_t> last_pairs{0};
   std::atomic<int> host_error{0};    // a host callback failed (reported by the next call)
 };
@@ -149,6 +152,7 @@ struct CallCtx {
   mi_moe_hybrid* hh;
   int64_t T, K;
   int act;
+  std::chrono::steady_clock::time_point enqueued;
 };
 
 void run_host(mi_moe_hybrid* hh, const uint16_t* x, int act, const int32_t* ids, const float* w, int64_t T,
@@ -165,6 +169,8 @@ void run_host(mi_moe_hybrid* hh, const uint16_t* x, int act, const int32_t* ids,
 void host_callback(void* arg) {
   std::unique_ptr<CallCtx> ctx(static_cast<CallCtx*>(arg));
   mi_moe_hybrid* hh = ctx->hh;
+  hh->last_queue_ms.store(
+      std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - ctx->enqueued).count());
   try {
     run_host(hh, (const uint16_t*)hh->x_h.p, ctx->act, (const int32_t*)hh->ids_h.p, (const float*)hh->w_h.p,
              ctx->T, ctx->K, (float*)hh->part_h.p);
@@ -192,7 +198,6 @@ int grow(mi_moe_hybrid* hh, int64_t T, int64_t n, hipStream_t st) {
   HCHK(hipStreamSynchronize(hh->side));
   HCHK(hh->x_h.alloc((size_t)capT * hh->H * 2));
   HCHK(hh->part_h.alloc((size_t)capT * hh->H * sizeof(float)));
-  HCHK(hh->part_dev.alloc((size_t)capT * hh->H * sizeof(float)));
   HCHK(hh->ids_h.alloc((size_t)capn * sizeof(int32_t)));
   HCHK(hh->w_h.alloc((size_t)capn * sizeof(float)));
   HCHK(hh->ids_dev.alloc((size_t)capn * sizeof(int32_t)));
@@ -296,7 +301,7 @@ MI_API int mi_moe_hybrid_destroy(mi_moe_hybrid* hh) {
   if (hh->side) (void)hipStreamSynchronize(hh->side);
   if (hh->device >= 0) (void)hipDeviceSynchronize();
   if (hh->dev) mi_moe_destroy(hh->dev);
-  hh->slot_dev.release(); hh->ids_dev.release(); hh->part_dev.release();
+  hh->slot_dev.release(); hh->ids_dev.release();
   hh->x_h.release(); hh->ids_h.release(); hh->w_h.release(); hh->part_h.release();
   if (hh->ev_in) (void)hipEventDestroy(hh->ev_in);
   if (hh->ev_part) (void)hipEventDestroy(hh->ev_part);
@@ -377,14 +382,13 @@ MI_API int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y, cons
   HCHK(hipMemcpyAsync(hh->x_h.p, x, (size_t)(T * H) * 2, hipMemcpyDeviceToHost, hh->side));
   HCHK(hipMemcpyAsync(hh->ids_h.p, topk_ids, (size_t)n * sizeof(int32_t), hipMemcpyDeviceToHost, hh->side));
   HCHK(hipMemcpyAsync(hh->w_h.p, topk_w, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, hh->side));
-  CallCtx* ctx = new (std::nothrow) CallCtx{hh, T, K, act_dtype};
+  CallCtx* ctx = new (std::nothrow) CallCtx{hh, T, K, act_dtype, std::chrono::steady_clock::now()};
   if (!ctx) return hfail(MI_MOE_EINVAL, "out of host memory");
   hipError_t e = hipLaunchHostFunc(hh->side, host_callback, ctx);
   if (e != hipSuccess) {
     delete ctx;
     return hfail(MI_MOE_EHIP, "hipLaunchHostFunc failed: %s", hipGetErrorString(e));
   }
-  HCHK(hipMemcpyAsync(hh->part_dev.p, hh->part_h.p, (size_t)(T * H) * sizeof(float), hipMemcpyHostToDevice, hh->side));
   HCHK(hipEventRecord(hh->ev_part, hh->side));
   // caller stream: the hot experts on the device
   if (hh->dev) {
@@ -400,10 +404,10 @@ MI_API int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y, cons
   const int grid = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
   if (act_dtype == MI_MOE_BF16)
     hipLaunchKernelGGL(add_partial_kernel<1>, dim3(grid), dim3(256), 0, st, (uint16_t*)y,
-                       (const float*)hh->part_dev.p, n4, hh->dev ? 1 : 0);
+                       (const float*)hh->part_h.p, n4, hh->dev ? 1 : 0);
   else
     hipLaunchKernelGGL(add_partial_kernel<0>, dim3(grid), dim3(256), 0, st, (uint16_t*)y,
-                       (const float*)hh->part_dev.p, n4, hh->dev ? 1 : 0);
+                       (const float*)hh->part_h.p, n4, hh->dev ? 1 : 0);
   HCHK(hipGetLastError());
   return MI_MOE_OK;
 }
@@ -426,7 +430,8 @@ MI_API int mi_moe_hybrid_host_forward(mi_moe_hybrid* hh, const void* x_host, con
 }
 
 MI_API int mi_moe_hybrid_get_stats(mi_moe_hybrid* hh, int64_t* device_experts, int64_t* host_experts,
-                                   int64_t* host_weight_bytes, double* last_host_ms, int64_t* last_host_pairs) {
+                                   int64_t* host_weight_bytes, double* last_host_ms, int64_t* last_host_pairs,
+                                   double* last_queue_ms) {
   if (!hh) return hfail(MI_MOE_EINVAL, "null hybrid handle");
   if (device_experts) *device_experts = hh->Eg;
   if (host_experts) *host_experts = hh->cold.Ec;
@@ -437,5 +442,6 @@ MI_API int mi_moe_hybrid_get_stats(mi_moe_hybrid* hh, int64_t* device_experts, i
   }
   if (last_host_ms) *last_host_ms = hh->last_host_ms.load();
   if (last_host_pairs) *last_host_pairs = hh->last_pairs.load();
+  if (last_queue_ms) *last_queue_ms = hh->last_queue_ms.load();
   return MI_MOE_OK;
 }

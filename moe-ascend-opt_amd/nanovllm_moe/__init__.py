@@ -97,7 +97,7 @@ def capi():
     L.mi_moe_hybrid_store_awq.argtypes = [P, P, P, P, P, P, P, I64, I, I, P]
     L.mi_moe_hybrid_forward.argtypes = [P, P, P, P, P, I64, I64, I, P]
     L.mi_moe_hybrid_host_forward.argtypes = [P, P, P, P, I64, I64, I, P]
-    L.mi_moe_hybrid_get_stats.argtypes = [P, P, P, P, P, P]
+    L.mi_moe_hybrid_get_stats.argtypes = [P, P, P, P, P, P, P]
     for name in C_SYMBOLS:
         fn = getattr(L, name)
         if fn.restype is ctypes.c_int or fn.restype is None:

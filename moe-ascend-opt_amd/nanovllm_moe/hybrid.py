@@ -107,8 +107,9 @@ class HybridMoE:
     def stats(self) -> dict:
         from . import check
         dev, host, hb, pairs = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
-        ms = ctypes.c_double()
+        ms, qms = ctypes.c_double(), ctypes.c_double()
         check(self._L.mi_moe_hybrid_get_stats(self._h, ctypes.byref(dev), ctypes.byref(host), ctypes.byref(hb),
-                                              ctypes.byref(ms), ctypes.byref(pairs)), "mi_moe_hybrid_get_stats")
+                                              ctypes.byref(ms), ctypes.byref(pairs), ctypes.byref(qms)),
+              "mi_moe_hybrid_get_stats")
         return {"device_experts": dev.value, "host_experts": host.value, "host_weight_bytes": hb.value,
-                "last_host_ms": ms.value, "last_host_pairs": pairs.value}
+                "last_host_ms": ms.value, "last_host_pairs": pairs.value, "last_queue_ms": qms.value}

@@ -136,7 +136,7 @@ def test_hybrid_host_only_handle_errors():
     assert L.mi_moe_hybrid_host_forward(h, p(x), p(w), p(ids), 2, 1, 1, p(y)) == 2   # not loaded
     assert L.mi_moe_hybrid_host_forward(h, p(x), p(w), p(ids), 2, 0, 1, p(y)) in (1, 2)
     dev, host, hb = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
-    assert L.mi_moe_hybrid_get_stats(h, ctypes.byref(dev), ctypes.byref(host), ctypes.byref(hb), None, None) == 0
+    assert L.mi_moe_hybrid_get_stats(h, ctypes.byref(dev), ctypes.byref(host), ctypes.byref(hb), None, None, None) == 0
     assert (dev.value, host.value, hb.value) == (0, E, 0)
     assert L.mi_moe_hybrid_destroy(h) == 0
 
