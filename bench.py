@@ -458,7 +458,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the single-GPU kernel is the unit of work, see DESIGN.md for sharding.",
+              "the single-GPU kernel is the unit of work (several GPUs would each run it on E/N "
+              "experts and sum y with one all-reduce).",
               file=sys.stderr)
         sys.exit(2)
     if args.copy_calibration:

@@ -423,8 +423,9 @@ void w4a16_down_token_kernel(W4Args a) {
 
 // ================================================================ grouped GEMMs (sorted path)
 // Work item: a row tile (up to kGemmRows = 64 routed rows of one expert, from
-// the routing kernel's tile list) x a 64-row block of the output, one wave per
-// 16-row tile of the block and all of K per wave, so no cross-wave reduction.
+// the routing kernel's tile list) x a block of output rows (gate_up: 8 gate/up
+// slices; down: 4 quads of 64 rows), each wave owning 16-row weight tiles of
+// the block over all of K, so no cross-wave reduction.
 // Per 128-k group the workgroup stages the tile's activation rows (bf16, row
 // stride kGemmRowStride) and their sums into LDS, double-buffered with one
 // barrier per group; each wave holds its 16 weight rows of the group (16 B per
@@ -443,8 +444,8 @@ void w4a16_down_token_kernel(W4Args a) {
 constexpr int kGemmRowStride = 272;   // 256 B of a row + 16 B that spread the rows over the LDS banks
 constexpr int kGemmABytes = kGemmRows * kGemmRowStride;
 // LDS: staged rows [2][kGemmABytes] | row sums [2][kGemmRows] f32 | pair of each row [kGemmRows]
-// | the workgroup's metadata (gemm13: 4 slice blocks of 80*G1 B; gemm2: 4
-// sections of w2_meta_sec_bytes(G2) B)
+// | the workgroup's metadata (gemm13: 4 * kGemm13Blocks slice blocks of 80*G1 B;
+// gemm2: 4 * kGemm2Quads sections of w2_meta_sec_bytes(G2) B)
 constexpr size_t kGemmLds = 2 * (size_t)kGemmABytes + 3 * kGemmRows * sizeof(float);
 
 // Copy nbytes (a multiple of 16) from global to LDS with the workgroup's
