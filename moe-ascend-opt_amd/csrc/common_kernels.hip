@@ -31,43 +31,6 @@ __device__ __forceinline__ uint64_t route_match(int e, bool valid, int nbits) {
   return m;
 }
 
-// One wave: per-expert counts of ids[lo, hi) added into mine[E].
-__device__ void route_wave_count(const int32_t* __restrict__ ids, int lo, int hi, int E, int nbits,
-                                 int lane, int* mine) {
-  for (int b0 = lo; b0 < hi; b0 += kWave) {
-    const int i = b0 + lane;
-    const int e = (i < hi) ? ids[i] : -1;
-    const bool valid = (i < hi) && ((unsigned)e < (unsigned)E);
-    const uint64_t m = route_match(e, valid, nbits);
-    if (valid && __ffsll((long long)m) - 1 == lane) mine[e] += __popcll(m);
-    __builtin_amdgcn_wave_barrier();
-  }
-}
-
-// One wave: ranks of ids[lo, hi) from the running bases mine[E].
-__device__ void route_wave_rank(const int32_t* __restrict__ ids, int lo, int hi, int K, int E, int nbits,
-                                int lane, int* mine, int32_t* tok, int32_t* scat, int tok_div) {
-  for (int b0 = lo; b0 < hi; b0 += kWave) {
-    const int i = b0 + lane;
-    const int e = (i < hi) ? ids[i] : -1;
-    const bool valid = (i < hi) && ((unsigned)e < (unsigned)E);
-    const uint64_t m = route_match(e, valid, nbits);
-    int add = 0;
-    if (valid) {
-      const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
-      const int pos = mine[e] + __popcll(m & lt);
-      scat[i] = pos;
-      tok[pos] = tok_div ? i / K : i;
-      if (__ffsll((long long)m) - 1 == lane) add = __popcll(m);
-    } else if (i < hi) {
-      scat[i] = -1;
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (add) mine[e] += add;
-    __builtin_amdgcn_wave_barrier();
-  }
-}
-
 // Wave 0: per-expert totals counts[E] (LDS) -> counts_out, starts_out, the
 // active list, U and the row tiles; counts[] becomes the starts.
 __device__ void route_finish(int* counts, int E, int lane, int32_t* counts_out, int32_t* starts_out,
@@ -122,42 +85,97 @@ __device__ __forceinline__ int route_bits(int E) {
   return nbits;
 }
 
-// One workgroup for all n ids.  LDS: (kRouteWaves + 1) * E ints (E <= 512).
+// A wave's ids (up to kRouteSegIter batches of 64) and their match masks,
+// kept in registers between the counting and the ranking pass.
+constexpr int kRouteSegIter = 4;
+struct RouteSeg {
+  int e[kRouteSegIter];
+  uint64_t m[kRouteSegIter];
+};
+
+// Counting pass over ids[lo, hi) (hi - lo <= 64 * kRouteSegIter): per-expert
+// counts added into mine[E], ids and masks kept in seg.
+__device__ __forceinline__ void route_seg_count(const int32_t* __restrict__ ids, int lo, int hi, int E, int nbits,
+                                                int lane, int* mine, RouteSeg& seg) {
+#pragma unroll
+  for (int it = 0; it < kRouteSegIter; ++it) {
+    const int i = lo + 64 * it + lane;
+    int e = -1;
+    uint64_t m = 0;
+    if (lo + 64 * it < hi) {   // uniform
+      e = (i < hi) ? ids[i] : -1;
+      const bool valid = (i < hi) && ((unsigned)e < (unsigned)E);
+      m = route_match(e, valid, nbits);
+      if (!valid) e = -1;
+      if (valid && __ffsll((long long)m) - 1 == lane) mine[e] += __popcll(m);
+      __builtin_amdgcn_wave_barrier();
+    }
+    seg.e[it] = e;
+    seg.m[it] = m;
+  }
+}
+
+// Ranking pass: pos = base[e] (if base) + mine[e] (this wave's running
+// offset) + rank within the batch; scat[i] = pos and tok[pos] = the token
+// (tok_div) or pair index, scat[i] = -1 for an invalid id.
+__device__ __forceinline__ void route_seg_rank(int lo, int hi, int K, const int* base, int lane, int* mine,
+                                               const RouteSeg& seg, int32_t* tok, int32_t* scat, int tok_div) {
+  const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+#pragma unroll
+  for (int it = 0; it < kRouteSegIter; ++it) {
+    if (lo + 64 * it >= hi) break;   // uniform
+    const int i = lo + 64 * it + lane, e = seg.e[it];
+    const uint64_t m = seg.m[it];
+    int add = 0;
+    if (e >= 0) {
+      const int pos = (base ? base[e] : 0) + mine[e] + __popcll(m & lt);
+      scat[i] = pos;
+      tok[pos] = tok_div ? i / K : i;
+      if (__ffsll((long long)m) - 1 == lane) add = __popcll(m);
+    } else if (i < hi) {
+      scat[i] = -1;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (add) mine[e] += add;
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// One workgroup for n <= kRouteMultiMin ids: each wave counts its segment
+// (ids kept in registers), the per-wave counts give the totals and the
+// exclusive prefix over waves, then the segments are ranked.
+// LDS: (kRouteWaves + 1) * E ints (E <= 512).
+static_assert(kRouteMultiMin <= kRouteThreads * kRouteSegIter, "a wave segment fits kRouteSegIter batches");
 __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
     const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
     int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out,
     int tok_div, int32_t* tiles_out, int32_t* ntiles_out) {
   extern __shared__ int lds[];
-  int* counts = lds;            // [E]
+  int* counts = lds;            // [E]: totals, then the starts
   int* cw = lds + E;            // [kRouteWaves][E]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int e = tid; e < E; e += kRouteThreads) counts[e] = 0;
   for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) cw[i] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += kRouteThreads) {
-    const int e = ids[i];
-    if ((unsigned)e < (unsigned)E) atomicAdd(&counts[e], 1);
-  }
-  __syncthreads();
-  if (tid < kWave) route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out);
-  __syncthreads();
   const int nbits = route_bits(E);
-  const int seg = ((n + kRouteWaves - 1) / kRouteWaves + kWave - 1) / kWave * kWave;
-  const int lo = wave * seg, hi = min(n, lo + seg);
+  const int segw = ((n + kRouteWaves - 1) / kRouteWaves + kWave - 1) / kWave * kWave;
+  const int lo = wave * segw, hi = min(n, lo + segw);
   int* mine = cw + wave * E;
-  route_wave_count(ids, lo, hi, E, nbits, lane, mine);
+  RouteSeg seg;
+  route_seg_count(ids, lo, hi, E, nbits, lane, mine, seg);
   __syncthreads();
-  // prefix over waves, seeded with starts
-  for (int e = tid; e < E; e += kRouteThreads) {
-    int run = counts[e];
+  for (int e = tid; e < E; e += kRouteThreads) {   // exclusive prefix over waves; totals
+    int run = 0;
     for (int w = 0; w < kRouteWaves; ++w) {
       const int c = cw[w * E + e];
       cw[w * E + e] = run;
       run += c;
     }
+    counts[e] = run;
   }
   __syncthreads();
-  route_wave_rank(ids, lo, hi, K, E, nbits, lane, mine, tok, scat, tok_div);
+  if (tid < kWave) route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out);
+  __syncthreads();
+  route_seg_rank(lo, hi, K, counts, lane, mine, seg, tok, scat, tok_div);
 }
 
 // Multi-workgroup routing, step 1: the expert histogram of one chunk of ids.
@@ -214,10 +232,12 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(const int3
   for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) cw[i] = 0;
   __syncthreads();
   const int nbits = route_bits(E);
-  constexpr int seg = kRouteChunk / kRouteWaves;
-  const int lo = min(n, c * kRouteChunk + wave * seg), hi = min(n, lo + seg);
+  constexpr int segw = kRouteChunk / kRouteWaves;
+  static_assert(segw <= 64 * kRouteSegIter, "a wave segment fits kRouteSegIter batches");
+  const int lo = min(n, c * kRouteChunk + wave * segw), hi = min(n, lo + segw);
   int* mine = cw + wave * E;
-  route_wave_count(ids, lo, hi, E, nbits, lane, mine);
+  RouteSeg seg;
+  route_seg_count(ids, lo, hi, E, nbits, lane, mine, seg);
   __syncthreads();
   for (int e = tid; e < E; e += kRouteThreads) {
     int run = chunk_base[(size_t)c * E + e];
@@ -228,13 +248,14 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(const int3
     }
   }
   __syncthreads();
-  route_wave_rank(ids, lo, hi, K, E, nbits, lane, mine, tok, scat, tok_div);
+  route_seg_rank(lo, hi, K, nullptr, lane, mine, seg, tok, scat, tok_div);
 }
 
 // tok_div = 0: tok[] holds pair indices t*K+k (fused kernels); 1: token ids.
 hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const RouteGlobal& rg,
                                hipStream_t st, int tok_div) {
-  if (n > kRouteMultiMin && rg.chunk) {
+  if (n > kRouteMultiMin) {
+    if (!rg.chunk) return hipErrorInvalidValue;   // the chunked routing needs its scratch
     const int C = (n + kRouteChunk - 1) / kRouteChunk;
     hipLaunchKernelGGL(route_count_kernel, dim3(C), dim3(kRouteCountThreads), (size_t)E * sizeof(int), st, ids,
                        n, E, rg.chunk);
