@@ -189,7 +189,8 @@ def time_eager(torch, op_out, calls, out, warmup):
 
 def run_config(cfg, steps, warmup, eager=False):
     """The other BASELINE configurations, as one JSON line each (not the
-    headline line): 3 = Q4_0 prefill, Qwen3 shape, T 32..4096; 4 = MiniMax-M2
+    headline line): 1 = Q8_0, Qwen3 shape, T = 1 (the reference CPU
+    configuration, here on the GPU; bs 2/4/8 beside it); 3 = Q4_0 prefill, Qwen3 shape, T 32..4096; 4 = MiniMax-M2
     W4A16, bs 1/8/64; 5 = Zipf-skewed routing (p ~ r^-1.2), T = 512, Qwen3
     W4A16.  Weights are random in the format (timing does not depend on the
     values); enough copies rotate that the 256 MB Infinity Cache cannot hold
@@ -206,7 +207,9 @@ def run_config(cfg, steps, warmup, eager=False):
         v = torch.randint(0, 2**32, shape, generator=g, dtype=torch.int64, device=dev)
         return torch.where(v >= 2**31, v - 2**32, v).to(torch.int32)
 
-    if cfg == 3:
+    if cfg == 1:
+        E_, H_, I_, K_, quant, Ts, copies = 128, 2048, 768, 8, 0, (1, 2, 4, 8), 4
+    elif cfg == 3:
         E_, H_, I_, K_, quant, Ts, copies = 128, 2048, 768, 8, 1, (32, 128, 1024, 4096), 2
     elif cfg == 4:
         E_, H_, I_, K_, quant, Ts, copies = 256, 3072, 1536, 8, 2, (1, 8, 64), 4
@@ -215,7 +218,14 @@ def run_config(cfg, steps, warmup, eager=False):
     handles = []
     for _ in range(copies):
         h = torch.classes.nanovllm.MoEInfer(E_, H_, I_, quant)
-        if quant == 1:
+        if quant == 0:
+            q13 = torch.randint(-127, 128, (E_, 2 * I_, H_), generator=g, dtype=torch.int8, device=dev)
+            q2 = torch.randint(-127, 128, (E_, H_, I_), generator=g, dtype=torch.int8, device=dev)
+            d13 = (torch.rand(E_, 2 * I_, H_ // 32, generator=g, device=dev) * 1e-3).half()
+            d2 = (torch.rand(E_, H_, I_ // 32, generator=g, device=dev) * 1e-3).half()
+            h.store_quantized_repack(q13, d13, q2, d2)
+            del q13, q2
+        elif quant == 1:
             q13, d13 = fmt.q4_0_random((E_, 2 * I_), H_, generator=g, device=dev)
             q2, d2 = fmt.q4_0_random((E_, H_), I_, generator=g, device=dev)
             h.store_quantized_repack(q13, d13, q2, d2)
@@ -260,7 +270,8 @@ def run_config(cfg, steps, warmup, eager=False):
             per[str(T)]["routing_histogram"] = {"max_rows": int(c.max()), "min_rows": int(c.min()),
                                                 "experts_at_zero": int((c == 0).sum())}
         log(f"[bench config {cfg}] T={T}: {us:.2f} us/layer, {per[str(T)]['GB_per_s']} GB/s")
-    names = {3: "Q4_0 prefill, Qwen3-30B-A3B shape (H=2048, I=768, E=128, top-8), Q8_0 activations",
+    names = {1: "Q8_0 (fp16 d per 32), Qwen3-30B-A3B shape (H=2048, I=768, E=128, top-8), Q8_0 activations",
+             3: "Q4_0 prefill, Qwen3-30B-A3B shape (H=2048, I=768, E=128, top-8), Q8_0 activations",
              4: "W4A16, MiniMax-M2 shape (H=3072, I=1536, E=256, top-8, group 128)",
              5: "W4A16, Qwen3-30B-A3B shape, Zipf-skewed routing (p ~ r^-1.2, distinct top-8)"}
     print(json.dumps({"config_id": cfg, "workload": names[cfg], "unit": "us/layer and GB/s",
@@ -447,9 +458,9 @@ def main():
     ap.add_argument("--traffic-file", type=str,
                     default=os.path.join(ROOT, "profiles", "w4a16_decode_traffic_qwen3_bs8.txt"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
-                    help="BASELINE configuration: 2 (default) is the headline line; 3/4/5 print a "
-                         "measurement line for Q4_0 prefill / MiniMax / Zipf routing")
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
+                    help="BASELINE configuration: 2 (default) is the headline line; 1/3/4/5 print a "
+                         "measurement line for Q8_0 decode / Q4_0 prefill / MiniMax / Zipf routing")
     ap.add_argument("--offload", type=int, default=0, metavar="NCOLD",
                     help="hybrid CPU-offload executor with NCOLD experts on the host (one JSON line)")
     ap.add_argument("--host-threads", type=int, default=0)
