@@ -125,16 +125,54 @@ __device__ __forceinline__ float quant_block_q8_0(const float (&v)[32], int8_t* 
   return d;
 }
 
+// Integer decode path (lane-per-row kernels): the NW waves of a workgroup
+// split K, and a wave's first batch of weight groups is issued before the
+// activations are staged.  NW = 8 for the smallest calls (kQDecWideMaxPairs
+// routed pairs or fewer: few workgroups, each wave's chain is shorter), 4
+// above (occupancy).
+constexpr int kQDecWavesMax = 8;
+constexpr int kQDecWideMaxPairs = 8;
+
+// One lane's row weights (whole 4-block layout groups, as 16-byte loads) and
+// the blocks' raw scale bits for up to NG groups: 32 VGPRs of weights.
+template <int QT>
+struct QRowBatch {
+  static constexpr int NV = 4 * QFmt<QT>::chunks;   // 16-byte loads per group
+  static constexpr int NG = QT == 0 ? 1 : 2;        // groups per batch
+  u32x4_t v[NG][NV];
+  uint32_t sw[NG][4];
+};
+
+// Issue the loads of the whole groups gs, gs+4, .. (up to NG) that start below
+// kb1 and lie inside the row (g + 4 <= KB); a partial last group is left to
+// rows_dot's per-block tail.
+template <int QT>
+__device__ __forceinline__ void rows_issue(QRowBatch<QT>& B, const char* wtile, const uint16_t* stile, int lane,
+                                           int gs, int kb1, int KB) {
+#pragma unroll
+  for (int j = 0; j < QRowBatch<QT>::NG; ++j) {
+    const int g0 = gs + 4 * j;
+    if (g0 < kb1 && g0 + 4 <= KB) {   // uniform
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(wtile + QLay<QT>::off(KB, g0, lane, 0));
+#pragma unroll
+      for (int i = 0; i < QRowBatch<QT>::NV; ++i) B.v[j][i] = p[i];
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) B.sw[j][bb] = stile[(g0 + bb) * 64 + lane];
+    }
+  }
+}
+
 // Dot of this lane's weight row against the staged activations for k blocks
-// [kb0, kb1), accumulating into acc[c] for the cntp staged tokens.  Whole
-// layout groups are read; blocks of a group outside the range are skipped
-// (the neighbouring wave reads the same group, mostly from the cache).
+// [kb0, kb1), accumulating into acc[c] for the cntp staged tokens, block by
+// block in ascending order.  B holds the first batch (rows_issue at
+// kb0 & ~3) when `issued`; later batches are loaded here.  Blocks of a group
+// outside the range are skipped (the neighbouring wave reads the same group,
+// mostly from the cache).
 template <int QT, int SC>
-__device__ __forceinline__ void rows_dot(const char* wtile, const uint16_t* stile, int lane, int kb0,
-                                         int kb1, const int8_t* xq, const float* xd, const int* xs,
-                                         int K, int KB, int cntp, float (&acc)[kQTokPerPass]) {
-  auto block = [&](int kb, const u32x4_t& w0, const u32x4_t& w1) {
-    const float dw = to_f32<SC>(stile[kb * 64 + lane]);
+__device__ __forceinline__ void rows_dot(QRowBatch<QT>& B, bool issued, const char* wtile, const uint16_t* stile,
+                                         int lane, int kb0, int kb1, const int8_t* xq, const float* xd,
+                                         const int* xs, int K, int KB, int cntp, float (&acc)[kQTokPerPass]) {
+  auto block = [&](int kb, const u32x4_t& w0, const u32x4_t& w1, float dw) {
     int wd[8];
     unpack_w<QT>(w0, w1, wd);
 #pragma unroll
@@ -147,33 +185,35 @@ __device__ __forceinline__ void rows_dot(const char* wtile, const uint16_t* stil
       acc[cc] = acc[cc] + t2;
     }
   };
-  for (int g0 = kb0 & ~3; g0 < kb1; g0 += 4) {
-    if (g0 + 4 <= KB) {
-      // the row's whole group: 4 (Q4_0) or 8 (Q8_0) 16-byte loads
-      constexpr int NV = 4 * QFmt<QT>::chunks;
-      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(wtile + QLay<QT>::off(KB, g0, lane, 0));
-      u32x4_t v[NV];
+  constexpr int NG = QRowBatch<QT>::NG;
+  const int gs0 = kb0 & ~3, KBw = KB & ~3;   // KBw: end of the whole groups
+  for (int gs = gs0; gs < kb1 && gs < KBw; gs += 4 * NG) {
+    if (gs != gs0 || !issued) rows_issue<QT>(B, wtile, stile, lane, gs, kb1, KB);
 #pragma unroll
-      for (int i = 0; i < NV; ++i) v[i] = p[i];
+    for (int j = 0; j < NG; ++j) {
+      const int g0 = gs + 4 * j;
+      if (g0 >= kb1 || g0 >= KBw) break;   // uniform
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        if (g0 + b < kb0 || g0 + b >= kb1) continue;   // uniform
+      for (int bb = 0; bb < 4; ++bb) {
+        if (g0 + bb < kb0 || g0 + bb >= kb1) continue;   // uniform
+        const float dw = to_f32<SC>(B.sw[j][bb]);
         if constexpr (QT == 1) {
-          block(g0 + b, u32x4_t{v[0][b], v[1][b], v[2][b], v[3][b]}, u32x4_t{0, 0, 0, 0});
+          block(g0 + bb, u32x4_t{B.v[j][0][bb], B.v[j][1][bb], B.v[j][2][bb], B.v[j][3][bb]},
+                u32x4_t{0, 0, 0, 0}, dw);
         } else {
-          // quarter q of block b: dwords 2b, 2b+1 of the 32-byte run v[2q], v[2q+1]
-          const int h = 2 * (b & 1), i = b >> 1;
-          block(g0 + b, u32x4_t{v[i][h], v[i][h + 1], v[2 + i][h], v[2 + i][h + 1]},
-                u32x4_t{v[4 + i][h], v[4 + i][h + 1], v[6 + i][h], v[6 + i][h + 1]});
+          // quarter q of block bb: dwords 2bb, 2bb+1 of the 32-byte run v[2q], v[2q+1]
+          const int h = 2 * (bb & 1), i = bb >> 1;
+          block(g0 + bb, u32x4_t{B.v[j][i][h], B.v[j][i][h + 1], B.v[j][2 + i][h], B.v[j][2 + i][h + 1]},
+                u32x4_t{B.v[j][4 + i][h], B.v[j][4 + i][h + 1], B.v[j][6 + i][h], B.v[j][6 + i][h + 1]}, dw);
         }
       }
-    } else {
-      for (int kb = max(g0, kb0); kb < kb1; ++kb) {
-        u32x4_t w0, w1;
-        load_block<QT>(wtile, KB, kb, lane, w0, w1);
-        block(kb, w0, w1);
-      }
     }
+  }
+  // a partial last group (KB % 4 != 0): per-block loads
+  for (int kb = max(kb0, KBw); kb < kb1; ++kb) {
+    u32x4_t w0, w1;
+    load_block<QT>(wtile, KB, kb, lane, w0, w1);
+    block(kb, w0, w1, to_f32<SC>(stile[kb * 64 + lane]));
   }
 }
 
@@ -181,7 +221,7 @@ struct QLds {
   int8_t* xq;   // [kQTokPerPass][Kmax]
   float* xd;    // [kQTokPerPass][KBmax]
   int* xs;      // [kQTokPerPass][KBmax]
-  float* red;   // [4][kQTokPerPass][64]
+  float* red;   // [kQDecWavesMax][kQTokPerPass][64]
   int* route;
 };
 
@@ -192,27 +232,30 @@ __device__ __forceinline__ QLds carve(unsigned char* smem, int Kmax) {
   L.xd = reinterpret_cast<float*>(smem + kQTokPerPass * Kmax);
   L.xs = reinterpret_cast<int*>(L.xd + kQTokPerPass * KBmax);
   L.red = reinterpret_cast<float*>(L.xs + kQTokPerPass * KBmax);
-  L.route = reinterpret_cast<int*>(L.red + 4 * kQTokPerPass * 64);
+  L.route = reinterpret_cast<int*>(L.red + kQDecWavesMax * kQTokPerPass * 64);
   return L;
 }
 
 // ---------------------------------------------------------------- phase 1
-template <int QT, int ACT, int SC>
+template <int QT, int ACT, int SC, int NW>
 __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, const QLds& L) {
   const SchedArgs& c = a.c;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int e = rv.active[ui];
   const int p0 = rv.starts[e], cnt = rv.starts[e + 1] - p0;
   const int KB = c.H / 32, S = c.I / 32;
-  const int kb0 = KB * wave / 4, kb1 = KB * (wave + 1) / 4;
+  const int kb0 = KB * wave / NW, kb1 = KB * (wave + 1) / NW;
   const size_t tile = (size_t)e * S + sl;
   const char* wtile = (const char*)a.w13 + tile * KB * QFmt<QT>::block_bytes;
   const uint16_t* stile = a.w13_d + tile * KB * 64;
+  // the first weight batch is in flight while the activations are staged
+  QRowBatch<QT> B;
+  rows_issue<QT>(B, wtile, stile, lane, kb0 & ~3, kb1, KB);
 
   for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
     const int cntp = min(kQTokPerPass, cnt - cb0);
     // Stage A for the staged tokens (Int8-gemm/q8_gemm.cpp:360-377)
-    for (int idx = tid; idx < cntp * KB; idx += kBlock) {
+    for (int idx = tid; idx < cntp * KB; idx += NW * kWave) {
       const int cc = idx / KB, kb = idx - cc * KB;
       const int t = rv.pair[p0 + cb0 + cc] / c.K;
       const u32x4_t* src = reinterpret_cast<const u32x4_t*>(c.x + (size_t)t * c.H + kb * 32);
@@ -235,19 +278,19 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
     float acc[kQTokPerPass];
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
-    rows_dot<QT, SC>(wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.H, KB, cntp, acc);
+    rows_dot<QT, SC>(B, cb0 == 0, wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.H, KB, cntp, acc);
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc)
       if (cc < cntp) L.red[(wave * kQTokPerPass + cc) * 64 + lane] = acc[cc];
     __syncthreads();
-    {
+    if (tid < kQTokPerPass * 32) {
       // thread t -> token cc = t/32, intermediate column r = t%32 of the slice
       const int cc = tid >> 5, r = tid & 31;
       const int ccl = cc < cntp ? cc : 0;
       float g = L.red[(0 * kQTokPerPass + ccl) * 64 + r];
       float u = L.red[(0 * kQTokPerPass + ccl) * 64 + r + 32];
 #pragma unroll
-      for (int w = 1; w < 4; ++w) {
+      for (int w = 1; w < NW; ++w) {
         g = g + L.red[(w * kQTokPerPass + ccl) * 64 + r];
         u = u + L.red[(w * kQTokPerPass + ccl) * 64 + r + 32];
       }
@@ -274,21 +317,23 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
 }
 
 // ---------------------------------------------------------------- phase 2
-template <int QT, int ACT, int SC>
+template <int QT, int ACT, int SC, int NW>
 __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, const QLds& L) {
   const SchedArgs& c = a.c;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int e = rv.active[ui];
   const int p0 = rv.starts[e], cnt = rv.starts[e + 1] - p0;
   const int KB2 = c.I / 32, HB = c.H / 64;
-  const int kb0 = KB2 * wave / 4, kb1 = KB2 * (wave + 1) / 4;
+  const int kb0 = KB2 * wave / NW, kb1 = KB2 * (wave + 1) / NW;
   const size_t tile = (size_t)e * HB + hb;
   const char* wtile = (const char*)a.w2 + tile * KB2 * QFmt<QT>::block_bytes;
   const uint16_t* stile = a.w2_d + tile * KB2 * 64;
+  QRowBatch<QT> B;   // in flight while the intermediate rows are staged
+  rows_issue<QT>(B, wtile, stile, lane, kb0 & ~3, kb1, KB2);
 
   for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
     const int cntp = min(kQTokPerPass, cnt - cb0);
-    for (int idx = tid; idx < cntp * KB2; idx += kBlock) {
+    for (int idx = tid; idx < cntp * KB2; idx += NW * kWave) {
       const int cc = idx / KB2, kb = idx - cc * KB2;
       const size_t row = (size_t)rv.pair[p0 + cb0 + cc];
       const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.act_q + row * c.I + kb * 32);
@@ -309,15 +354,15 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
     float acc[kQTokPerPass];
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
-    rows_dot<QT, SC>(wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.I, KB2, cntp, acc);
+    rows_dot<QT, SC>(B, cb0 == 0, wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.I, KB2, cntp, acc);
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc)
       if (cc < cntp) L.red[(wave * kQTokPerPass + cc) * 64 + lane] = acc[cc];
     __syncthreads();
-    for (int cc = wave; cc < cntp; cc += 4) {
+    for (int cc = wave; cc < cntp; cc += NW) {
       float v = L.red[(0 * kQTokPerPass + cc) * 64 + lane];
 #pragma unroll
-      for (int w = 1; w < 4; ++w) v = v + L.red[(w * kQTokPerPass + cc) * 64 + lane];
+      for (int w = 1; w < NW; ++w) v = v + L.red[(w * kQTokPerPass + cc) * 64 + lane];
       c.eout[(size_t)rv.pair[p0 + cb0 + cc] * c.H + 64 * hb + lane] = v;
     }
     __syncthreads();
@@ -327,11 +372,11 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
 // ---------------------------------------------------------------- kernels
 __host__ __device__ inline size_t q_stage_bytes(int Kmax) {
   return (size_t)kQTokPerPass * Kmax + (size_t)kQTokPerPass * (Kmax / 32) * 8 +
-         (size_t)4 * kQTokPerPass * 64 * 4;
+         (size_t)kQDecWavesMax * kQTokPerPass * 64 * 4;
 }
 
-template <int QT, int ACT, int SC>
-__global__ __launch_bounds__(kBlock) void q_phase1_kernel(QArgs a) {
+template <int QT, int ACT, int SC, int NW>
+__global__ __launch_bounds__(NW * kWave) void q_phase1_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
   const QLds L = carve(smem, a.c.H);
@@ -339,11 +384,11 @@ __global__ __launch_bounds__(kBlock) void q_phase1_kernel(QArgs a) {
   const int S = a.c.I / 32;
   const int ui = blockIdx.x / S;
   if (ui >= rv.U) return;
-  q_phase1<QT, ACT, SC>(a, rv, ui, blockIdx.x % S, L);
+  q_phase1<QT, ACT, SC, NW>(a, rv, ui, blockIdx.x % S, L);
 }
 
-template <int QT, int ACT, int SC>
-__global__ __launch_bounds__(kBlock) void q_phase2_kernel(QArgs a) {
+template <int QT, int ACT, int SC, int NW>
+__global__ __launch_bounds__(NW * kWave) void q_phase2_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
   const QLds L = carve(smem, a.c.I);
@@ -351,19 +396,26 @@ __global__ __launch_bounds__(kBlock) void q_phase2_kernel(QArgs a) {
   const int HB = a.c.H / 64;
   const int ui = blockIdx.x / HB;
   if (ui >= rv.U) return;
-  q_phase2<QT, ACT, SC>(a, rv, ui, blockIdx.x % HB, L);
+  q_phase2<QT, ACT, SC, NW>(a, rv, ui, blockIdx.x % HB, L);
+}
+
+template <int QT, int ACT, int SC, int NW>
+static hipError_t launch_q_nw(const QArgs& a, int grid1, int grid2, size_t route, hipStream_t st) {
+  hipLaunchKernelGGL((q_phase1_kernel<QT, ACT, SC, NW>), dim3(grid1), dim3(NW * kWave),
+                     q_stage_bytes(a.c.H) + route, st, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((q_phase2_kernel<QT, ACT, SC, NW>), dim3(grid2), dim3(NW * kWave),
+                     q_stage_bytes(a.c.I) + route, st, a);
+  return hipGetLastError();
 }
 
 template <int QT, int ACT, int SC>
 static hipError_t launch_q_t(const QArgs& a, int grid1, int grid2, hipStream_t st) {
   const size_t route = a.c.route_global ? 0 : route_lds_ints(a.c.E, a.c.n) * sizeof(int);
-  hipLaunchKernelGGL((q_phase1_kernel<QT, ACT, SC>), dim3(grid1), dim3(kBlock),
-                     q_stage_bytes(a.c.H) + route, st, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((q_phase2_kernel<QT, ACT, SC>), dim3(grid2), dim3(kBlock),
-                     q_stage_bytes(a.c.I) + route, st, a);
-  return hipGetLastError();
+  if (q_stage_bytes(a.c.H) + route > kMaxLds || q_stage_bytes(a.c.I) + route > kMaxLds) return hipErrorInvalidValue;
+  return a.c.n <= kQDecWideMaxPairs ? launch_q_nw<QT, ACT, SC, 8>(a, grid1, grid2, route, st)
+                                    : launch_q_nw<QT, ACT, SC, 4>(a, grid1, grid2, route, st);
 }
 
 hipError_t launch_qint(const QArgs& a, int qt, int act, int sc, int grid1, int grid2, hipStream_t st) {
