@@ -36,7 +36,7 @@ hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*,
 W4Plan w4a16_plan(int, int);
 hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
-hipError_t launch_qint(const QArgs&, int, int, int, int, int, hipStream_t);
+hipError_t launch_qint(const QArgs&, int, int, int, int, int, bool, hipStream_t);
 hipError_t launch_qint_gemm(const QArgs&, int, int, int, hipStream_t);
 hipError_t launch_topk_softmax(const void*, int, int, int, int, int, int32_t*, float*, hipStream_t);
 hipError_t launch_q_repack(int, const void*, const uint16_t*, void*, uint16_t*, int, int, int, int,
@@ -278,8 +278,10 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
   const int64_t umax = n < h->E ? n : h->E;
   const int64_t grid1 = umax * (h->I / 32), grid2 = umax * (h->H / 64);
-  HIPCHK(launch_qint(a, h->quant, act, h->scale_dtype, (int)grid1, (int)grid2, st));
-  HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
+  // decode sizes: down + combine token-major in one launch (no eout round trip)
+  const bool token_down = n <= kQGemmMinPairs && K <= kDownMaxK;
+  HIPCHK(launch_qint(a, h->quant, act, h->scale_dtype, (int)grid1, (int)grid2, token_down, st));
+  if (!token_down) HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
   return MI_MOE_OK;
 }
 

@@ -399,32 +399,123 @@ __global__ __launch_bounds__(NW * kWave) void q_phase2_kernel(QArgs a) {
   q_phase2<QT, ACT, SC, NW>(a, rv, ui, blockIdx.x % HB, L);
 }
 
+// Down projection at decode sizes, token-major with the combine fused:
+// workgroup (token t, 16-row tile of H), one wave per routed expert k < K
+// (K <= kDownMaxK).  Lane (q, r) of wave k computes row r of the tile over
+// quarter q of I (the row's exact block dots, block order within the
+// quarter), the quarters are summed in order, and y[t, tile] = cast(sum_k
+// w[t,k] * out_k) over the valid ids in k order -- Stage C1 + C2 of
+// Int8-gemm/q8_gemm.cpp:593-641 without an eout round trip.  A wave with an
+// invalid id computes on expert 0 and is left out of the sum; a token with
+// no valid id gets y = 0.
+// LDS: act bytes [K][I] | act d [K][I/32] | act byte sums [K][I/32] | quarter
+// partials [K][64] | outputs [K][16] | valid [K].
+__host__ __device__ inline size_t q_down_token_lds_bytes(int I, int K) {
+  return (size_t)K * I + (size_t)K * (I / 32) * 8 + (size_t)K * 64 * 4 + (size_t)K * 16 * 4 + (size_t)K * 4;
+}
+
+template <int QT, int ACT, int SC>
+__global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
+  const SchedArgs& c = a.c;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = c.H, I = c.I, K = c.K, KB2 = I / 32, HB = H / 64, NT = H / 16;
+  const int t = blockIdx.x / NT, jt = blockIdx.x - t * NT;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  int8_t* xq = reinterpret_cast<int8_t*>(smem);
+  float* xd = reinterpret_cast<float*>(smem + (size_t)K * I);
+  int* xs = reinterpret_cast<int*>(xd + K * KB2);
+  float* part = reinterpret_cast<float*>(xs + K * KB2);
+  float* outs = part + K * 64;
+  int* valid = reinterpret_cast<int*>(outs + K * 16);
+  const int e = c.ids[t * K + wave];
+  const bool ok = (unsigned)e < (unsigned)c.E;
+  // this lane's row in the 64-row layout tile, and its quarter of the blocks
+  const int row = (jt & 3) * 16 + r;
+  const size_t tile = (size_t)(ok ? e : 0) * HB + (jt >> 2);
+  const char* wtile = (const char*)a.w2 + tile * KB2 * QFmt<QT>::block_bytes;
+  const uint16_t* stile = a.w2_d + tile * KB2 * 64;
+  const int kb0 = KB2 * q / 4, kb1 = KB2 * (q + 1) / 4;
+  QRowBatch<QT> B;   // in flight while the token's intermediate rows are staged
+  rows_issue<QT>(B, wtile, stile, row, kb0 & ~3, kb1, KB2);
+  for (int idx = tid; idx < K * KB2; idx += K * 64) {
+    const int cc = idx / KB2, kb = idx - cc * KB2;
+    const size_t prow = (size_t)t * K + cc;   // pair rows of a token are contiguous
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.act_q + prow * I + kb * 32);
+    const u32x4_t q0 = src[0], q1 = src[1];
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(xq + cc * I + kb * 32);
+    dst[0] = q0;
+    dst[1] = q1;
+    if constexpr (QT == 1) {
+      const uint32_t ws[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      int sum = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum = __builtin_amdgcn_sdot4((int)ws[j], 0x01010101, sum, false);
+      xs[cc * KB2 + kb] = sum;
+    }
+    xd[cc * KB2 + kb] = a.act_d[prow * KB2 + kb];
+  }
+  if (lane == 0) valid[wave] = ok;
+  __syncthreads();
+  float acc[kQTokPerPass];
+#pragma unroll
+  for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
+  rows_dot<QT, SC>(B, true, wtile, stile, row, kb0, kb1, xq + wave * I, xd + wave * KB2, xs + wave * KB2, I,
+                   KB2, 1, acc);
+  part[wave * 64 + lane] = acc[0];
+  __syncthreads();
+  if (lane < 16) {
+    const float* pw = part + wave * 64;
+    outs[wave * 16 + lane] = ((pw[lane] + pw[16 + lane]) + pw[32 + lane]) + pw[48 + lane];
+  }
+  __syncthreads();
+  if (tid < 16) {
+    float y = 0.0f;
+    for (int k = 0; k < K; ++k)
+      if (valid[k]) {
+        const float prod = c.tw[t * K + k] * outs[16 * k + tid];
+        y = y + prod;
+      }
+    c.y[(size_t)t * H + 16 * jt + tid] = from_f32<ACT>(y);
+  }
+}
+
 template <int QT, int ACT, int SC, int NW>
-static hipError_t launch_q_nw(const QArgs& a, int grid1, int grid2, size_t route, hipStream_t st) {
+static hipError_t launch_q_nw(const QArgs& a, int grid1, int grid2, size_t route, bool token_down,
+                              hipStream_t st) {
   hipLaunchKernelGGL((q_phase1_kernel<QT, ACT, SC, NW>), dim3(grid1), dim3(NW * kWave),
                      q_stage_bytes(a.c.H) + route, st, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
+  if (token_down) {
+    hipLaunchKernelGGL((q_down_token_kernel<QT, ACT, SC>), dim3(a.c.T * (a.c.H / 16)), dim3(64 * a.c.K),
+                       q_down_token_lds_bytes(a.c.I, a.c.K), st, a);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((q_phase2_kernel<QT, ACT, SC, NW>), dim3(grid2), dim3(NW * kWave),
                      q_stage_bytes(a.c.I) + route, st, a);
   return hipGetLastError();
 }
 
 template <int QT, int ACT, int SC>
-static hipError_t launch_q_t(const QArgs& a, int grid1, int grid2, hipStream_t st) {
+static hipError_t launch_q_t(const QArgs& a, int grid1, int grid2, bool token_down, hipStream_t st) {
   const size_t route = a.c.route_global ? 0 : route_lds_ints(a.c.E, a.c.n) * sizeof(int);
   if (q_stage_bytes(a.c.H) + route > kMaxLds || q_stage_bytes(a.c.I) + route > kMaxLds) return hipErrorInvalidValue;
-  return a.c.n <= kQDecWideMaxPairs ? launch_q_nw<QT, ACT, SC, 8>(a, grid1, grid2, route, st)
-                                    : launch_q_nw<QT, ACT, SC, 4>(a, grid1, grid2, route, st);
+  if (token_down && q_down_token_lds_bytes(a.c.I, a.c.K) > kMaxLds) return hipErrorInvalidValue;
+  return a.c.n <= kQDecWideMaxPairs ? launch_q_nw<QT, ACT, SC, 8>(a, grid1, grid2, route, token_down, st)
+                                    : launch_q_nw<QT, ACT, SC, 4>(a, grid1, grid2, route, token_down, st);
 }
 
-hipError_t launch_qint(const QArgs& a, int qt, int act, int sc, int grid1, int grid2, hipStream_t st) {
+// token_down: the down projection and the combine in one token-major launch
+// (decode sizes); otherwise expert-major down into eout (the caller combines).
+hipError_t launch_qint(const QArgs& a, int qt, int act, int sc, int grid1, int grid2, bool token_down,
+                       hipStream_t st) {
+  const bool td = token_down;
   if (qt == 0) {
-    if (act == 1) return sc == 1 ? launch_q_t<0, 1, 1>(a, grid1, grid2, st) : launch_q_t<0, 1, 0>(a, grid1, grid2, st);
-    return sc == 1 ? launch_q_t<0, 0, 1>(a, grid1, grid2, st) : launch_q_t<0, 0, 0>(a, grid1, grid2, st);
+    if (act == 1) return sc == 1 ? launch_q_t<0, 1, 1>(a, grid1, grid2, td, st) : launch_q_t<0, 1, 0>(a, grid1, grid2, td, st);
+    return sc == 1 ? launch_q_t<0, 0, 1>(a, grid1, grid2, td, st) : launch_q_t<0, 0, 0>(a, grid1, grid2, td, st);
   }
-  if (act == 1) return sc == 1 ? launch_q_t<1, 1, 1>(a, grid1, grid2, st) : launch_q_t<1, 1, 0>(a, grid1, grid2, st);
-  return sc == 1 ? launch_q_t<1, 0, 1>(a, grid1, grid2, st) : launch_q_t<1, 0, 0>(a, grid1, grid2, st);
+  if (act == 1) return sc == 1 ? launch_q_t<1, 1, 1>(a, grid1, grid2, td, st) : launch_q_t<1, 1, 0>(a, grid1, grid2, td, st);
+  return sc == 1 ? launch_q_t<1, 0, 1>(a, grid1, grid2, td, st) : launch_q_t<1, 0, 0>(a, grid1, grid2, td, st);
 }
 
 // ---------------------------------------------------------------- grouped GEMMs (int8 MFMA)
