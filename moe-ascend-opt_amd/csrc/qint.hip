@@ -134,28 +134,33 @@ constexpr int kQDecWavesMax = 8;
 constexpr int kQDecWideMaxPairs = 8;
 
 // One lane's row weights (whole 4-block layout groups, as 16-byte loads) and
-// the blocks' raw scale bits for up to NG groups: 32 VGPRs of weights.
-template <int QT>
+// the blocks' raw scale bits for up to NG_ groups (Q8_0: 32 VGPRs of weights
+// per group, Q4_0: 16).  kQBatchGroups: the phase kernels' batch, 64 VGPRs of
+// weights in the 8-wave form (the smallest calls: a wave's whole share of K
+// for H = 2048), 32 in the 4-wave form (occupancy).
+template <int QT, int NG_>
 struct QRowBatch {
   static constexpr int NV = 4 * QFmt<QT>::chunks;   // 16-byte loads per group
-  static constexpr int NG = QT == 0 ? 1 : 2;        // groups per batch
+  static constexpr int NG = NG_;                    // groups per batch
   u32x4_t v[NG][NV];
   uint32_t sw[NG][4];
 };
+template <int QT, int NW>
+constexpr int kQBatchGroups = (QT == 0 ? 1 : 2) * (NW == 8 ? 2 : 1);
 
 // Issue the loads of the whole groups gs, gs+4, .. (up to NG) that start below
 // kb1 and lie inside the row (g + 4 <= KB); a partial last group is left to
 // rows_dot's per-block tail.
-template <int QT>
-__device__ __forceinline__ void rows_issue(QRowBatch<QT>& B, const char* wtile, const uint16_t* stile, int lane,
-                                           int gs, int kb1, int KB) {
+template <int QT, int NG>
+__device__ __forceinline__ void rows_issue(QRowBatch<QT, NG>& B, const char* wtile, const uint16_t* stile,
+                                           int lane, int gs, int kb1, int KB) {
 #pragma unroll
-  for (int j = 0; j < QRowBatch<QT>::NG; ++j) {
+  for (int j = 0; j < NG; ++j) {
     const int g0 = gs + 4 * j;
     if (g0 < kb1 && g0 + 4 <= KB) {   // uniform
       const u32x4_t* p = reinterpret_cast<const u32x4_t*>(wtile + QLay<QT>::off(KB, g0, lane, 0));
 #pragma unroll
-      for (int i = 0; i < QRowBatch<QT>::NV; ++i) B.v[j][i] = p[i];
+      for (int i = 0; i < QRowBatch<QT, NG>::NV; ++i) B.v[j][i] = p[i];
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb) B.sw[j][bb] = stile[(g0 + bb) * 64 + lane];
     }
@@ -168,8 +173,8 @@ __device__ __forceinline__ void rows_issue(QRowBatch<QT>& B, const char* wtile, 
 // kb0 & ~3) when `issued`; later batches are loaded here.  Blocks of a group
 // outside the range are skipped (the neighbouring wave reads the same group,
 // mostly from the cache).
-template <int QT, int SC>
-__device__ __forceinline__ void rows_dot(QRowBatch<QT>& B, bool issued, const char* wtile, const uint16_t* stile,
+template <int QT, int SC, int NG>
+__device__ __forceinline__ void rows_dot(QRowBatch<QT, NG>& B, bool issued, const char* wtile, const uint16_t* stile,
                                          int lane, int kb0, int kb1, const int8_t* xq, const float* xd,
                                          const int* xs, int K, int KB, int cntp, float (&acc)[kQTokPerPass]) {
   auto block = [&](int kb, const u32x4_t& w0, const u32x4_t& w1, float dw) {
@@ -185,10 +190,9 @@ __device__ __forceinline__ void rows_dot(QRowBatch<QT>& B, bool issued, const ch
       acc[cc] = acc[cc] + t2;
     }
   };
-  constexpr int NG = QRowBatch<QT>::NG;
   const int gs0 = kb0 & ~3, KBw = KB & ~3;   // KBw: end of the whole groups
   for (int gs = gs0; gs < kb1 && gs < KBw; gs += 4 * NG) {
-    if (gs != gs0 || !issued) rows_issue<QT>(B, wtile, stile, lane, gs, kb1, KB);
+    if (gs != gs0 || !issued) rows_issue<QT, NG>(B, wtile, stile, lane, gs, kb1, KB);
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
       const int g0 = gs + 4 * j;
@@ -249,8 +253,8 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
   const char* wtile = (const char*)a.w13 + tile * KB * QFmt<QT>::block_bytes;
   const uint16_t* stile = a.w13_d + tile * KB * 64;
   // the first weight batch is in flight while the activations are staged
-  QRowBatch<QT> B;
-  rows_issue<QT>(B, wtile, stile, lane, kb0 & ~3, kb1, KB);
+  QRowBatch<QT, kQBatchGroups<QT, NW>> B;
+  rows_issue<QT, kQBatchGroups<QT, NW>>(B, wtile, stile, lane, kb0 & ~3, kb1, KB);
 
   for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
     const int cntp = min(kQTokPerPass, cnt - cb0);
@@ -278,7 +282,8 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
     float acc[kQTokPerPass];
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
-    rows_dot<QT, SC>(B, cb0 == 0, wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.H, KB, cntp, acc);
+    rows_dot<QT, SC, kQBatchGroups<QT, NW>>(B, cb0 == 0, wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.H, KB,
+                                        cntp, acc);
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc)
       if (cc < cntp) L.red[(wave * kQTokPerPass + cc) * 64 + lane] = acc[cc];
@@ -328,8 +333,8 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
   const size_t tile = (size_t)e * HB + hb;
   const char* wtile = (const char*)a.w2 + tile * KB2 * QFmt<QT>::block_bytes;
   const uint16_t* stile = a.w2_d + tile * KB2 * 64;
-  QRowBatch<QT> B;   // in flight while the intermediate rows are staged
-  rows_issue<QT>(B, wtile, stile, lane, kb0 & ~3, kb1, KB2);
+  QRowBatch<QT, kQBatchGroups<QT, NW>> B;   // in flight while the intermediate rows are staged
+  rows_issue<QT, kQBatchGroups<QT, NW>>(B, wtile, stile, lane, kb0 & ~3, kb1, KB2);
 
   for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
     const int cntp = min(kQTokPerPass, cnt - cb0);
@@ -354,7 +359,8 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
     float acc[kQTokPerPass];
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
-    rows_dot<QT, SC>(B, cb0 == 0, wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.I, KB2, cntp, acc);
+    rows_dot<QT, SC, kQBatchGroups<QT, NW>>(B, cb0 == 0, wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.I, KB2,
+                                        cntp, acc);
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc)
       if (cc < cntp) L.red[(wave * kQTokPerPass + cc) * 64 + lane] = acc[cc];
@@ -435,8 +441,8 @@ __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
   const char* wtile = (const char*)a.w2 + tile * KB2 * QFmt<QT>::block_bytes;
   const uint16_t* stile = a.w2_d + tile * KB2 * 64;
   const int kb0 = KB2 * q / 4, kb1 = KB2 * (q + 1) / 4;
-  QRowBatch<QT> B;   // in flight while the token's intermediate rows are staged
-  rows_issue<QT>(B, wtile, stile, row, kb0 & ~3, kb1, KB2);
+  QRowBatch<QT, 2> B;   // both groups a quarter can touch, in flight while the rows are staged
+  rows_issue<QT, 2>(B, wtile, stile, row, kb0 & ~3, kb1, KB2);
   for (int idx = tid; idx < K * KB2; idx += K * 64) {
     const int cc = idx / KB2, kb = idx - cc * KB2;
     const size_t prow = (size_t)t * K + cc;   // pair rows of a token are contiguous
@@ -459,8 +465,8 @@ __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
   float acc[kQTokPerPass];
 #pragma unroll
   for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
-  rows_dot<QT, SC>(B, true, wtile, stile, row, kb0, kb1, xq + wave * I, xd + wave * KB2, xs + wave * KB2, I,
-                   KB2, 1, acc);
+  rows_dot<QT, SC, 2>(B, true, wtile, stile, row, kb0, kb1, xq + wave * I, xd + wave * KB2, xs + wave * KB2, I,
+                      KB2, 1, acc);
   part[wave * 64 + lane] = acc[0];
   __syncthreads();
   if (lane < 16) {
