@@ -277,7 +277,7 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   }
   if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
   const int64_t umax = n < h->E ? n : h->E;
-  const int64_t grid1 = umax * (h->I / 32), grid2 = umax * (h->H / 64);
+  const int64_t grid1 = (n <= kQBallotMaxPairs ? n : umax) * (h->I / 32), grid2 = umax * (h->H / 64);
   // decode sizes: down + combine token-major in one launch (no eout round trip)
   const bool token_down = n <= kQGemmMinPairs && K <= kDownMaxK;
   HIPCHK(launch_qint(a, h->quant, act, h->scale_dtype, (int)grid1, (int)grid2, token_down, st));

@@ -35,6 +35,9 @@ __host__ __device__ constexpr int route_chunks(int n) { return (n + kRouteChunk 
 constexpr int kGemmRows = 64;
 // Q8_0 / Q4_0: above this many routed pairs the int8 grouped GEMMs run
 constexpr int kQGemmMinPairs = 64;
+// Q8_0 / Q4_0 lane-per-row gate_up: up to this many routed pairs the work
+// items are pairs routed by one ballot per wave (grid = pairs x slices).
+constexpr int kQBallotMaxPairs = 64;
 __host__ __device__ inline int64_t gemm_tiles_max(int64_t n, int E) {
   return n / kGemmRows + (n < E ? n : E);
 }

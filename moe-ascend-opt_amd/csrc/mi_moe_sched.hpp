@@ -44,4 +44,35 @@ __device__ inline RouteView sched_route(const SchedArgs& c, int* route_lds_buf, 
   return rv;
 }
 
+__device__ __forceinline__ uint64_t lanemask_lt(int lane) {
+  return lane ? (~0ull >> (64 - lane)) : 0ull;
+}
+
+// Routing for T*K <= 64 without a sort: every wave reads all ids at once.
+// Work item pi (a pair index) serves its expert iff pi is the expert's first
+// pair; column j of the expert is its j-th pair in ascending pair order, the
+// order the stable counting sort of preprocess_moe_routing
+// (Int8-gemm/moe_common.cpp:146-216) gives.  Lane l of `colpair` holds the
+// pair index of column l.  Whole-wave routine.
+struct BallotCols {
+  int e, cnt, colpair;
+  uint64_t vmask;      // bit i: pair i has a valid expert id
+  bool serve;
+};
+__device__ __forceinline__ BallotCols ballot_cols(const SchedArgs& c, int pi, int lane) {
+  BallotCols b;
+  const int myid = lane < c.n ? c.ids[lane] : -1;
+  const bool myvalid = lane < c.n && (unsigned)myid < (unsigned)c.E;
+  b.vmask = __ballot(myvalid);
+  b.e = __shfl(myid, pi);
+  const uint64_t match = __ballot(myvalid && myid == b.e);
+  b.serve = (unsigned)b.e < (unsigned)c.E && (__ffsll((long long)match) - 1) == pi;
+  b.cnt = __popcll(match);
+  const bool inm = (match >> lane) & 1;
+  const uint64_t lt = lanemask_lt(lane);
+  const int dst = inm ? __popcll(match & lt) : b.cnt + __popcll(~match & lt);
+  b.colpair = __builtin_amdgcn_ds_permute(dst << 2, lane);   // full permutation
+  return b;
+}
+
 }  // namespace mimoe

@@ -242,11 +242,9 @@ __device__ __forceinline__ QLds carve(unsigned char* smem, int Kmax) {
 
 // ---------------------------------------------------------------- phase 1
 template <int QT, int ACT, int SC, int NW>
-__device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, const QLds& L) {
+__device__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int sl, const QLds& L) {
   const SchedArgs& c = a.c;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int e = rv.active[ui];
-  const int p0 = rv.starts[e], cnt = rv.starts[e + 1] - p0;
   const int KB = c.H / 32, S = c.I / 32;
   const int kb0 = KB * wave / NW, kb1 = KB * (wave + 1) / NW;
   const size_t tile = (size_t)e * S + sl;
@@ -261,7 +259,7 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
     // Stage A for the staged tokens (Int8-gemm/q8_gemm.cpp:360-377)
     for (int idx = tid; idx < cntp * KB; idx += NW * kWave) {
       const int cc = idx / KB, kb = idx - cc * KB;
-      const int t = rv.pair[p0 + cb0 + cc] / c.K;
+      const int t = pairs[cb0 + cc] / c.K;
       const u32x4_t* src = reinterpret_cast<const u32x4_t*>(c.x + (size_t)t * c.H + kb * 32);
       float v[32];
 #pragma unroll
@@ -312,7 +310,7 @@ __device__ void q_phase1(const QArgs& a, const RouteView& rv, int ui, int sl, co
       const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
       const int8_t q = q8_round(act * id);
       if (cc < cntp) {
-        const size_t row = (size_t)rv.pair[p0 + cb0 + cc];
+        const size_t row = (size_t)pairs[cb0 + cc];
         a.act_q[row * c.I + 32 * sl + r] = q;
         if (r == 0) a.act_d[row * S + sl] = d;
       }
@@ -381,16 +379,29 @@ __host__ __device__ inline size_t q_stage_bytes(int Kmax) {
          (size_t)kQDecWavesMax * kQTokPerPass * 64 * 4;
 }
 
+// Work items: up to kQBallotMaxPairs routed pairs, one per pair (the item
+// serves its expert iff it is the expert's first pair; ballot routing, the
+// expert's pair list staged in LDS); above, one per active expert of the
+// counting sort (in LDS, or the routing kernel's arrays).
 template <int QT, int ACT, int SC, int NW>
 __global__ __launch_bounds__(NW * kWave) void q_phase1_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
   const QLds L = carve(smem, a.c.H);
+  const int S = a.c.I / 32, item = blockIdx.x / S;
+  if (a.c.n <= kQBallotMaxPairs) {   // uniform
+    const int tid = threadIdx.x;
+    const BallotCols cl = ballot_cols(a.c, item, tid & 63);   // every wave: same result
+    if (!cl.serve) return;   // uniform
+    if (tid < kWave) L.route[tid] = cl.colpair;
+    __syncthreads();
+    q_phase1<QT, ACT, SC, NW>(a, cl.e, cl.cnt, L.route, blockIdx.x % S, L);
+    return;
+  }
   const RouteView rv = sched_route(a.c, L.route, &s_U);
-  const int S = a.c.I / 32;
-  const int ui = blockIdx.x / S;
-  if (ui >= rv.U) return;
-  q_phase1<QT, ACT, SC, NW>(a, rv, ui, blockIdx.x % S, L);
+  if (item >= rv.U) return;
+  const int e = rv.active[item], p0 = rv.starts[e];
+  q_phase1<QT, ACT, SC, NW>(a, e, rv.starts[e + 1] - p0, rv.pair + p0, blockIdx.x % S, L);
 }
 
 template <int QT, int ACT, int SC, int NW>
@@ -504,7 +515,8 @@ static hipError_t launch_q_nw(const QArgs& a, int grid1, int grid2, size_t route
 
 template <int QT, int ACT, int SC>
 static hipError_t launch_q_t(const QArgs& a, int grid1, int grid2, bool token_down, hipStream_t st) {
-  const size_t route = a.c.route_global ? 0 : route_lds_ints(a.c.E, a.c.n) * sizeof(int);
+  size_t route = a.c.route_global ? 0 : route_lds_ints(a.c.E, a.c.n) * sizeof(int);
+  if (route < kWave * sizeof(int)) route = kWave * sizeof(int);   // the ballot path's pair list
   if (q_stage_bytes(a.c.H) + route > kMaxLds || q_stage_bytes(a.c.I) + route > kMaxLds) return hipErrorInvalidValue;
   if (token_down && q_down_token_lds_bytes(a.c.I, a.c.K) > kMaxLds) return hipErrorInvalidValue;
   return a.c.n <= kQDecWideMaxPairs ? launch_q_nw<QT, ACT, SC, 8>(a, grid1, grid2, route, token_down, st)
