@@ -82,10 +82,13 @@ constexpr size_t kMaxLds = 65536;   // dynamic LDS a kernel launch may ask for
 constexpr int kDownMaxK = 8;
 
 // LDS bytes of the W4A16 decode kernels.
-constexpr int kP1RedBytes = 4 * 2 * 64 * 4 * 4;
-__host__ __device__ inline size_t w4_p1_lds_bytes(int H, int xrows, int slices) {
-  return (size_t)slices * (kP1RedBytes + 80 * (H >> 7)) + (size_t)xrows * H * 2;
+// Phase-1 cross-wave reduction buffer of one slice: [NW waves][gate,up][64][4] f32.
+__host__ __device__ constexpr int p1_red_bytes(int NW) { return NW * 2 * 64 * 4 * 4; }
+__host__ __device__ inline size_t w4_p1_lds_bytes(int H, int xrows, int slices, int NW = 4) {
+  return (size_t)slices * (p1_red_bytes(NW) + 80 * (H >> 7)) + (size_t)xrows * H * 2;
 }
+// W4A16 decode gate_up: up to this many routed pairs the K split is 8 waves.
+constexpr int kW4WideMaxPairs = 8;
 __host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) {
   return (size_t)K * I * 2 + (size_t)K * RT * w2_meta_sec_bytes(I >> 7) + (size_t)K * 16 * RT * 4 + (size_t)K * 4;
 }

@@ -172,19 +172,19 @@ constexpr int kDownWavesPerEU = 6;
 // rows of each pass's columns are copied once the routing is known.  Work
 // item = pair index; the items of an expert's later pairs exit at once.
 // LDS (w4_p1_lds_bytes): red [S][wave][gate,up][64][4] f32 | metadata S x 80*G1 B | x rows.
-template <int ACT, int NB, int S>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kP1WavesPerEU)))
+template <int ACT, int NB, int S, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(kP1WavesPerEU)))
 void w4a16_phase1_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, NJS = NI1 / S, P = a.p1_cols, HI = H >> 3;
   float* red = reinterpret_cast<float*>(smem);
-  unsigned char* meta = smem + S * kP1RedBytes;
+  unsigned char* meta = smem + S * p1_red_bytes(NW);
   uint16_t* xs = reinterpret_cast<uint16_t*>(meta + S * 80 * G1);
   const int item = blockIdx.x / NJS, j0 = (blockIdx.x - item * NJS) * S;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   if (a.x_all)   // uniform; x is [T][H] contiguous
-    stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, 4, lane,
+    stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, NW, lane,
               [&](int k) { return (const void*)(c.x + 8 * (size_t)k); });
   const BallotCols cl = ballot_cols(c, item, lane);
   if (!cl.serve) {   // uniform
@@ -196,8 +196,8 @@ void w4a16_phase1_kernel(W4Args a) {
   const int e = cl.e, cnt = cl.cnt;
   const size_t blk = (size_t)e * NI1 + j0;   // S consecutive slices: contiguous weights and metadata
   const unsigned char* msrc = a.w13_m + blk * 80 * G1;
-  stage_lds(meta, S * 5 * G1, wave, 4, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
-  const int g0 = G1 * wave / 4, ng = G1 * (wave + 1) / 4 - g0;   // equal for all waves (G1 % 4 == 0)
+  stage_lds(meta, S * 5 * G1, wave, NW, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
+  const int g0 = G1 * wave / NW, ng = G1 * (wave + 1) / NW - g0;   // equal for all waves (G1 % NW == 0)
   const char* wg = (const char*)a.w13 + (blk * 2 * G1 + g0) * 1024 + lane * 16;   // slice s: + 2*G1 KB
   constexpr float off = W4Consts<ACT>::offset;
   for (int cb0 = 0; cb0 < cnt; cb0 += P) {
@@ -206,7 +206,7 @@ void w4a16_phase1_kernel(W4Args a) {
     if (a.x_all) {
       xr = pair_of(cb0 + min(r, ncol - 1)) / c.K;
     } else {
-      stage_lds(reinterpret_cast<unsigned char*>(xs), ncol * HI, wave, 4, lane, [&](int k) {
+      stage_lds(reinterpret_cast<unsigned char*>(xs), ncol * HI, wave, NW, lane, [&](int k) {
         const int cc = k / HI;
         const int t = pair_of(cb0 + cc) / c.K;
         return (const void*)(c.x + (size_t)t * H + 8 * (k - cc * HI));
@@ -258,18 +258,18 @@ void w4a16_phase1_kernel(W4Args a) {
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      float* rs = red + s * (kP1RedBytes / 4);
+      float* rs = red + s * (p1_red_bytes(NW) / 4);
       *reinterpret_cast<f32x4_t*>(rs + ((wave * 2 + 0) * 64 + lane) * 4) = accg[s];
       *reinterpret_cast<f32x4_t*>(rs + ((wave * 2 + 1) * 64 + lane) * 4) = accu[s];
     }
     __syncthreads();
     if (tid < 64 * S) {   // thread (slice s, lane ln)
       const int s = tid >> 6, ln = tid & 63;
-      const float* rs = red + s * (kP1RedBytes / 4);
+      const float* rs = red + s * (p1_red_bytes(NW) / 4);
       f32x4_t g = *reinterpret_cast<const f32x4_t*>(rs + ((0 * 2 + 0) * 64 + ln) * 4);
       f32x4_t u = *reinterpret_cast<const f32x4_t*>(rs + ((0 * 2 + 1) * 64 + ln) * 4);
 #pragma unroll
-      for (int w = 1; w < 4; ++w) {
+      for (int w = 1; w < NW; ++w) {
         g += *reinterpret_cast<const f32x4_t*>(rs + ((w * 2 + 0) * 64 + ln) * 4);
         u += *reinterpret_cast<const f32x4_t*>(rs + ((w * 2 + 1) * 64 + ln) * 4);
       }
@@ -843,18 +843,20 @@ hipError_t launch_awq_repack_all(const int32_t* w13q, const int32_t* w13z, const
 }
 
 // ================================================================ launchers
-template <int ACT, int NB, int S>
+template <int ACT, int NB, int S, int NW>
 static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, NB, S>), dim3(grid), dim3(kBlock), lds, st, a);
+  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, NB, S, NW>), dim3(grid), dim3(NW * kWave), lds, st, a);
 }
 
-// (NB, S) pairs instantiated for phase 1.  S > 1 measured slower on the
-// decode shapes (occupancy), so only S = 1 is built.
+// (NB, S, NW) instantiated for phase 1.  S > 1 measured slower on the
+// decode shapes (occupancy), so only S = 1 is built; NW = 8 waves (K split 8
+// ways) for the smallest calls.
 template <int ACT>
-static hipError_t dispatch_p1(const W4Args& a, int nb, int s, int grid, size_t lds, hipStream_t st) {
-#define P1_CASE(NB_, S_) \
-  if (nb == NB_ && s == S_) { launch_p1<ACT, NB_, S_>(a, grid, lds, st); return hipGetLastError(); }
-  P1_CASE(1, 1) P1_CASE(2, 1) P1_CASE(3, 1) P1_CASE(4, 1) P1_CASE(6, 1) P1_CASE(8, 1)
+static hipError_t dispatch_p1(const W4Args& a, int nb, int s, int nw, int grid, size_t lds, hipStream_t st) {
+#define P1_CASE(NB_, S_, NW_) \
+  if (nb == NB_ && s == S_ && nw == NW_) { launch_p1<ACT, NB_, S_, NW_>(a, grid, lds, st); return hipGetLastError(); }
+  P1_CASE(1, 1, 4) P1_CASE(2, 1, 4) P1_CASE(3, 1, 4) P1_CASE(4, 1, 4) P1_CASE(6, 1, 4) P1_CASE(8, 1, 4)
+  P1_CASE(1, 1, 8) P1_CASE(2, 1, 8) P1_CASE(3, 1, 8) P1_CASE(4, 1, 8)
 #undef P1_CASE
   return hipErrorInvalidValue;
 }
@@ -900,9 +902,14 @@ W4Plan w4a16_plan(int H, int I) {
 template <int ACT>
 static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int grid2, hipStream_t st,
                               hipEvent_t mid) {
-  const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1);
+  // the smallest calls: gate_up's K split over 8 waves (shorter chains per wave)
+  const int G1 = a.c.H / 128;
+  const int nw1 = (a.c.n <= kW4WideMaxPairs && G1 % 8 == 0) ? 8 : 4;
+  int nb1 = p.nb1;
+  while ((G1 / nw1) % nb1) --nb1;   // the batch divides the wave's groups
+  const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1, nw1);
   const size_t lds2 = w4_down_token_lds_bytes(a.c.I, a.c.K, p.rt2);
-  hipError_t err = dispatch_p1<ACT>(a, p.nb1, p.s1, grid1 / p.s1, lds1, st);
+  hipError_t err = dispatch_p1<ACT>(a, nb1, p.s1, nw1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
   return dispatch_p2<ACT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
