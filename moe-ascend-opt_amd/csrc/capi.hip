@@ -224,7 +224,8 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
     // an expert rarely gets more than a few of the T tokens; a narrow pass
     // keeps the LDS small (occupancy), extra columns take another pass
     a.p1_cols = (int)(T < kDecodeCols ? T : kDecodeCols);
-    while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1) > kMaxLds) --a.p1_cols;
+    const int nw1 = w4_p1_waves(n, (int)h->H);
+    while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1, nw1) > kMaxLds) --a.p1_cols;
     const W4Plan plan = w4a16_plan((int)h->H, (int)h->I);
     HIPCHK(launch_w4a16(a, plan, act, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st, mid));
     h->mid_recorded = mid != nullptr;

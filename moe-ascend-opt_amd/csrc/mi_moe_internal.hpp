@@ -89,6 +89,11 @@ __host__ __device__ inline size_t w4_p1_lds_bytes(int H, int xrows, int slices, 
 }
 // W4A16 decode gate_up: up to this many routed pairs the K split is 8 waves.
 constexpr int kW4WideMaxPairs = 8;
+// Waves of a W4A16 decode gate_up workgroup for n routed pairs at hidden size H.
+// (8 only where its larger reduction buffer leaves room for one hidden row).
+inline int w4_p1_waves(int64_t n, int H) {
+  return (n <= kW4WideMaxPairs && (H / 128) % 8 == 0 && w4_p1_lds_bytes(H, 1, 1, 8) <= kMaxLds) ? 8 : 4;
+}
 __host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) {
   return (size_t)K * I * 2 + (size_t)K * RT * w2_meta_sec_bytes(I >> 7) + (size_t)K * 16 * RT * 4 + (size_t)K * 4;
 }

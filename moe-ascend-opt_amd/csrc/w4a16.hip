@@ -904,11 +904,13 @@ static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int g
                               hipEvent_t mid) {
   // the smallest calls: gate_up's K split over 8 waves (shorter chains per wave)
   const int G1 = a.c.H / 128;
-  const int nw1 = (a.c.n <= kW4WideMaxPairs && G1 % 8 == 0) ? 8 : 4;
-  int nb1 = p.nb1;
-  while ((G1 / nw1) % nb1) --nb1;   // the batch divides the wave's groups
+  const int nw1 = w4_p1_waves(a.c.n, a.c.H);
+  // the batch divides the wave's groups; 1-4 are built for every wave count
+  int nb1 = nw1 == 4 ? p.nb1 : min(p.nb1, 4);
+  while ((G1 / nw1) % nb1) --nb1;
   const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1, nw1);
   const size_t lds2 = w4_down_token_lds_bytes(a.c.I, a.c.K, p.rt2);
+  if (lds1 > kMaxLds || lds2 > kMaxLds) return hipErrorInvalidValue;
   hipError_t err = dispatch_p1<ACT>(a, nb1, p.s1, nw1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;

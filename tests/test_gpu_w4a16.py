@@ -159,9 +159,11 @@ def test_dtypes(cuda, adt, sdt):
     assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, adt)) <= TOL
 
 
-@pytest.mark.parametrize("H,T,K", [(1024, 4, 8), (1536, 8, 6), (3072, 5, 8), (2048, 8, 8), (512, 3, 4)])
+@pytest.mark.parametrize("H,T,K", [(1024, 4, 8), (1536, 8, 6), (3072, 5, 8), (2048, 8, 8), (512, 3, 4),
+                                   (6144, 1, 8), (4096, 1, 8), (6144, 4, 8)])
 def test_decode_widths(cuda, H, T, K):
-    """Decode path at every H/512 group count the kernels are built for."""
+    """Decode path at H/512 group counts of 1-12, with the gate_up K split
+    over 8 waves (at most 8 routed pairs) and over 4 or fewer above."""
     E, I = 16, 256
     w = w4a16_random(E, H, I, seed=H + T)
     h = _handle(E, H, I, w, True, cuda)
