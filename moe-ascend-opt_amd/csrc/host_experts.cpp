@@ -92,7 +92,7 @@ namespace {
 
 constexpr int kTokBlock = 256;    // tokens per pass (bounds the per-pair buffers)
 constexpr int kQRows = 32;        // output rows per Q task
-constexpr int kAwqWordsMax = 8;   // packed words (64 columns) per W4A16 task, at most
+constexpr int kAwqWordsMax = 16;  // packed words (128 columns) per W4A16 task, at most
 constexpr int kAwqOrder[8] = {0, 2, 4, 6, 1, 3, 5, 7};   // nibble slot s -> column 8j + order[s]
 
 float bits_f32(uint32_t u) {
@@ -173,40 +173,62 @@ void q_rows(int quant, int sdt, const uint8_t* wq, const uint16_t* wd, int64_t K
   }
 }
 
-// v[8*jj + sl] = nibble sl of w[jj] for nw packed words (packed-slot order:
-// column 8j + kAwqOrder[sl] of a word sits at slot sl).
-__attribute__((target_clones("avx2", "default")))
-void unpack_nibbles(const int32_t* __restrict__ w, float* __restrict__ v, int64_t nw) {
-  for (int64_t jj = 0; jj < nw; ++jj) {
-    const uint32_t u = (uint32_t)w[jj];
-    for (int sl = 0; sl < 8; ++sl) v[8 * jj + sl] = (float)((u >> (4 * sl)) & 15u);
+// One 128-k group of a W4A16 column block of packed words (VU: one vector of
+// them) for P rows: accg[p][sl][jj] = sum over the group's k, in order, of
+// x_p[k] * (nibble sl of word jj) -- one vector of words per k, the 8 slot
+// accumulators in registers.
+#define MIMOE_VEC(name, T, n) typedef T name __attribute__((vector_size(4 * (n))))
+MIMOE_VEC(vu16, uint32_t, 16); MIMOE_VEC(vi16, int32_t, 16); MIMOE_VEC(vf16, float, 16);
+MIMOE_VEC(vu8, uint32_t, 8); MIMOE_VEC(vi8, int32_t, 8); MIMOE_VEC(vf8, float, 8);
+MIMOE_VEC(vu4, uint32_t, 4); MIMOE_VEC(vi4, int32_t, 4); MIMOE_VEC(vf4, float, 4);
+MIMOE_VEC(vu2, uint32_t, 2); MIMOE_VEC(vi2, int32_t, 2); MIMOE_VEC(vf2, float, 2);
+#undef MIMOE_VEC
+
+template <typename VU, typename VI, typename VF>
+__attribute__((always_inline)) inline void awq_group_t(const int32_t* __restrict__ q, int64_t NW, int64_t k0,
+                                                       const float* const* xf, int64_t P, float* __restrict__ accg) {
+  for (int64_t p = 0; p < P; ++p) {
+    VF acc[8];
+    for (int sl = 0; sl < 8; ++sl) acc[sl] = VF{};
+    const float* x = xf[p] + k0;
+    for (int64_t k = 0; k < 128; ++k) {
+      VU w;
+      memcpy(&w, q + (k0 + k) * NW, sizeof(w));
+      const float xk = x[k];
+      for (int sl = 0; sl < 8; ++sl) {
+        const VI n = (VI)((w >> (uint32_t)(4 * sl)) & 15u);
+        acc[sl] += xk * __builtin_convertvector(n, VF);
+      }
+    }
+    memcpy(accg + p * 8 * (sizeof(VF) / 4), acc, sizeof(acc));
   }
 }
 
-__attribute__((target_clones("avx2", "default")))
-void axpy(float* __restrict__ y, const float* __restrict__ v, float a, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) y[i] += a * v[i];
+__attribute__((target_clones("avx512f", "avx2", "default")))
+void awq_group(int nww, const int32_t* q, int64_t NW, int64_t k0, const float* const* xf, int64_t P, float* accg) {
+  switch (nww) {
+    case 16: awq_group_t<vu16, vi16, vf16>(q, NW, k0, xf, P, accg); break;
+    case 8: awq_group_t<vu8, vi8, vf8>(q, NW, k0, xf, P, accg); break;
+    case 4: awq_group_t<vu4, vi4, vf4>(q, NW, k0, xf, P, accg); break;
+    default: awq_group_t<vu2, vi2, vf2>(q, NW, k0, xf, P, accg); break;
+  }
 }
 
 // Columns [8*j0, 8*j1) of an AWQ matrix (qweight [K][N/8], qzeros [K/128][N/8],
 // scales [K/128][N]) against P fp32 rows xf[p] [K] with group sums xs[p]
-// [K/128]: out[p][n] = sum_g s * (sum_k x_k q_kn - z * xs_g).
+// [K/128]: out[p][n] = sum_g s * (sum_k x_k q_kn - z * xs_g).  j1 - j0 is
+// 2, 4, 8 or 16 words.
 void awq_cols(const int32_t* q, const int32_t* z, const uint16_t* s, int sdt, int64_t K, int64_t N, int64_t j0,
               int64_t j1, const float* const* xf, const float* const* xs, int64_t P, float* const* out) {
   const int64_t NW = N / 8, G = K / 128, nw = j1 - j0, nc = nw * 8;
-  // acc / accg / sf / zf in packed-slot order: index 8*(j-j0) + sl
-  std::vector<float> acc((size_t)(P * nc), 0.0f), accg((size_t)(P * nc)), sf((size_t)nc), zf((size_t)nc),
-      v((size_t)nc);
+  // acc / accg / sf / zf in slot-major order: index sl*nw + (j - j0)
+  std::vector<float> acc((size_t)(P * nc), 0.0f), accg((size_t)(P * nc)), sf((size_t)nc), zf((size_t)nc);
   for (int64_t g = 0; g < G; ++g) {
-    std::fill(accg.begin(), accg.end(), 0.0f);
-    for (int64_t k = 128 * g; k < 128 * g + 128; ++k) {
-      unpack_nibbles(q + k * NW + j0, v.data(), nw);
-      for (int64_t p = 0; p < P; ++p) axpy(&accg[p * nc], v.data(), xf[p][k], nc);
-    }
+    awq_group((int)nw, q + j0, NW, 128 * g, xf, P, accg.data());
     for (int64_t j = j0; j < j1; ++j) {
       const uint32_t u = (uint32_t)z[g * NW + j];
       for (int sl = 0; sl < 8; ++sl) {
-        const int64_t i = 8 * (j - j0) + sl;
+        const int64_t i = sl * nw + (j - j0);
         zf[i] = (float)((u >> (4 * sl)) & 15u);
         sf[i] = half_f32(s[g * N + 8 * j + kAwqOrder[sl]], sdt);
       }
@@ -220,7 +242,7 @@ void awq_cols(const int32_t* q, const int32_t* z, const uint16_t* s, int sdt, in
   }
   for (int64_t p = 0; p < P; ++p)
     for (int64_t j = j0; j < j1; ++j)
-      for (int sl = 0; sl < 8; ++sl) out[p][8 * j + kAwqOrder[sl]] = acc[p * nc + 8 * (j - j0) + sl];
+      for (int sl = 0; sl < 8; ++sl) out[p][8 * j + kAwqOrder[sl]] = acc[p * nc + sl * nw + (j - j0)];
 }
 
 float silu_mul(float g, float u) { return u * (g / (1.0f + expf(-g))); }

@@ -113,6 +113,20 @@ __global__ void add_partial_kernel(uint16_t* __restrict__ y, const float* __rest
   }
 }
 
+// The call's inputs into the pinned host buffers the host callback reads:
+// hidden rows (nx16 16-byte words), ids and weights (n each).  Vector stores
+// straight into host memory, so the side stream carries no copy commands.
+__global__ void stage_inputs_kernel(const u32x4_t* __restrict__ x, int64_t nx16, const int32_t* __restrict__ ids,
+                                    const float* __restrict__ w, int64_t n, u32x4_t* __restrict__ xh,
+                                    int32_t* __restrict__ idsh, float* __restrict__ wh) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nx16; i += stride) xh[i] = x[i];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    idsh[i] = ids[i];
+    wh[i] = w[i];
+  }
+}
+
 int default_threads() {
   const unsigned hc = std::thread::hardware_concurrency();
   const int n = hc ? (int)hc : 1;
@@ -376,12 +390,19 @@ MI_API int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y, cons
   const int64_t n = T * K, H = hh->H;
   rc = grow(hh, T, n, st);
   if (rc) return rc;
-  // side stream: inputs to the host, cold experts, partial back to the device
+  // inputs to the host buffers on the caller's stream (after the previous
+  // call's add kernel, so after its host pass), then the side stream: cold
+  // experts in a host callback, the partial back to the device.  Copy
+  // commands on the side stream were measured to hold the caller's thread
+  // until the previous callback had run; a kernel does not.
+  const int64_t nx16 = T * H * 2 / 16;
+  const int64_t nmax = nx16 > n ? nx16 : n;
+  const int sgrid = (int)((nmax + 255) / 256 < 1024 ? (nmax + 255) / 256 : 1024);
+  hipLaunchKernelGGL(stage_inputs_kernel, dim3(sgrid), dim3(256), 0, st, (const u32x4_t*)x, nx16, topk_ids, topk_w, n,
+                     (u32x4_t*)hh->x_h.p, (int32_t*)hh->ids_h.p, (float*)hh->w_h.p);
+  HCHK(hipGetLastError());
   HCHK(hipEventRecord(hh->ev_in, st));
   HCHK(hipStreamWaitEvent(hh->side, hh->ev_in, 0));
-  HCHK(hipMemcpyAsync(hh->x_h.p, x, (size_t)(T * H) * 2, hipMemcpyDeviceToHost, hh->side));
-  HCHK(hipMemcpyAsync(hh->ids_h.p, topk_ids, (size_t)n * sizeof(int32_t), hipMemcpyDeviceToHost, hh->side));
-  HCHK(hipMemcpyAsync(hh->w_h.p, topk_w, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, hh->side));
   CallCtx* ctx = new (std::nothrow) CallCtx{hh, T, K, act_dtype, std::chrono::steady_clock::now()};
   if (!ctx) return hfail(MI_MOE_EINVAL, "out of host memory");
   hipError_t e = hipLaunchHostFunc(hh->side, host_callback, ctx);
