@@ -184,24 +184,31 @@ MIMOE_VEC(vu4, uint32_t, 4); MIMOE_VEC(vi4, int32_t, 4); MIMOE_VEC(vf4, float, 4
 MIMOE_VEC(vu2, uint32_t, 2); MIMOE_VEC(vi2, int32_t, 2); MIMOE_VEC(vf2, float, 2);
 #undef MIMOE_VEC
 
+template <typename VU, typename VI, typename VF, int PC>
+__attribute__((always_inline)) inline void awq_group_pc(const int32_t* __restrict__ q, int64_t NW, int64_t k0,
+                                                        const float* const* xf, float* __restrict__ accg) {
+  VF acc[PC][8];
+  for (int pp = 0; pp < PC; ++pp)
+    for (int sl = 0; sl < 8; ++sl) acc[pp][sl] = VF{};
+  for (int64_t k = k0; k < k0 + 128; ++k) {
+    VU w;
+    memcpy(&w, q + k * NW, sizeof(w));
+    for (int sl = 0; sl < 8; ++sl) {
+      const VF v = __builtin_convertvector((VI)((w >> (uint32_t)(4 * sl)) & 15u), VF);
+      for (int pp = 0; pp < PC; ++pp) acc[pp][sl] += xf[pp][k] * v;
+    }
+  }
+  memcpy(accg, acc, sizeof(acc));
+}
+
+// Rows in pairs (one unpack of the words for both), the last one alone.
 template <typename VU, typename VI, typename VF>
 __attribute__((always_inline)) inline void awq_group_t(const int32_t* __restrict__ q, int64_t NW, int64_t k0,
                                                        const float* const* xf, int64_t P, float* __restrict__ accg) {
-  for (int64_t p = 0; p < P; ++p) {
-    VF acc[8];
-    for (int sl = 0; sl < 8; ++sl) acc[sl] = VF{};
-    const float* x = xf[p] + k0;
-    for (int64_t k = 0; k < 128; ++k) {
-      VU w;
-      memcpy(&w, q + (k0 + k) * NW, sizeof(w));
-      const float xk = x[k];
-      for (int sl = 0; sl < 8; ++sl) {
-        const VI n = (VI)((w >> (uint32_t)(4 * sl)) & 15u);
-        acc[sl] += xk * __builtin_convertvector(n, VF);
-      }
-    }
-    memcpy(accg + p * 8 * (sizeof(VF) / 4), acc, sizeof(acc));
-  }
+  constexpr int64_t stride = 8 * (sizeof(VF) / 4);   // floats per row of accg
+  int64_t p = 0;
+  for (; p + 2 <= P; p += 2) awq_group_pc<VU, VI, VF, 2>(q, NW, k0, xf + p, accg + p * stride);
+  if (p < P) awq_group_pc<VU, VI, VF, 1>(q, NW, k0, xf + p, accg + p * stride);
 }
 
 __attribute__((target_clones("avx512f", "avx2", "default")))
