@@ -219,10 +219,10 @@ int mi_moe_hybrid_store_awq(mi_moe_hybrid* hh, const int32_t* w13_qweight,
 
 /* The fused MoE layer over all E experts, arguments as mi_moe_forward (device
  * pointers, stream-ordered).  On `stream`: the ids of cold experts are
- * remapped to -1 and the device handle runs the hot ones into y; meanwhile a
- * side stream of the handle copies x, ids and topk_w to pinned host memory
- * and runs the cold experts in a stream host callback into a pinned fp32
- * partial, which a device kernel then reads: y = round(y_hot + y_cold), with
+ * remapped to -1, a kernel writes x, ids and topk_w into pinned host memory
+ * and the device handle runs the hot ones into y; meanwhile a side stream of
+ * the handle runs the cold experts in a stream host callback into a pinned
+ * fp32 partial, which a device kernel then reads: y = round(y_hot + y_cold), with
  * y_hot already rounded to the activation dtype.  Calls that overlap on one handle race, as for
  * mi_moe_forward.  Growing the staging buffers synchronizes the streams, so
  * the call is not for graph capture. */
