@@ -149,3 +149,24 @@ def test_hybrid_stats_host_bytes():
     st = hm.stats()
     assert st["host_experts"] == E and st["device_experts"] == 0
     assert st["host_weight_bytes"] == sum(t.numel() * t.element_size() for t in ws)
+
+
+def test_w4a16_task_widths_bit_identical():
+    """One cold expert: the W4A16 column blocks narrow from 16 packed words
+    (1 thread) to 4 (4 threads) and 2 (16 threads) so every thread has work;
+    each output column is summed in the same order at every width."""
+    E, H, I, T, K = 4, 512, 128, 5, 2
+    ws = w4a16_random(E, H, I, seed=70)
+    ids = torch.tensor([[2, 0], [1, 2], [2, 3], [0, 1], [3, 2]], dtype=torch.int32)
+    tw = torch.softmax(torch.randn(T, K, generator=torch.Generator().manual_seed(71)), dim=-1)
+    x = _x(T, H, 72, torch.bfloat16)
+    masked = torch.from_numpy(_mask_ids(ids.numpy(), [2]))
+    ys = []
+    for threads in (1, 4, 16):
+        hm = HybridMoE(E, H, I, nm.W4A16, host_experts=range(E), num_threads=threads)
+        hm.store_awq(*ws)
+        ys.append(hm.host_forward(x, masked, tw))
+    assert torch.equal(ys[0], ys[1]) and torch.equal(ys[0], ys[2])
+    ref = _oracle_w4(x, masked.numpy(), tw.numpy(), ws, E, I)
+    assert max_rel_err(ys[0], torch.from_numpy(ref)) < 1e-5
+    assert torch.all(ys[0][3] == 0)   # token 3 routes no pair to expert 2
