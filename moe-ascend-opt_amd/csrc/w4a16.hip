@@ -177,11 +177,11 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(kP1W
 void w4a16_phase1_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, NJS = NI1 / S, P = a.p1_cols, HI = H >> 3;
+  const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, P = a.p1_cols, HI = H >> 3;
   float* red = reinterpret_cast<float*>(smem);
   unsigned char* meta = smem + S * p1_red_bytes(NW);
   uint16_t* xs = reinterpret_cast<uint16_t*>(meta + S * 80 * G1);
-  const int item = blockIdx.x / NJS, j0 = (blockIdx.x - item * NJS) * S;
+  const int item = blockIdx.y, j0 = blockIdx.x * S;   // grid (I/16/S, items): an item's slices adjacent
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   if (a.x_all)   // uniform; x is [T][H] contiguous
     stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, NW, lane,
@@ -193,6 +193,10 @@ void w4a16_phase1_kernel(W4Args a) {
   }
   // pair index of column col; every lane of the wave calls it
   auto pair_of = [&](int col) { return __shfl(cl.colpair, col & 63); };
+  // token of a pair (pairs are token-major): (pair + 0.5) / K rounded down is
+  // exact in fp32 for the decode path's pairs (< 64, K <= 8)
+  const float rk = 1.0f / (float)c.K;
+  auto tok_of = [&](int pair) { return (int)(((float)pair + 0.5f) * rk); };
   const int e = cl.e, cnt = cl.cnt;
   const size_t blk = (size_t)e * NI1 + j0;   // S consecutive slices: contiguous weights and metadata
   const unsigned char* msrc = a.w13_m + blk * 80 * G1;
@@ -204,13 +208,15 @@ void w4a16_phase1_kernel(W4Args a) {
     const int ncol = min(P, cnt - cb0);
     int xr;   // LDS row of this lane's column
     if (a.x_all) {
-      xr = pair_of(cb0 + min(r, ncol - 1)) / c.K;
+      xr = tok_of(pair_of(cb0 + min(r, ncol - 1)));
     } else {
-      stage_lds(reinterpret_cast<unsigned char*>(xs), ncol * HI, wave, NW, lane, [&](int k) {
-        const int cc = k / HI;
-        const int t = pair_of(cb0 + cc) / c.K;
-        return (const void*)(c.x + (size_t)t * H + 8 * (k - cc * HI));
-      });
+      // the pass's hidden rows: row cc at xs + cc * H, in 1 KB chunks of 64
+      // lanes x 16 B (H % 512 == 0: whole chunks), chunk ch by wave ch % NW
+      for (int cc = 0; cc < ncol; ++cc) {   // uniform
+        const char* src = reinterpret_cast<const char*>(c.x + (size_t)tok_of(pair_of(cb0 + cc)) * H) + 16 * lane;
+        unsigned char* dst = reinterpret_cast<unsigned char*>(xs + (size_t)cc * H);
+        for (int ch = wave; ch < (HI >> 6); ch += NW) __builtin_amdgcn_global_load_lds(src + 1024 * ch, dst + 1024 * ch, 16, 0, 0);
+      }
       xr = min(r, ncol - 1);
     }
     const uint16_t* xrow = xs + xr * H + 32 * q;
@@ -845,7 +851,8 @@ hipError_t launch_awq_repack_all(const int32_t* w13q, const int32_t* w13z, const
 // ================================================================ launchers
 template <int ACT, int NB, int S, int NW>
 static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, NB, S, NW>), dim3(grid), dim3(NW * kWave), lds, st, a);
+  const int njs = (a.c.I >> 4) / S;
+  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, NB, S, NW>), dim3(njs, grid / njs), dim3(NW * kWave), lds, st, a);
 }
 
 // (NB, S, NW) instantiated for phase 1.  S > 1 measured slower on the
