@@ -257,9 +257,11 @@ __device__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int s
   for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
     const int cntp = min(kQTokPerPass, cnt - cb0);
     // Stage A for the staged tokens (Int8-gemm/q8_gemm.cpp:360-377)
+    const float rkb = 1.0f / (float)KB, rk = 1.0f / (float)c.K;
     for (int idx = tid; idx < cntp * KB; idx += NW * kWave) {
-      const int cc = idx / KB, kb = idx - cc * KB;
-      const int t = pairs[cb0 + cc] / c.K;
+      const int cc = div_small(idx, rkb), kb = idx - cc * KB;
+      const int pr = pairs[cb0 + cc];
+      const int t = c.n < (1 << 21) ? div_small(pr, rk) : pr / c.K;   // uniform choice
       const u32x4_t* src = reinterpret_cast<const u32x4_t*>(c.x + (size_t)t * c.H + kb * 32);
       float v[32];
 #pragma unroll
@@ -336,8 +338,9 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
 
   for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
     const int cntp = min(kQTokPerPass, cnt - cb0);
+    const float rkb = 1.0f / (float)KB2;
     for (int idx = tid; idx < cntp * KB2; idx += NW * kWave) {
-      const int cc = idx / KB2, kb = idx - cc * KB2;
+      const int cc = div_small(idx, rkb), kb = idx - cc * KB2;
       const size_t row = (size_t)rv.pair[p0 + cb0 + cc];
       const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.act_q + row * c.I + kb * 32);
       const u32x4_t q0 = src[0], q1 = src[1];
@@ -388,20 +391,20 @@ __global__ __launch_bounds__(NW * kWave) void q_phase1_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
   const QLds L = carve(smem, a.c.H);
-  const int S = a.c.I / 32, item = blockIdx.x / S;
+  const int item = blockIdx.y, sl = blockIdx.x;   // grid (I/32 slices, items)
   if (a.c.n <= kQBallotMaxPairs) {   // uniform
     const int tid = threadIdx.x;
     const BallotCols cl = ballot_cols(a.c, item, tid & 63);   // every wave: same result
     if (!cl.serve) return;   // uniform
     if (tid < kWave) L.route[tid] = cl.colpair;
     __syncthreads();
-    q_phase1<QT, ACT, SC, NW>(a, cl.e, cl.cnt, L.route, blockIdx.x % S, L);
+    q_phase1<QT, ACT, SC, NW>(a, cl.e, cl.cnt, L.route, sl, L);
     return;
   }
   const RouteView rv = sched_route(a.c, L.route, &s_U);
   if (item >= rv.U) return;
   const int e = rv.active[item], p0 = rv.starts[e];
-  q_phase1<QT, ACT, SC, NW>(a, e, rv.starts[e + 1] - p0, rv.pair + p0, blockIdx.x % S, L);
+  q_phase1<QT, ACT, SC, NW>(a, e, rv.starts[e + 1] - p0, rv.pair + p0, sl, L);
 }
 
 template <int QT, int ACT, int SC, int NW>
@@ -410,10 +413,9 @@ __global__ __launch_bounds__(NW * kWave) void q_phase2_kernel(QArgs a) {
   __shared__ int s_U;
   const QLds L = carve(smem, a.c.I);
   const RouteView rv = sched_route(a.c, L.route, &s_U);
-  const int HB = a.c.H / 64;
-  const int ui = blockIdx.x / HB;
+  const int ui = blockIdx.y;   // grid (H/64 blocks, items)
   if (ui >= rv.U) return;
-  q_phase2<QT, ACT, SC, NW>(a, rv, ui, blockIdx.x % HB, L);
+  q_phase2<QT, ACT, SC, NW>(a, rv, ui, blockIdx.x, L);
 }
 
 // Down projection at decode sizes, token-major with the combine fused:
@@ -435,8 +437,8 @@ template <int QT, int ACT, int SC>
 __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, I = c.I, K = c.K, KB2 = I / 32, HB = H / 64, NT = H / 16;
-  const int t = blockIdx.x / NT, jt = blockIdx.x - t * NT;
+  const int H = c.H, I = c.I, K = c.K, KB2 = I / 32, HB = H / 64;
+  const int t = blockIdx.y, jt = blockIdx.x;   // grid (H/16 tiles, T)
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   int8_t* xq = reinterpret_cast<int8_t*>(smem);
   float* xd = reinterpret_cast<float*>(smem + (size_t)K * I);
@@ -454,8 +456,9 @@ __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
   const int kb0 = KB2 * q / 4, kb1 = KB2 * (q + 1) / 4;
   QRowBatch<QT, 2> B;   // both groups a quarter can touch, in flight while the rows are staged
   rows_issue<QT, 2>(B, wtile, stile, row, kb0 & ~3, kb1, KB2);
+  const float rkb = 1.0f / (float)KB2;
   for (int idx = tid; idx < K * KB2; idx += K * 64) {
-    const int cc = idx / KB2, kb = idx - cc * KB2;
+    const int cc = div_small(idx, rkb), kb = idx - cc * KB2;
     const size_t prow = (size_t)t * K + cc;   // pair rows of a token are contiguous
     const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.act_q + prow * I + kb * 32);
     const u32x4_t q0 = src[0], q1 = src[1];
@@ -499,16 +502,16 @@ __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
 template <int QT, int ACT, int SC, int NW>
 static hipError_t launch_q_nw(const QArgs& a, int grid1, int grid2, size_t route, bool token_down,
                               hipStream_t st) {
-  hipLaunchKernelGGL((q_phase1_kernel<QT, ACT, SC, NW>), dim3(grid1), dim3(NW * kWave),
+  hipLaunchKernelGGL((q_phase1_kernel<QT, ACT, SC, NW>), dim3(a.c.I / 32, grid1 / (a.c.I / 32)), dim3(NW * kWave),
                      q_stage_bytes(a.c.H) + route, st, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   if (token_down) {
-    hipLaunchKernelGGL((q_down_token_kernel<QT, ACT, SC>), dim3(a.c.T * (a.c.H / 16)), dim3(64 * a.c.K),
+    hipLaunchKernelGGL((q_down_token_kernel<QT, ACT, SC>), dim3(a.c.H / 16, a.c.T), dim3(64 * a.c.K),
                        q_down_token_lds_bytes(a.c.I, a.c.K), st, a);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((q_phase2_kernel<QT, ACT, SC, NW>), dim3(grid2), dim3(NW * kWave),
+  hipLaunchKernelGGL((q_phase2_kernel<QT, ACT, SC, NW>), dim3(a.c.H / 64, grid2 / (a.c.H / 64)), dim3(NW * kWave),
                      q_stage_bytes(a.c.I) + route, st, a);
   return hipGetLastError();
 }

@@ -193,10 +193,9 @@ void w4a16_phase1_kernel(W4Args a) {
   }
   // pair index of column col; every lane of the wave calls it
   auto pair_of = [&](int col) { return __shfl(cl.colpair, col & 63); };
-  // token of a pair (pairs are token-major): (pair + 0.5) / K rounded down is
-  // exact in fp32 for the decode path's pairs (< 64, K <= 8)
+  // token of a pair (pairs are token-major)
   const float rk = 1.0f / (float)c.K;
-  auto tok_of = [&](int pair) { return (int)(((float)pair + 0.5f) * rk); };
+  auto tok_of = [&](int pair) { return div_small(pair, rk); };
   const int e = cl.e, cnt = cl.cnt;
   const size_t blk = (size_t)e * NI1 + j0;   // S consecutive slices: contiguous weights and metadata
   const unsigned char* msrc = a.w13_m + blk * 80 * G1;
@@ -360,9 +359,9 @@ __global__ __launch_bounds__(kDownMaxK * 64) __attribute__((amdgpu_waves_per_eu(
 void w4a16_down_token_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, I = c.I, K = c.K, MQ = H >> 6, G2 = I >> 7, NTG = (H >> 4) / RT, II = I >> 3;
+  const int H = c.H, I = c.I, K = c.K, MQ = H >> 6, G2 = I >> 7, II = I >> 3;
   const int SEC = w2_meta_sec_bytes(G2);
-  const int t = blockIdx.x / NTG, tile0 = (blockIdx.x - t * NTG) * RT, m = tile0 >> 2, jj0 = tile0 & 3;
+  const int t = blockIdx.y, tile0 = blockIdx.x * RT, m = tile0 >> 2, jj0 = tile0 & 3;   // grid (H/16/RT, T)
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
   uint16_t* as = reinterpret_cast<uint16_t*>(smem);
   unsigned char* meta = smem + (size_t)K * I * 2;
@@ -874,8 +873,8 @@ template <int ACT>
 static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int grid, size_t lds, hipStream_t st) {
 #define P2_CASE(NB_, RT_)                                                                           \
   if (nb == NB_ && rt == RT_) {                                                                     \
-    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3(grid), dim3(64 * a.c.K), lds, \
-                       st, a);                                                                      \
+    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3((a.c.H >> 4) / RT_, grid / ((a.c.H >> 4) / RT_)), \
+                       dim3(64 * a.c.K), lds, st, a);                                               \
     return hipGetLastError();                                                                       \
   }
   P2_CASE(1, 1) P2_CASE(2, 1) P2_CASE(3, 1) P2_CASE(4, 1) P2_CASE(6, 1) P2_CASE(8, 1)
