@@ -154,17 +154,16 @@ __device__ __forceinline__ void wait_copies_and_sync() {
 // weight loads must be issued after the direct-to-LDS copies).
 __device__ __forceinline__ void issue_order_fence() { asm volatile("" ::: "memory"); }
 
-// ================================================================ routing
 // ================================================================ phase 1
 // Register budgets, as waves per SIMD: phase 1 spills above 4; the down
 // kernel (8-wave workgroups) fits 6 without spills, i.e. 3 workgroups per CU.
 constexpr int kP1WavesPerEU = 4;
 constexpr int kDownWavesPerEU = 6;
 // Workgroup (item, slices j = S*js .. S*js+S-1 of 16 rows): gate/up rows of
-// the item's expert over all H (the 4 waves split the H groups), every routed
-// pair of the expert in passes of p1_cols columns; SiLU*mul into act[pair].
-// Each wave keeps the weights of NB groups x S slices in flight together (NB,
-// from the host, divides the wave's H/512 groups); the column sums X of a
+// the item's expert over all H (the NW waves split the H/128 groups), every
+// routed pair of the expert in passes of p1_cols columns; SiLU*mul into
+// act[pair].  Each wave keeps the weights of NB groups x S slices in flight
+// together (NB, from the host, divides the wave's groups); the column sums X of a
 // group are shared by the S slices.  Lanes of columns past the pass read the
 // pass's last column, so the loop body has no branches; their results are
 // never stored.  Hidden rows: with a.x_all the rows of all T tokens are copied
