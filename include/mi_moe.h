@@ -132,8 +132,8 @@ int mi_moe_set_timing(mi_moe_handle* h, int enable);
 int mi_moe_get_last_phase_times_ms(mi_moe_handle* h, double* ms, int max_phases);
 
 /* Stage A activation quantization alone: x [T,H] fp16/bf16 -> x_qs [T,H]
- * int8, x_d [T,H/32] fp32, with the device block quantizer used inside the
- * fused kernels.  Replaces Stage A of moe_forward_ptr_impl
+ * int8, x_d [T,H/32] fp32, with quant_block_q8_0, the device block
+ * quantizer the decode kernels' Stage A also calls.  Replaces Stage A of moe_forward_ptr_impl
  * (Int8-gemm/q8_gemm.cpp:360-377; quantize_block_q8_0,
  * Int8-gemm/gemm_kernels.cpp:25-58). */
 int mi_moe_quantize_act_q8_0(const void* x, int act_dtype, int64_t T,
@@ -157,6 +157,20 @@ int mi_moe_route(const int32_t* topk_ids, int64_t T, int64_t K, int64_t E,
 int mi_moe_block_dots(mi_moe_handle* h, int64_t expert, int proj,
                       const int8_t* a_qs, int64_t M, int32_t* isum,
                       void* stream);
+
+/* The same block dots through the int8-MFMA block routine of the grouped
+ * GEMMs (the path of Q8_0 / Q4_0 calls above 64 routed pairs), for bit-exact
+ * checking of its two exact rewrites: acc[m][n][kb] int32 = the MFMA result
+ * less its 1.5*2^23 bias (Q8_0: isum; Q4_0: 16*isum, the nibbles enter as
+ * bytes 16*(n-8)), prod[m][n][kb] fp32 = the first scaled product the GEMMs
+ * form from that result read as a float (Q8_0: round(isum*dw); Q4_0:
+ * 16*round(isum*dw)).  Shapes as mi_moe_block_dots; needs H and I multiples
+ * of 128; a_qs 8-byte aligned.  Counterpart of the integer block dot and the
+ * first product of its per-block scaling, (float)isum*dw
+ * (Int8-gemm/gemm_kernels.cpp:102-179, 262-358). */
+int mi_moe_block_dots_mfma(mi_moe_handle* h, int64_t expert, int proj,
+                           const int8_t* a_qs, int64_t M, int32_t* acc,
+                           float* prod, void* stream);
 
 /* Router top-k + softmax: logits [T,E] (fp16, bf16 or fp32, device) ->
  * topk_ids [T,K] int32 and topk_w [T,K] fp32 (device), the K largest logits

@@ -8,6 +8,7 @@
 // readable with mi_moe_last_error().
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdlib>
 #include <cstdio>
@@ -45,6 +46,8 @@ hipError_t launch_q8_online_quant(const void*, int, int, int, int, int, int, voi
                                   hipStream_t);
 hipError_t launch_q_block_dots(int, const void*, const int8_t*, int32_t*, int, int, int, int, int,
                                int, int, hipStream_t);
+hipError_t launch_q_mfma_block_check(int, int, const void*, const uint16_t*, const int8_t*, int32_t*, float*,
+                                     int, int, int, int, int, int, int, hipStream_t);
 }  // namespace mimoe
 
 using namespace mimoe;
@@ -216,16 +219,18 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
   a.act = (uint16_t*)h->act.p;
   a.sdt = h->scale_dtype;
   // decode path: T*K <= 64 pairs, at most kDownMaxK experts per token (a
-  // wave each in the down kernel)
+  // wave each in the down kernel), and both kernels' LDS fits; otherwise the
+  // sorted path (mi_moe_create checked that it fits)
   hipEvent_t mid = h->timing ? h->evmid : nullptr;
-  if (n <= 64 && K <= kDownMaxK) {
+  const size_t lmax = device_max_lds();
+  if (n <= 64 && K <= kDownMaxK && w4_decode_fits((int)h->H, (int)h->I, (int)K, lmax)) {
     // phase 1 copies the hidden rows of every token when they are few
-    a.x_all = (size_t)T * h->H * 2 <= kXAllBytes;
+    const int nw1 = w4_p1_waves(n, (int)h->H);
+    a.x_all = (size_t)T * h->H * 2 <= kXAllBytes && w4_p1_lds_bytes((int)h->H, (int)T, 1, nw1) <= lmax;
     // an expert rarely gets more than a few of the T tokens; a narrow pass
     // keeps the LDS small (occupancy), extra columns take another pass
     a.p1_cols = (int)(T < kDecodeCols ? T : kDecodeCols);
-    const int nw1 = w4_p1_waves(n, (int)h->H);
-    while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1, nw1) > kMaxLds) --a.p1_cols;
+    while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1, nw1) > lmax) --a.p1_cols;
     const W4Plan plan = w4a16_plan((int)h->H, (int)h->I);
     HIPCHK(launch_w4a16(a, plan, act, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st, mid));
     h->mid_recorded = mid != nullptr;
@@ -265,7 +270,16 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   a.w2 = h->w2.p; a.w2_d = (const uint16_t*)h->w2_s.p;
   a.act_q = (int8_t*)h->act.p;
   a.act_d = (float*)h->act_d.p;
-  if (n > kQGemmMinPairs && h->H % 128 == 0 && h->I % 128 == 0) {
+  // decode sizes: the lane-per-row kernels, with the down projection and the
+  // combine token-major in one launch (no eout round trip) where it fits;
+  // above kQGemmMinPairs routed pairs, or where the lane-per-row LDS does not
+  // fit, the int8 grouped GEMMs (mi_moe_create checked that one of the two
+  // serves every call)
+  const size_t lmax = device_max_lds();
+  const int iE = (int)h->E, iH = (int)h->H, iI = (int)h->I, in = (int)n, iK = (int)K;
+  bool token_down = n <= kQGemmMinPairs && K <= kDownMaxK && q_lpr_fits(iH, iI, iE, in, iK, true, lmax);
+  const bool lpr_small = n <= kQGemmMinPairs && (token_down || q_lpr_fits(iH, iI, iE, in, iK, false, lmax));
+  if (q_gemm_ok(iH, iI) && !lpr_small) {
     // sorted path: Q8_0 activations once per token, routing with row tiles,
     // the two int8 grouped GEMMs, the combine
     a.xq = (const int8_t*)h->xq.p;
@@ -279,8 +293,8 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
   const int64_t umax = n < h->E ? n : h->E;
   const int64_t grid1 = (n <= kQBallotMaxPairs ? n : umax) * (h->I / 32), grid2 = umax * (h->H / 64);
-  // decode sizes: down + combine token-major in one launch (no eout round trip)
-  const bool token_down = n <= kQGemmMinPairs && K <= kDownMaxK;
+  if (!q_lpr_fits(iH, iI, iE, in, iK, token_down, lmax))
+    return fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 call of %lld routed pairs does not fit the device's LDS", (long long)n);
   HIPCHK(launch_qint(a, h->quant, act, h->scale_dtype, (int)grid1, (int)grid2, token_down, st));
   if (!token_down) HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
   return MI_MOE_OK;
@@ -309,7 +323,33 @@ int check_dims(int64_t E, int64_t H, int64_t I, int quant_type) {
   if (quant_type == MI_MOE_W4A16 && (H % 512 != 0 || I % 128 != 0))
     return fail(MI_MOE_EINVAL, "W4A16 needs hidden_size %% 512 == 0 and intermediate_size %% 128 == 0");
   if (E > 512) return fail(MI_MOE_EUNSUPPORTED, "at most 512 experts");
+  // one path must serve calls of every size: the W4A16 grouped GEMMs, or for
+  // Q8_0 / Q4_0 the int8 grouped GEMMs or else the lane-per-row kernels at
+  // the largest in-LDS routing
+  const size_t lmax = device_max_lds();
+  if (quant_type == MI_MOE_W4A16 && !w4_sorted_fits((int)H, (int)I, lmax))
+    return fail(MI_MOE_EUNSUPPORTED, "W4A16 H=%lld I=%lld: the grouped GEMMs need %zu and %zu bytes of LDS, "
+                "the device allows %zu", (long long)H, (long long)I, w4_gemm13_lds_bytes((int)H),
+                w4_gemm2_lds_bytes((int)I), lmax);
+  if (quant_type != MI_MOE_W4A16 && !q_gemm_ok((int)H, (int)I) &&
+      !q_lpr_fits((int)H, (int)I, (int)E, kRouteLdsMax, 1, false, lmax))
+    return fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 H=%lld I=%lld: not multiples of 128 and too large for the "
+                "lane-per-row kernels' LDS", (long long)H, (long long)I);
   return MI_MOE_OK;
+}
+
+size_t device_max_lds() {
+  static std::atomic<int> cache[64];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kMaxLds;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return (size_t)v;
+  int lds = 0;
+  if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+      lds < (int)kMaxLds)
+    lds = (int)kMaxLds;
+  cache[dev].store(lds, std::memory_order_relaxed);
+  return (size_t)lds;
 }
 }  // namespace mimoe
 
@@ -483,6 +523,30 @@ MI_API int mi_moe_block_dots(mi_moe_handle* h, int64_t expert, int proj, const i
   const int tiles = proj == 0 ? (int)(h->I / 32) : (int)(h->H / 64);
   HIPCHK(launch_q_block_dots(h->quant, proj == 0 ? h->w13.p : h->w2.p, a_qs, isum, (int)M, (int)N,
                              (int)K, (int)expert, proj, (int)h->I, tiles, (hipStream_t)stream));
+  return MI_MOE_OK;
+}
+
+MI_API int mi_moe_block_dots_mfma(mi_moe_handle* h, int64_t expert, int proj, const int8_t* a_qs,
+                                  int64_t M, int32_t* acc, float* prod, void* stream) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  if (h->quant != MI_MOE_Q8_0 && h->quant != MI_MOE_Q4_0)
+    return fail(MI_MOE_EINVAL, "block dots need a Q8_0 or Q4_0 handle");
+  if (!h->loaded) return fail(MI_MOE_ENOTLOADED, "weights not stored");
+  if (h->H % 128 != 0 || h->I % 128 != 0)
+    return fail(MI_MOE_EUNSUPPORTED, "the int8-MFMA grouped GEMMs need H %% 128 == 0 and I %% 128 == 0");
+  if (expert < 0 || expert >= h->E || (proj != 0 && proj != 1) || M < 0)
+    return fail(MI_MOE_EINVAL, "bad expert / proj / M");
+  if (M == 0) return MI_MOE_OK;
+  if (M > 65535 * 16) return fail(MI_MOE_EINVAL, "M too large");
+  if (!a_qs || !acc || !prod) return fail(MI_MOE_EINVAL, "null pointer");
+  if (((uintptr_t)a_qs & 7u) != 0) return fail(MI_MOE_EINVAL, "a_qs must be 8-byte aligned");
+  const int64_t N = proj == 0 ? 2 * h->I : h->H, K = proj == 0 ? h->H : h->I;
+  const int tiles = proj == 0 ? (int)(h->I / 32) : (int)(h->H / 64);
+  HIPCHK(launch_q_mfma_block_check(h->quant, h->scale_dtype, proj == 0 ? h->w13.p : h->w2.p,
+                                   (const uint16_t*)(proj == 0 ? h->w13_s.p : h->w2_s.p), a_qs, acc, prod,
+                                   (int)M, (int)N, (int)K, (int)expert, proj, (int)h->I, tiles,
+                                   (hipStream_t)stream));
   return MI_MOE_OK;
 }
 

@@ -323,9 +323,10 @@ hipError_t launch_combine(const float* eout, const float* tw, const int32_t* ids
   return hipGetLastError();
 }
 
-// Stage A: one thread per 32-element block.  quantize_block_q8_0 rule
-// (Int8-gemm/gemm_kernels.cpp:37-57): amax, d = amax/127, id = 1/d (0 if d==0),
-// q = sat8(RNE(x*id)); d stays fp32 (Int8-gemm/q8_gemm.cpp:371-375).
+// Stage A: one thread per 32-element block, through quant_block_q8_0 (the
+// block quantizer of the decode kernels too): amax, d = amax/127, id = 1/d (0
+// if d == 0), q = sat8(RNE(x*id)) (Int8-gemm/gemm_kernels.cpp:37-57); d stays
+// fp32 (Int8-gemm/q8_gemm.cpp:371-375).
 template <int ACT>
 __global__ void quant_act_q8_0_kernel(const uint16_t* __restrict__ x, int64_t nblk,
                                       int8_t* __restrict__ qs, float* __restrict__ d) {
@@ -343,27 +344,8 @@ __global__ void quant_act_q8_0_kernel(const uint16_t* __restrict__ x, int64_t nb
         v[8 * c + 2 * h + 1] = to_f32<ACT>(ws[h] >> 16);
       }
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const float av = __builtin_fabsf(v[j]);
-      amax = av > amax ? av : amax;
-    }
-    const float dd = amax / 127.0f;
-    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-    uint32_t packed[8];
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int h = 0; h < 4; ++h)
-        word |= ((uint32_t)(uint8_t)q8_round(v[4 * w + h] * id)) << (8 * h);
-      packed[w] = word;
-    }
-    u32x4_t* dst = reinterpret_cast<u32x4_t*>(qs + b * 32);
-    dst[0] = u32x4_t{packed[0], packed[1], packed[2], packed[3]};
-    dst[1] = u32x4_t{packed[4], packed[5], packed[6], packed[7]};
-    d[b] = dd;
+    int qsum;
+    d[b] = quant_block_q8_0(v, qs + b * 32, &qsum);
   }
 }
 

@@ -108,6 +108,48 @@ __device__ __forceinline__ int8_t q8_round(float v) {
   return (int8_t)(int)r;
 }
 
+// Scale of a Q8_0 block from its amax: d = amax / 127, *id = 1 / d (0 when
+// d == 0).  Every Q8_0 quantization in this library goes through it.
+__device__ __forceinline__ float q8_block_scale(float amax, float* id) {
+  const float d = amax / 127.0f;
+  *id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  return d;
+}
+
+// Q8_0 quantization of 32 fp32 values (quantize_block_q8_0,
+// Int8-gemm/gemm_kernels.cpp:25-58): returns d, writes the 32 bytes to dst
+// (16-byte aligned) and the sum of the q values to *qsum.  The one block
+// quantizer of the activation paths: the standalone Stage-A kernel, the
+// decode kernels' Stage A and the online weight quantization call it.
+__device__ __forceinline__ float quant_block_q8_0(const float (&v)[32], int8_t* dst, int* qsum) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const float av = __builtin_fabsf(v[j]);
+    amax = av > amax ? av : amax;
+  }
+  float id;
+  const float d = q8_block_scale(amax, &id);
+  int s = 0;
+  uint32_t packed[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int8_t q = q8_round(v[4 * w + h] * id);
+      s += q;
+      word |= ((uint32_t)(uint8_t)q) << (8 * h);
+    }
+    packed[w] = word;
+  }
+  u32x4_t* o = reinterpret_cast<u32x4_t*>(dst);
+  o[0] = u32x4_t{packed[0], packed[1], packed[2], packed[3]};
+  o[1] = u32x4_t{packed[4], packed[5], packed[6], packed[7]};
+  *qsum = s;
+  return d;
+}
+
 // ------------------------------------------------------------ routing
 // Stable counting sort of the routed (t,k) pairs by expert, the semantics of
 // preprocess_moe_routing (Int8-gemm/moe_common.cpp:146-216): counts, exclusive

@@ -76,7 +76,13 @@ struct W4Args {
 // Bytes of the w2 metadata of one 16-row tile: G2 = I/128 groups of 16 u16
 // scales and 8 bytes of zero nibbles, rounded up to 16 bytes.
 __host__ __device__ inline int w2_meta_sec_bytes(int G2) { return (40 * G2 + 15) & ~15; }
-constexpr size_t kMaxLds = 65536;   // dynamic LDS a kernel launch may ask for
+// LDS a launch may ask for without opting in (hipFuncSetAttribute), and the
+// most a workgroup may use on the current device
+// (hipDeviceAttributeMaxSharedMemoryPerBlock, queried once per device; 64 KB
+// if the query fails).  Path choices test the layer's LDS needs against the
+// latter.
+constexpr size_t kMaxLds = 65536;
+size_t device_max_lds();
 
 // The decode down kernel runs a wave per routed expert of a token.
 constexpr int kDownMaxK = 8;
@@ -98,11 +104,65 @@ __host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) 
   return (size_t)K * I * 2 + (size_t)K * RT * w2_meta_sec_bytes(I >> 7) + (size_t)K * 16 * RT * 4 + (size_t)K * 4;
 }
 
+// W4A16 decode path: both kernels fit in `lds` bytes (phase 1 with one token
+// column per pass).
+inline bool w4_decode_fits(int H, int I, int K, size_t lds) {
+  return w4_p1_lds_bytes(H, 1, 1, 4) <= lds && w4_down_token_lds_bytes(I, K, 1) <= lds;
+}
+
+// W4A16 grouped GEMMs (sorted path): 64-row tiles staged with a 272-byte row
+// stride (256 B of a 128-group + 16 B that spread the rows over the LDS
+// banks), double-buffered, with the row sums and pair indices; gate_up takes
+// kGemm13Blocks blocks of 4 slices, down kGemm2Quads quads of 64 rows of H,
+// and each stages the workgroup's metadata for all of K.
+constexpr int kGemmRowStride = 272;
+constexpr int kGemmABytes = kGemmRows * kGemmRowStride;
+constexpr size_t kGemmLds = 2 * (size_t)kGemmABytes + 3 * kGemmRows * sizeof(float);
+constexpr int kGemm13Blocks = 2;
+constexpr int kGemm2Quads = 4;
+inline size_t w4_gemm13_lds_bytes(int H) { return kGemmLds + (size_t)4 * kGemm13Blocks * 80 * (H >> 7); }
+inline size_t w4_gemm2_lds_bytes(int I) { return kGemmLds + (size_t)kGemm2Quads * 4 * w2_meta_sec_bytes(I >> 7); }
+inline bool w4_sorted_fits(int H, int I, size_t lds) {
+  return (H / 64) % kGemm2Quads == 0 && (I / 64) % kGemm13Blocks == 0 && w4_gemm13_lds_bytes(H) <= lds &&
+         w4_gemm2_lds_bytes(I) <= lds;
+}
+
 // Launch geometry of the W4A16 kernels (see w4a16_plan).
 struct W4Plan {
   int nb1, s1;    // phase 1: groups per load batch, 16-row slices per workgroup
   int nb2, rt2;   // down: groups per load batch, 16-row tiles per wave
 };
+
+// Q8_0 / Q4_0 lane-per-row kernels: LDS of the phase kernels for a K range
+// of Kmax (kQTokPerPass tokens' activation bytes, scales and byte sums, and
+// the cross-wave partials of up to kQDecWavesMax waves), plus the routing
+// arrays when they live in LDS; the token-major down kernel's LDS: act bytes
+// [K][I] | act d [K][I/32] | act byte sums [K][I/32] | quarter partials
+// [K][64] | outputs [K][16] | valid [K].
+constexpr int kQDecWavesMax = 8;
+__host__ __device__ inline size_t q_stage_bytes(int Kmax) {
+  return (size_t)kQTokPerPass * Kmax + (size_t)kQTokPerPass * (Kmax / 32) * 8 +
+         (size_t)kQDecWavesMax * kQTokPerPass * 64 * 4;
+}
+__host__ __device__ inline size_t q_down_token_lds_bytes(int I, int K) {
+  return (size_t)K * I + (size_t)K * (I / 32) * 8 + (size_t)K * 64 * 4 + (size_t)K * 16 * 4 + (size_t)K * 4;
+}
+__host__ __device__ inline size_t route_lds_ints(int E, int n) { return (size_t)3 * E + 1 + 2 * (size_t)n; }
+// LDS of the routing arrays of the lane-per-row kernels for n routed pairs
+// (at least the ballot path's 64-entry pair list).
+inline size_t q_route_lds_bytes(int E, int n) {
+  const size_t r = n > kRouteLdsMax ? 0 : route_lds_ints(E, n) * sizeof(int);
+  return r < 64 * sizeof(int) ? 64 * sizeof(int) : r;
+}
+// The lane-per-row path fits for n routed pairs (token_down: the down
+// projection token-major, the combine fused; else expert-major phase 2).
+inline bool q_lpr_fits(int H, int I, int E, int n, int K, bool token_down, size_t lds) {
+  const size_t route = q_route_lds_bytes(E, n);
+  if (q_stage_bytes(H) + route > lds) return false;
+  return token_down ? q_down_token_lds_bytes(I, K) <= lds : q_stage_bytes(I) + route <= lds;
+}
+// The int8 grouped GEMMs (any n) need H and I multiples of 128.
+inline bool q_gemm_ok(int H, int I) { return H % 128 == 0 && I % 128 == 0; }
 
 // Q8_0 / Q4_0 fused kernel (qint.hip).
 struct QArgs {

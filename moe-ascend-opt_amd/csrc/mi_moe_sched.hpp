@@ -23,8 +23,6 @@ struct RouteView {
   int U;
 };
 
-__host__ __device__ inline size_t route_lds_ints(int E, int n) { return (size_t)3 * E + 1 + 2 * (size_t)n; }
-
 // Route (LDS or global) -> RouteView.  route_lds_buf holds route_lds_ints(E,n)
 // ints when !c.route_global.
 __device__ inline RouteView sched_route(const SchedArgs& c, int* route_lds_buf, int* s_U) {

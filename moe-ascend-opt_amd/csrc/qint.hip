@@ -94,43 +94,11 @@ __device__ __forceinline__ int block_isum(const int (&wd)[8], const int* xv, int
   return s;
 }
 
-// Q8_0 quantization of 32 fp32 values (quantize_block_q8_0,
-// Int8-gemm/gemm_kernels.cpp:25-58): returns d, writes 32 bytes, sum of q.
-__device__ __forceinline__ float quant_block_q8_0(const float (&v)[32], int8_t* dst, int* qsum) {
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const float av = __builtin_fabsf(v[j]);
-    amax = av > amax ? av : amax;
-  }
-  const float d = amax / 127.0f;
-  const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
-  int s = 0;
-  uint32_t packed[8];
-#pragma unroll
-  for (int w = 0; w < 8; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int8_t q = q8_round(v[4 * w + h] * id);
-      s += q;
-      word |= ((uint32_t)(uint8_t)q) << (8 * h);
-    }
-    packed[w] = word;
-  }
-  u32x4_t* o = reinterpret_cast<u32x4_t*>(dst);
-  o[0] = u32x4_t{packed[0], packed[1], packed[2], packed[3]};
-  o[1] = u32x4_t{packed[4], packed[5], packed[6], packed[7]};
-  *qsum = s;
-  return d;
-}
-
 // Integer decode path (lane-per-row kernels): the NW waves of a workgroup
 // split K, and a wave's first batch of weight groups is issued before the
 // activations are staged.  NW = 8 for the smallest calls (kQDecWideMaxPairs
 // routed pairs or fewer: few workgroups, each wave's chain is shorter), 4
 // above (occupancy).
-constexpr int kQDecWavesMax = 8;
 constexpr int kQDecWideMaxPairs = 8;
 
 // One lane's row weights (whole 4-block layout groups, as 16-byte loads) and
@@ -308,8 +276,8 @@ __device__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int s
         const float o = __shfl_xor(amax, m, 32);
         amax = o > amax ? o : amax;
       }
-      const float d = amax / 127.0f;
-      const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+      float id;
+      const float d = q8_block_scale(amax, &id);
       const int8_t q = q8_round(act * id);
       if (cc < cntp) {
         const size_t row = (size_t)pairs[cb0 + cc];
@@ -377,10 +345,6 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
 }
 
 // ---------------------------------------------------------------- kernels
-__host__ __device__ inline size_t q_stage_bytes(int Kmax) {
-  return (size_t)kQTokPerPass * Kmax + (size_t)kQTokPerPass * (Kmax / 32) * 8 +
-         (size_t)kQDecWavesMax * kQTokPerPass * 64 * 4;
-}
 
 // Work items: up to kQBallotMaxPairs routed pairs, one per pair (the item
 // serves its expert iff it is the expert's first pair; ballot routing, the
@@ -429,9 +393,6 @@ __global__ __launch_bounds__(NW * kWave) void q_phase2_kernel(QArgs a) {
 // no valid id gets y = 0.
 // LDS: act bytes [K][I] | act d [K][I/32] | act byte sums [K][I/32] | quarter
 // partials [K][64] | outputs [K][16] | valid [K].
-__host__ __device__ inline size_t q_down_token_lds_bytes(int I, int K) {
-  return (size_t)K * I + (size_t)K * (I / 32) * 8 + (size_t)K * 64 * 4 + (size_t)K * 16 * 4 + (size_t)K * 4;
-}
 
 template <int QT, int ACT, int SC>
 __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
@@ -499,29 +460,39 @@ __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
   }
 }
 
+// Dynamic LDS beyond kMaxLds needs the kernel's opt-in.
+template <class Kern>
+static void lds_opt_in(Kern k, size_t lds) {
+  if (lds > kMaxLds)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+}
+
 template <int QT, int ACT, int SC, int NW>
 static hipError_t launch_q_nw(const QArgs& a, int grid1, int grid2, size_t route, bool token_down,
                               hipStream_t st) {
+  const size_t l1 = q_stage_bytes(a.c.H) + route;
+  lds_opt_in(q_phase1_kernel<QT, ACT, SC, NW>, l1);
   hipLaunchKernelGGL((q_phase1_kernel<QT, ACT, SC, NW>), dim3(a.c.I / 32, grid1 / (a.c.I / 32)), dim3(NW * kWave),
-                     q_stage_bytes(a.c.H) + route, st, a);
+                     l1, st, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   if (token_down) {
-    hipLaunchKernelGGL((q_down_token_kernel<QT, ACT, SC>), dim3(a.c.H / 16, a.c.T), dim3(64 * a.c.K),
-                       q_down_token_lds_bytes(a.c.I, a.c.K), st, a);
+    const size_t l2 = q_down_token_lds_bytes(a.c.I, a.c.K);
+    lds_opt_in(q_down_token_kernel<QT, ACT, SC>, l2);
+    hipLaunchKernelGGL((q_down_token_kernel<QT, ACT, SC>), dim3(a.c.H / 16, a.c.T), dim3(64 * a.c.K), l2, st, a);
     return hipGetLastError();
   }
+  const size_t l2 = q_stage_bytes(a.c.I) + route;
+  lds_opt_in(q_phase2_kernel<QT, ACT, SC, NW>, l2);
   hipLaunchKernelGGL((q_phase2_kernel<QT, ACT, SC, NW>), dim3(a.c.H / 64, grid2 / (a.c.H / 64)), dim3(NW * kWave),
-                     q_stage_bytes(a.c.I) + route, st, a);
+                     l2, st, a);
   return hipGetLastError();
 }
 
 template <int QT, int ACT, int SC>
 static hipError_t launch_q_t(const QArgs& a, int grid1, int grid2, bool token_down, hipStream_t st) {
-  size_t route = a.c.route_global ? 0 : route_lds_ints(a.c.E, a.c.n) * sizeof(int);
-  if (route < kWave * sizeof(int)) route = kWave * sizeof(int);   // the ballot path's pair list
-  if (q_stage_bytes(a.c.H) + route > kMaxLds || q_stage_bytes(a.c.I) + route > kMaxLds) return hipErrorInvalidValue;
-  if (token_down && q_down_token_lds_bytes(a.c.I, a.c.K) > kMaxLds) return hipErrorInvalidValue;
+  const size_t route = q_route_lds_bytes(a.c.E, a.c.n);
+  if (!q_lpr_fits(a.c.H, a.c.I, a.c.E, a.c.n, a.c.K, token_down, device_max_lds())) return hipErrorInvalidValue;
   return a.c.n <= kQDecWideMaxPairs ? launch_q_nw<QT, ACT, SC, 8>(a, grid1, grid2, route, token_down, st)
                                     : launch_q_nw<QT, ACT, SC, 4>(a, grid1, grid2, route, token_down, st);
 }
@@ -591,6 +562,27 @@ constexpr size_t kQgLds = 2 * (size_t)kQgBufBytes + kGemmRows * 4;
 constexpr int kQgBias = 0x4B400000;      // bits of 1.5 * 2^23
 constexpr float kQgBiasF = 12582912.0f;  // 1.5 * 2^23
 
+// A weight scale as the GEMMs use it: dw (fp32) and nb = -1.5 * 2^23 * dw.
+template <int SC>
+__device__ __forceinline__ void qg_wscale(uint32_t bits, float& dw, float& nb) {
+  dw = to_f32<SC>(bits);
+  nb = -kQgBiasF * dw;
+}
+
+// The int8 MFMA of one 32-element block from the bias accumulator: lane
+// 16q + r of the result holds kQgBias + (weight row 4q + i) . (tile row r)
+// for i < 4 (Q4_0: kQgBias + 16 * isum).
+__device__ __forceinline__ i32x4_t qg_mfma(long wb, long av) {
+  i32x4_t d = {kQgBias, kQgBias, kQgBias, kQgBias};
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(wb, av, d, 0, 0, 0);
+}
+
+// The first scaled product of a block, round(isum * dw) (Q4_0: 16 times it),
+// from an MFMA result read as a float: fma(1.5 * 2^23 + isum, dw, nb).
+__device__ __forceinline__ float qg_scaled(int dbits, float dw, float nb) {
+  return __builtin_fmaf(__int_as_float(dbits), dw, nb);
+}
+
 // one thread's share of a step's staging: a 32-byte block of its row and the
 // block's scale; in wave 0 also 4 weight scales (block lane / 16, rows
 // 4 * (lane % 16) .. +3)
@@ -616,11 +608,14 @@ __device__ __forceinline__ void qg_store(unsigned char* buf, int srow, int sblk,
   if (w0 && !CONV) {
     *reinterpret_cast<u32x2_t*>(buf + kQgABytes + kQgDaBytes + (lane >> 4) * 128 + 8 * (lane & 15)) = s.dw;
   } else if (w0) {
-    const float d0 = to_f32<SC>(s.dw.x & 0xffffu), d1 = to_f32<SC>(s.dw.x >> 16);
-    const float d2 = to_f32<SC>(s.dw.y & 0xffffu), d3 = to_f32<SC>(s.dw.y >> 16);
+    float d[4], nb[4];
+    qg_wscale<SC>(s.dw.x & 0xffffu, d[0], nb[0]);
+    qg_wscale<SC>(s.dw.x >> 16, d[1], nb[1]);
+    qg_wscale<SC>(s.dw.y & 0xffffu, d[2], nb[2]);
+    qg_wscale<SC>(s.dw.y >> 16, d[3], nb[3]);
     f32x4_t* o = reinterpret_cast<f32x4_t*>(buf + kQgABytes + kQgDaBytes + (lane >> 4) * 512 + 32 * (lane & 15));
-    o[0] = f32x4_t{d0, -kQgBiasF * d0, d1, -kQgBiasF * d1};
-    o[1] = f32x4_t{d2, -kQgBiasF * d2, d3, -kQgBiasF * d3};
+    o[0] = f32x4_t{d[0], nb[0], d[1], nb[1]};
+    o[1] = f32x4_t{d[2], nb[2], d[3], nb[3]};
   }
 }
 
@@ -646,16 +641,12 @@ __device__ __forceinline__ void qg_block(const unsigned char* buf, int sblk, int
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) {
     const long av = *reinterpret_cast<const long*>(buf + (16 * s + r) * kQgRowStride + 32 * sblk + 8 * q);
-    i32x4_t d = {kQgBias, kQgBias, kQgBias, kQgBias};
-    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(wb, av, d, 0, 0, 0);
+    const i32x4_t d = qg_mfma(wb, av);
     const float da = dq[s][sblk];
     const int dv[4] = {d.x, d.y, d.z, d.w};
     float* ac = reinterpret_cast<float*>(&acc[s]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float t1 = __builtin_fmaf(__int_as_float(dv[i]), dws[i], nb[i]);
-      ac[i] = __builtin_fmaf(t1, da, ac[i]);
-    }
+    for (int i = 0; i < 4; ++i) ac[i] = __builtin_fmaf(qg_scaled(dv[i], dws[i], nb[i]), da, ac[i]);
   }
 }
 
@@ -741,10 +732,7 @@ __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq,
                 *reinterpret_cast<const u32x2_t*>(buf + kQgABytes + kQgDaBytes + b * 128 + (tlb + 4 * q) * 2);
             const uint32_t rw[4] = {raw.x & 0xffffu, raw.x >> 16, raw.y & 0xffffu, raw.y >> 16};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              dws[i] = to_f32<SC>(rw[i]);
-              nb[i] = -kQgBiasF * dws[i];
-            }
+            for (int i = 0; i < 4; ++i) qg_wscale<SC>(rw[i], dws[i], nb[i]);
           }
           qg_block<NSUB>(buf, b, r, q, qg_wbytes<QT>(ws[u].w[b]), dws, nb, dq, acc);
           // keep each block's scaling next to its MFMAs: left free, the fma
@@ -835,8 +823,8 @@ __global__ __launch_bounds__(kBlock) void q_gemm13_kernel(QArgs a) {
       const float o = __shfl_xor(amax, m);
       amax = o > amax ? o : amax;
     }
-    const float d = amax / 127.0f;
-    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    float id;
+    const float d = q8_block_scale(amax, &id);
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -1060,6 +1048,65 @@ __global__ void q_block_dots_kernel(const void* __restrict__ wbase, const int8_t
     }
     isum[idx] = block_isum<QT>(wd, xv, xsum);
   }
+}
+
+// Inverse of row_to_tile: the matrix row held by lane `lane` of tile ti.
+__device__ __forceinline__ int tile_lane_row(int proj, int ti, int lane, int I) {
+  if (proj == 0) return lane < 32 ? 32 * ti + lane : I + 32 * ti + lane - 32;
+  return 64 * ti + lane;
+}
+
+// The grouped GEMMs' int8-MFMA block routine on given activation rows: the
+// weights of one step as QgWSet loads them, qg_wbytes, qg_mfma from the bias
+// accumulator and qg_scaled with qg_wscale's (dw, nb) -- the functions
+// qg_block and qg_gemm call.  acc[m][n][kb] = the MFMA result minus the bias
+// (Q8_0: isum; Q4_0: 16 * isum), prod[m][n][kb] = the first scaled product
+// (Q8_0: round(isum * dw); Q4_0: 16 * round(isum * dw)).  A wave per (16
+// lanes of a weight tile, step of kQgStage blocks, 16 activation rows).
+template <int QT, int SC>
+__global__ __launch_bounds__(64) void q_mfma_block_check_kernel(const void* __restrict__ wbase,
+                                                                const uint16_t* __restrict__ sbase,
+                                                                const int8_t* __restrict__ a_qs,
+                                                                int32_t* __restrict__ acc, float* __restrict__ prod,
+                                                                int M, int N, int K, int e, int proj, int I,
+                                                                int tiles_per_e) {
+  const int KB = K / 32;
+  const int lane = threadIdx.x, q = lane >> 4, r = lane & 15;
+  const int ti = blockIdx.x >> 2, tlb = (blockIdx.x & 3) * 16;
+  const int kb0 = blockIdx.y * kQgStage, m0 = blockIdx.z * 16;
+  const size_t tile = (size_t)e * tiles_per_e + ti;
+  const char* wtile = (const char*)wbase + tile * KB * QFmt<QT>::block_bytes;
+  const uint16_t* stile = sbase + tile * KB * 64;
+  QgWSet<QT> ws;
+  ws.load(wtile, KB, kb0, tlb + r, q);
+  const int ma = min(m0 + r, M - 1);   // activation row of this lane's column
+#pragma unroll
+  for (int b = 0; b < kQgStage; ++b) {
+    const long av = *reinterpret_cast<const long*>(a_qs + (size_t)ma * K + 32 * (kb0 + b) + 8 * q);
+    const i32x4_t d = qg_mfma(qg_wbytes<QT>(ws.w[b]), av);
+    const int dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tl = tlb + 4 * q + i;
+      float dw, nb;
+      qg_wscale<SC>(stile[(kb0 + b) * 64 + tl], dw, nb);
+      if (m0 + r < M) {
+        const size_t o = ((size_t)(m0 + r) * N + tile_lane_row(proj, ti, tl, I)) * KB + kb0 + b;
+        acc[o] = dv[i] - kQgBias;
+        prod[o] = qg_scaled(dv[i], dw, nb);
+      }
+    }
+  }
+}
+
+hipError_t launch_q_mfma_block_check(int qt, int sdt, const void* wbase, const uint16_t* sbase, const int8_t* a_qs,
+                                     int32_t* acc, float* prod, int M, int N, int K, int e, int proj, int I,
+                                     int tiles_per_e, hipStream_t st) {
+  const dim3 grid((unsigned)(tiles_per_e * 4), (unsigned)(K / 32 / kQgStage), (unsigned)((M + 15) / 16));
+  auto kern = qt == 0 ? (sdt == 1 ? q_mfma_block_check_kernel<0, 1> : q_mfma_block_check_kernel<0, 0>)
+                      : (sdt == 1 ? q_mfma_block_check_kernel<1, 1> : q_mfma_block_check_kernel<1, 0>);
+  hipLaunchKernelGGL(kern, grid, dim3(64), 0, st, wbase, sbase, a_qs, acc, prod, M, N, K, e, proj, I, tiles_per_e);
+  return hipGetLastError();
 }
 
 hipError_t launch_q_block_dots(int qt, const void* wbase, const int8_t* a_qs, int32_t* isum, int M,

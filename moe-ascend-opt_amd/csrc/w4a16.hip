@@ -416,12 +416,10 @@ void w4a16_down_token_kernel(W4Args a) {
 // staged rows.  Every weight byte is read and dequantized once per
 // row tile, so an expert with many rows streams its weights a few times and
 // the MFMAs work on full 16-row operands.
-constexpr int kGemmRowStride = 272;   // 256 B of a row + 16 B that spread the rows over the LDS banks
-constexpr int kGemmABytes = kGemmRows * kGemmRowStride;
-// LDS: staged rows [2][kGemmABytes] | row sums [2][kGemmRows] f32 | pair of each row [kGemmRows]
-// | the workgroup's metadata (gemm13: 4 * kGemm13Blocks slice blocks of 80*G1 B;
-// gemm2: 4 * kGemm2Quads sections of w2_meta_sec_bytes(G2) B)
-constexpr size_t kGemmLds = 2 * (size_t)kGemmABytes + 3 * kGemmRows * sizeof(float);
+// LDS (kGemmLds, w4_gemm13_lds_bytes, w4_gemm2_lds_bytes): staged rows
+// [2][kGemmABytes] | row sums [2][kGemmRows] f32 | pair of each row
+// [kGemmRows] | the workgroup's metadata (gemm13: 4 * kGemm13Blocks slice
+// blocks of 80*G1 B; gemm2: 4 * kGemm2Quads sections of w2_meta_sec_bytes(G2) B)
 
 // Copy nbytes (a multiple of 16) from global to LDS with the workgroup's
 // threads; the caller's barrier makes them visible.
@@ -494,7 +492,6 @@ __device__ __forceinline__ void gemm_group(const unsigned char* buf, const float
 // 4 slices, a slice = 16 gate and 16 up rows); wave w owns slice w of each
 // block, so a staged activation row serves 2 * kGemm13Blocks weight tiles per
 // wave.  act[pair] gets the slices' 16 values each.
-constexpr int kGemm13Blocks = 2;
 template <int ACT>
 __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
   constexpr int NB = kGemm13Blocks;
@@ -608,7 +605,6 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
 // activation row serves kGemm2Quads weight tiles (the rows are re-staged by
 // every workgroup of the tile: 2 quads halve that traffic).  eout[pair] gets
 // the tiles' fp32 values; the combine kernel sums over k.
-constexpr int kGemm2Quads = 4;
 template <int ACT>
 __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
   const SchedArgs& c = a.c;
@@ -699,10 +695,12 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
 
 hipError_t launch_w4a16_gemm(const W4Args& a, int act, int tiles_max, hipStream_t st, hipEvent_t mid) {
   const int g13 = tiles_max * (a.c.I / 64 / kGemm13Blocks), g2 = tiles_max * (a.c.H / 64 / kGemm2Quads);
-  const size_t lds13 = kGemmLds + (size_t)4 * kGemm13Blocks * 80 * (a.c.H / 128);
-  const size_t lds2 = kGemmLds + (size_t)kGemm2Quads * 4 * w2_meta_sec_bytes(a.c.I / 128);
-  if ((a.c.H / 64) % kGemm2Quads || (a.c.I / 64) % kGemm13Blocks) return hipErrorInvalidValue;
-  if (lds13 > kMaxLds || lds2 > kMaxLds) return hipErrorInvalidValue;
+  const size_t lds13 = w4_gemm13_lds_bytes(a.c.H), lds2 = w4_gemm2_lds_bytes(a.c.I);
+  if (!w4_sorted_fits(a.c.H, a.c.I, device_max_lds())) return hipErrorInvalidValue;
+  if (lds13 > kMaxLds) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(act == 1 ? w4a16_gemm13_kernel<1> : w4a16_gemm13_kernel<0>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds13);
+  if (lds2 > kMaxLds) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(act == 1 ? w4a16_gemm2_kernel<1> : w4a16_gemm2_kernel<0>),
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
   if (act == 1)
     hipLaunchKernelGGL((w4a16_gemm13_kernel<1>), dim3(g13), dim3(kBlock), lds13, st, a);
   else
@@ -849,6 +847,9 @@ hipError_t launch_awq_repack_all(const int32_t* w13q, const int32_t* w13z, const
 // ================================================================ launchers
 template <int ACT, int NB, int S, int NW>
 static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
+  if (lds > kMaxLds)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_phase1_kernel<ACT, NB, S, NW>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   const int njs = (a.c.I >> 4) / S;
   hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, NB, S, NW>), dim3(njs, grid / njs), dim3(NW * kWave), lds, st, a);
 }
@@ -872,6 +873,9 @@ template <int ACT>
 static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int grid, size_t lds, hipStream_t st) {
 #define P2_CASE(NB_, RT_)                                                                           \
   if (nb == NB_ && rt == RT_) {                                                                     \
+    if (lds > kMaxLds)                                                                              \
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_down_token_kernel<ACT, NB_, RT_>), \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);              \
     hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3((a.c.H >> 4) / RT_, grid / ((a.c.H >> 4) / RT_)), \
                        dim3(64 * a.c.K), lds, st, a);                                               \
     return hipGetLastError();                                                                       \
@@ -915,7 +919,7 @@ static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int g
   while ((G1 / nw1) % nb1) --nb1;
   const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1, nw1);
   const size_t lds2 = w4_down_token_lds_bytes(a.c.I, a.c.K, p.rt2);
-  if (lds1 > kMaxLds || lds2 > kMaxLds) return hipErrorInvalidValue;
+  if (lds1 > device_max_lds() || lds2 > device_max_lds()) return hipErrorInvalidValue;
   hipError_t err = dispatch_p1<ACT>(a, nb1, p.s1, nw1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;

@@ -36,6 +36,7 @@ C_SYMBOLS = (
     "mi_moe_get_info", "mi_moe_store_quantized", "mi_moe_quantize_and_store_expert",
     "mi_moe_store_awq", "mi_moe_forward", "mi_moe_get_last_run_time_ms",
     "mi_moe_set_timing", "mi_moe_quantize_act_q8_0", "mi_moe_route", "mi_moe_block_dots",
+    "mi_moe_block_dots_mfma",
     "mi_moe_get_last_phase_times_ms", "mi_moe_topk_softmax", "mi_moe_forward_logits",
     "mi_moe_hybrid_create", "mi_moe_hybrid_destroy", "mi_moe_hybrid_store_quantized",
     "mi_moe_hybrid_store_awq", "mi_moe_hybrid_forward", "mi_moe_hybrid_host_forward",
@@ -89,6 +90,7 @@ def capi():
     L.mi_moe_quantize_act_q8_0.argtypes = [P, I, I64, I64, P, P, P]
     L.mi_moe_route.argtypes = [P, I64, I64, I64, P, P, P, P, P]
     L.mi_moe_block_dots.argtypes = [P, I64, I, P, I64, P, P]
+    L.mi_moe_block_dots_mfma.argtypes = [P, I64, I, P, I64, P, P, P]
     L.mi_moe_topk_softmax.argtypes = [P, I, I64, I64, I64, I, P, P, P]
     L.mi_moe_forward_logits.argtypes = [P, P, P, P, I, I64, I64, I, I, P, P, P]
     L.mi_moe_hybrid_create.argtypes = [I64, I64, I64, I, P, I, ctypes.POINTER(P)]

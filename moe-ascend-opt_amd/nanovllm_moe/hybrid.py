@@ -78,11 +78,32 @@ class HybridMoE:
         if on_dev:
             torch.cuda.synchronize()
 
+    def _check_shapes(self, hidden, topk_ids, topk_w):
+        """The C ABI trusts T, H and K; mismatched tensors are rejected here
+        (the same rules as the torch op, nanovllm_shim.cpp forward_into)."""
+        import torch
+        if hidden.dim() != 2 or topk_ids.dim() != 2 or topk_w.dim() != 2:
+            raise ValueError("expected hidden [T,H], topk_ids [T,K], topk_w [T,K]")
+        if hidden.shape[1] != self.H:
+            raise ValueError(f"hidden size {hidden.shape[1]} != handle H {self.H}")
+        if topk_ids.shape[0] != hidden.shape[0] or topk_w.shape[0] != hidden.shape[0]:
+            raise ValueError("topk_ids / topk_w rows must equal the token count of hidden")
+        if topk_w.shape[1] != topk_ids.shape[1]:
+            raise ValueError("topk_ids and topk_w must have the same top_k")
+        if hidden.dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError(f"hidden must be float16 or bfloat16, got {hidden.dtype}")
+
     def forward(self, hidden, topk_ids, topk_w, out=None):
         import torch
         from . import check, dtype_code, stream_ptr
         if not (hidden.is_cuda and topk_ids.is_cuda and topk_w.is_cuda):
             raise ValueError("forward takes HIP tensors; host_forward runs the cold experts on host tensors")
+        self._check_shapes(hidden, topk_ids, topk_w)
+        if topk_ids.device != hidden.device or topk_w.device != hidden.device:
+            raise ValueError("hidden, topk_ids and topk_w must be on the same device")
+        if out is not None and (out.shape != hidden.shape or out.dtype != hidden.dtype
+                                or out.device != hidden.device or not out.is_contiguous()):
+            raise ValueError("out must be a contiguous tensor with hidden's shape, dtype and device")
         x = hidden.contiguous()
         ids = topk_ids.to(torch.int32).contiguous()
         w = topk_w.to(torch.float32).contiguous()
@@ -95,6 +116,7 @@ class HybridMoE:
     def host_forward(self, hidden, topk_ids, topk_w):
         import torch
         from . import check, dtype_code
+        self._check_shapes(hidden, topk_ids, topk_w)
         x = hidden.detach().cpu().contiguous()
         ids = topk_ids.detach().cpu().to(torch.int32).contiguous()
         w = topk_w.detach().cpu().to(torch.float32).contiguous()

@@ -59,7 +59,6 @@ def lib():
         _lib.orc_route.restype = ctypes.c_int64
         _lib.orc_moe_forward_q.restype = ctypes.c_int
         _lib.orc_moe_forward_w4a16.restype = ctypes.c_int
-        _lib.orc_expert_row_q.restype = ctypes.c_int
         for fn in ("orc_f32_to_f16", "orc_f32_to_bf16"):
             getattr(_lib, fn).restype = ctypes.c_uint16
             getattr(_lib, fn).argtypes = [ctypes.c_float]
@@ -170,24 +169,6 @@ def moe_forward_q(qt, act_dtype, scale_dtype, x_bits, topk_w, topk_ids,
     if rc != 0:
         raise RuntimeError("orc_moe_forward_q failed (unsupported top_k or shape)")
     return y, yf
-
-
-def expert_row_q(qt, scale_dtype, x_qs_row, x_d_row, e, gate_up_qs, gate_up_d,
-                 down_qs, down_d, H, I):
-    gate_up = np.zeros(2 * I, np.float32)
-    act = np.zeros(I, np.float32)
-    act_qs = np.zeros(I, np.int8)
-    act_d = np.zeros(I // 32, np.float32)
-    out = np.zeros(H, np.float32)
-    rc = lib().orc_expert_row_q(
-        ctypes.c_int(qt), ctypes.c_int(scale_dtype),
-        _p(np.ascontiguousarray(x_qs_row, dtype=np.int8)),
-        _p(np.ascontiguousarray(x_d_row, dtype=np.float32)), _i64(e),
-        _p(np.ascontiguousarray(gate_up_qs)), _p(np.ascontiguousarray(gate_up_d, dtype=np.uint16)),
-        _p(np.ascontiguousarray(down_qs)), _p(np.ascontiguousarray(down_d, dtype=np.uint16)),
-        _i64(H), _i64(I), _p(gate_up), _p(act), _p(act_qs), _p(act_d), _p(out))
-    assert rc == 0
-    return gate_up, act, act_qs, act_d, out
 
 
 def awq_dequant(qweight, qzeros, scales_bits, scale_dtype, group):

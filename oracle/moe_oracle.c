@@ -246,36 +246,6 @@ void orc_silu_and_mul(float* row, int64_t ish) {
 /* ------------------------------------------------------------------ */
 /* Fused forward, Q8_0 / Q4_0 -- Int8-gemm/q8_gemm.cpp:276-646          */
 /* ------------------------------------------------------------------ */
-int orc_expert_row_q(int qt, int scale_dtype, const int8_t* x_qs,
-                     const float* x_d, int64_t e, const void* gate_up_qs,
-                     const uint16_t* gate_up_d, const void* down_qs,
-                     const uint16_t* down_d, int64_t H, int64_t I,
-                     float* gate_up, float* act, int8_t* act_qs, float* act_d,
-                     float* expert_out) {
-  if (H % 32 || I % 32) return -1;
-  const int64_t wdiv = (qt == 1) ? 8 : 1;
-  const int8_t* gu_base8 = (const int8_t*)gate_up_qs;
-  const uint32_t* gu_base4 = (const uint32_t*)gate_up_qs;
-  const void* gu = qt == 1 ? (const void*)(gu_base4 + e * 2 * I * H / wdiv)
-                           : (const void*)(gu_base8 + e * 2 * I * H);
-  const uint16_t* gud = gate_up_d + e * 2 * I * (H / 32);
-  for (int64_t n = 0; n < 2 * I; ++n)
-    gate_up[n] = gemm_row_dot(qt, x_qs, x_d, gu, gud, scale_dtype, n, H, 0, H / 32);
-  float* tmp = (float*)malloc(sizeof(float) * 2 * I);
-  memcpy(tmp, gate_up, sizeof(float) * 2 * I);
-  orc_silu_and_mul(tmp, I);
-  memcpy(act, tmp, sizeof(float) * I);
-  free(tmp);
-  for (int64_t b = 0; b < I / 32; ++b)
-    orc_quantize_block_q8_0(act + b * 32, &act_d[b], act_qs + b * 32);
-  const void* dn = qt == 1 ? (const void*)((const uint32_t*)down_qs + e * H * I / wdiv)
-                           : (const void*)((const int8_t*)down_qs + e * H * I);
-  const uint16_t* dnd = down_d + e * H * (I / 32);
-  for (int64_t h = 0; h < H; ++h)
-    expert_out[h] = gemm_row_dot(qt, act_qs, act_d, dn, dnd, scale_dtype, h, I, 0, I / 32);
-  return 0;
-}
-
 int orc_moe_forward_q(int qt, int act_dtype, int scale_dtype,
                       const uint16_t* x, uint16_t* y, float* y_f32,
                       const float* topk_w, const int32_t* topk_ids,

@@ -89,16 +89,6 @@ int orc_moe_forward_q(int qt, int act_dtype, int scale_dtype,
                       int64_t T, int64_t H, int64_t E, int64_t I, int64_t tp,
                       int64_t K);
 
-/* Per-expert intermediates of the Q path for one (token,k) routed row
- * (tp = 1): gate_up fp32 [2I], act fp32 [I] (after silu_and_mul), act_qs [I],
- * act_d [I/32], expert_out fp32 [H].  Used to pin each stage separately. */
-int orc_expert_row_q(int qt, int scale_dtype, const int8_t* x_qs,
-                     const float* x_d, int64_t e, const void* gate_up_qs,
-                     const uint16_t* gate_up_d, const void* down_qs,
-                     const uint16_t* down_d, int64_t H, int64_t I,
-                     float* gate_up, float* act, int8_t* act_qs, float* act_d,
-                     float* expert_out);
-
 /* W4A16 AWQ-style weight dequantization of one expert projection:
  * qweight int32 [K, N/8], qzeros int32 [K/g, N/8], scales [K/g, N] (bits) ->
  * w fp32 [N, K] (row n = output).  Nibble slot s of a packed word holds

@@ -70,3 +70,17 @@ def test_argument_errors_are_status_codes():
     assert b"null handle" in L.mi_moe_last_error()
     assert L.mi_moe_destroy(None) == 0
     assert L.mi_moe_get_last_run_time_ms(None) < 0
+
+
+def test_create_rejects_shapes_no_path_serves():
+    """Without a GPU the LDS limit is 64 KB: a W4A16 handle whose grouped GEMMs
+    do not fit (DeepSeek-like H = 7168: 71,424 B for gate_up) is refused with
+    EUNSUPPORTED at create time; shapes that fit are accepted by the shape
+    rules (create then fails only for want of a HIP device)."""
+    L = nanovllm_moe.capi()
+    h = ctypes.c_void_p()
+    assert L.mi_moe_create(8, 7168, 2048, 2, ctypes.byref(h)) == 3
+    assert b"LDS" in L.mi_moe_last_error()
+    assert L.mi_moe_create(8, 2048, 768, 2, ctypes.byref(h)) in (0, 4)
+    if h.value:
+        L.mi_moe_destroy(h)

@@ -1,8 +1,12 @@
 """GPU parity of the Q8_0 / Q4_0 path (the reference CPU algorithm,
 Int8-gemm/q8_gemm.cpp:276-646) against the oracle on identical inputs.
 
-* per-32-block int32 dot products: bit-exact (mi_moe_block_dots, the same
-  device routine the fused kernels use), Q8_0 and Q4_0, both projections;
+* per-32-block int32 dot products: bit-exact (mi_moe_block_dots, the v_dot4
+  routine of the lane-per-row kernels), Q8_0 and Q4_0, both projections;
+* the int8-MFMA block routine of the grouped GEMMs (mi_moe_block_dots_mfma):
+  its bias-accumulator int32 result and the first scaled product read back
+  from it, bit-exact against the oracle's dots and (float)isum * dw, with
+  extreme weights and activations;
 * the fused layer: fp32 sums differ from the oracle only by the wave-split
   summation order, so outputs agree to max-rel-err <= 1e-2 (observed ~1e-3,
   dominated by rare intermediate Q8_0 rounding flips); above 64 routed pairs
@@ -165,6 +169,80 @@ def test_block_dots_bit_exact(cuda, qt):
         L.mi_moe_destroy(hp)
 
 
+def _extreme_wire(qt, E, H, I, seed):
+    """Wire weights whose first rows hold the extremes: Q8_0 rows of -128, of
+    127 and alternating; Q4_0 rows of nibble 0, of 15 and alternating; the
+    rest uniform over the whole code range.  Scales: random fp16 of both
+    signs, with a few large and tiny magnitudes."""
+    rng = np.random.default_rng(seed)
+    if qt == 0:
+        q13 = rng.integers(-128, 128, size=(E, 2 * I, H)).astype(np.int8)
+        q2 = rng.integers(-128, 128, size=(E, H, I)).astype(np.int8)
+        for q in (q13, q2):
+            q[:, 0] = -128
+            q[:, 1] = 127
+            q[:, 2, 0::2], q[:, 2, 1::2] = -128, 127
+    else:
+        def words(R, K):
+            nib = rng.integers(0, 16, size=(E, R, K)).astype(np.uint32)
+            nib[:, 0] = 0
+            nib[:, 1] = 15
+            nib[:, 2, 0::2], nib[:, 2, 1::2] = 0, 15
+            w = np.zeros((E, R, K // 8), np.uint32)
+            for i in range(8):
+                w |= nib[:, :, i::8] << np.uint32(4 * i)
+            return w.view(np.int32)
+        q13, q2 = words(2 * I, H), words(H, I)
+
+    def scales(shape):
+        d = (rng.standard_normal(shape) * 0.01).astype(np.float16)
+        d.reshape(-1)[:3] = np.array([60000.0, -1.0e-4, 6.1e-5], np.float16)
+        return torch.from_numpy(d)
+    return (torch.from_numpy(q13), scales((E, 2 * I, H // 32)), torch.from_numpy(q2), scales((E, H, I // 32)))
+
+
+@pytest.mark.parametrize("qt", [0, 1])
+def test_mfma_block_dots_bit_exact(cuda, qt):
+    """The int8-MFMA block routine of the grouped GEMMs (mi_moe_block_dots_mfma)
+    against the oracle's exact block dots: the MFMA result less its 1.5*2^23 bias
+    is isum (Q4_0: 16*isum, nibbles entering as bytes 16*(n-8)), and the first
+    scaled product read back from it as a float is the fp32 product
+    (float)isum * dw of gemm_kernels.cpp:156-179 (Q4_0: 16 times it), bit for
+    bit.  Activations include rows of -128, of 127 and alternating."""
+    E, H, I = 2, 256, 128
+    gq, gd, dq, dd = _extreme_wire(qt, E, H, I, seed=5 + qt)
+    L = nanovllm_moe.capi()
+    hp = ctypes.c_void_p()
+    nanovllm_moe.check(L.mi_moe_create(E, H, I, qt, ctypes.byref(hp)), "create")
+    try:
+        nanovllm_moe.check(L.mi_moe_store_quantized(hp, gq.data_ptr(), gd.data_ptr(), dq.data_ptr(),
+                                                    dd.data_ptr(), nanovllm_moe.F16, 0, None), "store")
+        rng = np.random.default_rng(11)
+        for e in range(E):
+            for proj, (N, K, wq, wd) in enumerate(((2 * I, H, gq, gd), (H, I, dq, dd))):
+                a = rng.integers(-128, 128, size=(19, K)).astype(np.int8)
+                a[0], a[1] = -128, 127
+                a[2, 0::2], a[2, 1::2] = -128, 127
+                at = torch.from_numpy(a).to(cuda)
+                acc = torch.empty(a.shape[0], N, K // 32, dtype=torch.int32, device=cuda)
+                prod = torch.empty(a.shape[0], N, K // 32, dtype=torch.float32, device=cuda)
+                nanovllm_moe.check(L.mi_moe_block_dots_mfma(hp, e, proj, at.data_ptr(), a.shape[0],
+                                                            acc.data_ptr(), prod.data_ptr(),
+                                                            nanovllm_moe.stream_ptr()), "block_dots_mfma")
+                torch.cuda.synchronize()
+                isum = oracle.block_dots(qt, a, wq[e].contiguous().numpy(), N, K)
+                dw = wd[e].numpy().astype(np.float32)[None, :, :]
+                want = isum.astype(np.float32) * dw             # fp32 RNE product, as the reference
+                m = 16 if qt == 1 else 1
+                got_acc, got_prod = acc.cpu().numpy(), prod.cpu().numpy()
+                assert np.array_equal(got_acc, isum * m), (e, proj)
+                assert np.array_equal(got_prod.view(np.uint32), (want * np.float32(m)).view(np.uint32)), (e, proj)
+                if qt == 0:   # the extremes reach the block's largest |isum|
+                    assert np.abs(isum).max() == 32 * 128 * 128
+    finally:
+        L.mi_moe_destroy(hp)
+
+
 def test_online_quant_matches_oracle(cuda):
     E, H, I = 8, 256, 128
     w = _weights(0, E, H, I, seed=31)
@@ -182,3 +260,19 @@ def test_online_quant_matches_oracle(cuda):
     y2 = _run(h2, x, ids, tw, cuda)
     assert torch.equal(y, y2)          # same bytes, same scales, same kernels
     assert max_rel_err(y, _oracle(0, x, ids, tw, w, E, I)) <= TOL
+
+
+@pytest.mark.parametrize("qt", [0, 1])
+@pytest.mark.parametrize("E,H,I,T,K", [(4, 5120, 256, 1, 4), (4, 5120, 256, 9, 8),
+                                       (3, 256, 14336, 1, 2), (3, 256, 14336, 30, 2)])
+def test_large_shape_parity(cuda, qt, E, H, I, T, K):
+    """GLM-like H = 5120 (the lane-per-row gate_up needs 10H + 16 KB of LDS) and
+    Mixtral-like I = 14336 at K = 2: calls of up to 64 routed pairs take the
+    lane-per-row kernels where their LDS fits and the int8 grouped GEMMs
+    otherwise."""
+    w = _weights(qt, E, H, I, seed=60 + qt)
+    h = _handle(qt, E, H, I, w, True, cuda)
+    ids, tw = topk_routing(T, E, K, seed=T + 1)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(T + 2)).to(torch.bfloat16)
+    y = _run(h, x, ids, tw, cuda)
+    assert max_rel_err(y, _oracle(qt, x, ids, tw, w, E, I)) <= TOL

@@ -238,3 +238,28 @@ def test_minimax_shape_parity(cuda):
         x = torch.randn(bs, H, generator=torch.Generator().manual_seed(bs)).to(torch.bfloat16)
         y = _run(h, x, ids, tw, cuda)
         assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, torch.bfloat16)) <= TOL
+
+
+def _device_lds():
+    p = torch.cuda.get_device_properties(0)
+    return max(getattr(p, "shared_memory_per_block_optin", 0), getattr(p, "shared_memory_per_block", 0), 65536)
+
+
+@pytest.mark.parametrize("T,K", [(1, 2), (3, 2), (40, 2)])
+def test_large_intermediate_parity(cuda, T, K):
+    """Mixtral-like I = 14336: the decode down kernel needs 66,440 B of LDS at
+    K = 2 and the sorted down GEMM 107,264 B.  Calls take the decode path where
+    it fits, else the sorted path; a handle is refused only if the sorted GEMMs
+    exceed the device's LDS (checked at create, status 3)."""
+    E, H, I = 3, 512, 14336
+    need_sorted = 2 * 64 * 272 + 3 * 64 * 4 + 16 * ((40 * (I // 128) + 15) & ~15)
+    w = w4a16_random(E, H, I, seed=77 + T)
+    if need_sorted > _device_lds():
+        with pytest.raises(RuntimeError, match="status 3"):
+            _handle(E, H, I, w, True, cuda)
+        return
+    h = _handle(E, H, I, w, True, cuda)
+    ids, tw = topk_routing(T, E, K, seed=T)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
+    y = _run(h, x, ids, tw, cuda)
+    assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, torch.bfloat16)) <= TOL

@@ -170,3 +170,28 @@ def test_w4a16_task_widths_bit_identical():
     ref = _oracle_w4(x, masked.numpy(), tw.numpy(), ws, E, I)
     assert max_rel_err(ys[0], torch.from_numpy(ref)) < 1e-5
     assert torch.all(ys[0][3] == 0)   # token 3 routes no pair to expert 2
+
+
+def test_host_forward_rejects_mismatched_shapes():
+    """The C ABI trusts T, H and K: HybridMoE checks the tensors first."""
+    E, H, I, T, K = 4, 256, 128, 3, 2
+    hm = HybridMoE(E, H, I, 0, host_experts=range(E), num_threads=1)
+    try:
+        x = torch.zeros(T, H, dtype=torch.bfloat16)
+        ids = torch.zeros(T, K, dtype=torch.int32)
+        w = torch.zeros(T, K, dtype=torch.float32)
+        bad = [
+            (torch.zeros(T, H + 32, dtype=torch.bfloat16), ids, w),     # hidden size
+            (x, torch.zeros(T + 1, K, dtype=torch.int32), w),          # ids rows
+            (x, ids, torch.zeros(T - 1, K)),                           # weight rows
+            (x, ids, torch.zeros(T, K + 1)),                           # top_k disagree
+            (x.reshape(-1), ids, w),                                   # not 2-D
+            (x.float(), ids, w),                                       # dtype
+        ]
+        for args in bad:
+            with pytest.raises(ValueError):
+                hm.host_forward(*args)
+        with pytest.raises(ValueError):   # forward needs HIP tensors, checked first
+            hm.forward(x, ids, w)
+    finally:
+        hm.close()
