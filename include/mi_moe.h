@@ -113,6 +113,28 @@ int mi_moe_forward(mi_moe_handle* h, const void* x, void* y,
                    const float* topk_w, const int32_t* topk_ids, int64_t T,
                    int64_t K, int act_dtype, void* stream);
 
+/* Size of the device array that holds the workspace of
+ * mi_moe_forward_noalloc: 32 MiB per GPU. */
+#define MI_MOE_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* mi_moe_forward without device memory allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as mi_moe_forward, but the call's
+ * workspace (routing arrays, intermediate activations, per-pair outputs) is
+ * carved from a static device array of MI_MOE_NOALLOC_SCRATCH_BYTES that each
+ * GPU holds from the library's load until the process ends, instead of the
+ * handle's grown buffers; it calls no hipMalloc / hipFree and records no
+ * timing events.  A call whose workspace exceeds the array returns
+ * MI_MOE_EINVAL (decode sizes need well under 1 MiB; at H=2048, I=768 the
+ * limit is about 3,000 routed pairs, where the per-pair fp32 outputs
+ * dominate).  Every call on a GPU shares that GPU's array and the array keeps
+ * the last call's contents (nothing in it has to start at zero): calls that
+ * overlap on one GPU, on any handles or streams, race. */
+int mi_moe_forward_noalloc(mi_moe_handle* h, const void* x, void* y,
+                           const float* topk_w, const int32_t* topk_ids,
+                           int64_t T, int64_t K, int act_dtype, void* stream);
+
 /* Wall time of the last mi_moe_forward on the handle, in ms, measured with
  * HIP events around its launches (synchronizes on the end event).
  * Replaces MoEInfer::get_last_run_time_ms (Int8-gemm/moe_infer.h:23,

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 #include <cstdarg>
 #include <cstdlib>
 #include <cstdio>
@@ -177,21 +178,6 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
   return MI_MOE_OK;
 }
 
-RouteGlobal route_view(mi_moe_handle* h);
-
-void fill_sched(mi_moe_handle* h, SchedArgs& c, const void* x, void* y, const float* tw,
-                const int32_t* ids, int64_t T, int64_t K) {
-  c.x = (const uint16_t*)x;
-  c.y = (uint16_t*)y;
-  c.tw = tw;
-  c.ids = ids;
-  c.T = (int)T; c.K = (int)K; c.E = (int)h->E; c.H = (int)h->H; c.I = (int)h->I;
-  c.n = (int)(T * K);
-  c.route_global = c.n > kRouteLdsMax;
-  c.rg = route_view(h);
-  c.eout = (float*)h->eout.p;
-}
-
 RouteGlobal route_view(mi_moe_handle* h) {
   RouteGlobal rg;
   rg.counts = (int32_t*)h->r_counts.p;
@@ -206,24 +192,134 @@ RouteGlobal route_view(mi_moe_handle* h) {
   return rg;
 }
 
+// Device workspace of one forward call: the handle's grown buffers
+// (mi_moe_forward) or slices of the no-alloc scratch (mi_moe_forward_noalloc).
+struct Work {
+  void* act = nullptr;      // [n, I] act dtype (W4A16) or int8 (Q8_0 / Q4_0)
+  float* act_d = nullptr;   // [n, I/32] intermediate Q8_0 scales
+  float* eout = nullptr;    // [n, H] per-pair outputs (paths with a separate combine)
+  int8_t* xq = nullptr;     // [T, H] Q8_0 activations (int8 grouped GEMMs)
+  float* xd = nullptr;      // [T, H/32]
+  RouteGlobal rg{};
+};
+
+// ---------------------------------------------------------------- no-alloc scratch
+// The workspace of mi_moe_forward_noalloc: one array per GPU, held from the
+// code object's load until the process ends.  Host code never names it
+// directly: its device address comes from hipGetSymbolAddress, once per
+// device at mi_moe_create (with that device current), and is kept in
+// g_scratch_ptr.  Every no-alloc call on a GPU uses the same array.
+constexpr size_t kNoAllocScratchBytes = (size_t)MI_MOE_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+int init_scratch(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return MI_MOE_OK;   // the no-alloc entry point then reports it
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev]) return MI_MOE_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr)
+    return fail(MI_MOE_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+  g_scratch_ptr[dev] = p;
+  return MI_MOE_OK;
+}
+
+void* scratch_of(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return g_scratch_ptr[dev];
+}
+
+// Slices of one call's workspace laid out from base (256-byte aligned);
+// returns the bytes taken.  With base == nullptr it only measures.
+size_t carve_work(unsigned char* base, const mi_moe_handle* h, int64_t T, int64_t n, bool need_eout, Work& w) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> void* {
+    void* p = base ? base + off : nullptr;
+    off += (bytes + 255) & ~(size_t)255;
+    return p;
+  };
+  const int64_t E = h->E, H = h->H, I = h->I;
+  w.rg.counts = (int32_t*)take((size_t)E * 4);
+  w.rg.starts = (int32_t*)take((size_t)(E + 1) * 4);
+  w.rg.active = (int32_t*)take((size_t)E * 4);
+  w.rg.U = (int32_t*)take(4);
+  w.rg.ntiles = (int32_t*)take(4);
+  w.rg.tok = (int32_t*)take((size_t)n * 4);
+  w.rg.scat = (int32_t*)take((size_t)n * 4);
+  w.rg.tiles = (int32_t*)take((size_t)gemm_tiles_max(n, (int)E) * 16);
+  w.rg.chunk = (int32_t*)take((size_t)route_chunks((int)n) * E * 4);
+  w.act = take((size_t)n * I * 2);
+  w.act_d = (float*)take((size_t)n * (I / 32) * 4);
+  w.eout = need_eout ? (float*)take((size_t)n * H * 4) : nullptr;
+  if (h->quant != MI_MOE_W4A16) {
+    w.xq = (int8_t*)take((size_t)T * H);
+    w.xd = (float*)take((size_t)T * (H / 32) * 4);
+  }
+  return off;
+}
+
+// The call's workspace: the handle's buffers (grown on demand; growth
+// synchronizes the stream) or, for the no-alloc entry point, the scratch.
+int get_work(mi_moe_handle* h, int64_t T, int64_t n, bool need_eout, bool noalloc, hipStream_t st, Work& w) {
+  if (!noalloc) {
+    const int rc = ensure_workspace(h, T, n, st);
+    if (rc) return rc;
+    w.act = h->act.p;
+    w.act_d = (float*)h->act_d.p;
+    w.eout = (float*)h->eout.p;
+    w.xq = (int8_t*)h->xq.p;
+    w.xd = (float*)h->xd.p;
+    w.rg = route_view(h);
+    return MI_MOE_OK;
+  }
+  unsigned char* base = (unsigned char*)scratch_of(h->device);
+  if (!base) return fail(MI_MOE_EHIP, "no-alloc scratch unavailable on device %d", h->device);
+  const size_t need = carve_work(nullptr, h, T, n, need_eout, w);
+  if (need > kNoAllocScratchBytes)
+    return fail(MI_MOE_EINVAL, "this call (T=%lld, %lld routed pairs) needs %zu bytes of workspace; "
+                "mi_moe_forward_noalloc holds at most %zu (use mi_moe_forward)", (long long)T, (long long)n,
+                need, kNoAllocScratchBytes);
+  carve_work(base, h, T, n, need_eout, w);
+  return MI_MOE_OK;
+}
+
+void fill_sched(mi_moe_handle* h, SchedArgs& c, const void* x, void* y, const float* tw,
+                const int32_t* ids, int64_t T, int64_t K, const Work& w) {
+  c.x = (const uint16_t*)x;
+  c.y = (uint16_t*)y;
+  c.tw = tw;
+  c.ids = ids;
+  c.T = (int)T; c.K = (int)K; c.E = (int)h->E; c.H = (int)h->H; c.I = (int)h->I;
+  c.n = (int)(T * K);
+  c.route_global = c.n > kRouteLdsMax;
+  c.rg = w.rg;
+  c.eout = w.eout;
+}
+
 int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, const int32_t* ids,
-                  int64_t T, int64_t K, int act, hipStream_t st) {
+                  int64_t T, int64_t K, int act, bool noalloc, hipStream_t st) {
   const int64_t n = T * K;
-  int rc = ensure_workspace(h, T, n, st);
-  if (rc) return rc;
-  W4Args a;
-  std::memset(&a, 0, sizeof(a));
-  fill_sched(h, a.c, x, y, tw, ids, T, K);
-  a.w13 = h->w13.p; a.w13_m = (const unsigned char*)h->w13_s.p;
-  a.w2 = h->w2.p; a.w2_m = (const unsigned char*)h->w2_s.p;
-  a.act = (uint16_t*)h->act.p;
-  a.sdt = h->scale_dtype;
   // decode path: T*K <= 64 pairs, at most kDownMaxK experts per token (a
   // wave each in the down kernel), and both kernels' LDS fits; otherwise the
   // sorted path (mi_moe_create checked that it fits)
-  hipEvent_t mid = h->timing ? h->evmid : nullptr;
   const size_t lmax = device_max_lds();
-  if (n <= 64 && K <= kDownMaxK && w4_decode_fits((int)h->H, (int)h->I, (int)K, lmax)) {
+  const bool decode = n <= 64 && K <= kDownMaxK && w4_decode_fits((int)h->H, (int)h->I, (int)K, lmax);
+  Work w;
+  int rc = get_work(h, T, n, !decode, noalloc, st, w);
+  if (rc) return rc;
+  W4Args a;
+  std::memset(&a, 0, sizeof(a));
+  fill_sched(h, a.c, x, y, tw, ids, T, K, w);
+  a.w13 = h->w13.p; a.w13_m = (const unsigned char*)h->w13_s.p;
+  a.w2 = h->w2.p; a.w2_m = (const unsigned char*)h->w2_s.p;
+  a.act = (uint16_t*)w.act;
+  a.sdt = h->scale_dtype;
+  hipEvent_t mid = h->timing && !noalloc ? h->evmid : nullptr;
+  if (decode) {
     // phase 1 copies the hidden rows of every token when they are few
     const int nw1 = w4_p1_waves(n, (int)h->H);
     a.x_all = (size_t)T * h->H * 2 <= kXAllBytes && w4_p1_lds_bytes((int)h->H, (int)T, 1, nw1) <= lmax;
@@ -259,17 +355,8 @@ int q_alloc_weights(mi_moe_handle* h) {
 }
 
 int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const int32_t* ids,
-              int64_t T, int64_t K, int act, hipStream_t st) {
+              int64_t T, int64_t K, int act, bool noalloc, hipStream_t st) {
   const int64_t n = T * K;
-  int rc = ensure_workspace(h, T, n, st);
-  if (rc) return rc;
-  QArgs a;
-  std::memset(&a, 0, sizeof(a));
-  fill_sched(h, a.c, x, y, tw, ids, T, K);
-  a.w13 = h->w13.p; a.w13_d = (const uint16_t*)h->w13_s.p;
-  a.w2 = h->w2.p; a.w2_d = (const uint16_t*)h->w2_s.p;
-  a.act_q = (int8_t*)h->act.p;
-  a.act_d = (float*)h->act_d.p;
   // decode sizes: the lane-per-row kernels, with the down projection and the
   // combine token-major in one launch (no eout round trip) where it fits;
   // above kQGemmMinPairs routed pairs, or where the lane-per-row LDS does not
@@ -277,14 +364,27 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   // serves every call)
   const size_t lmax = device_max_lds();
   const int iE = (int)h->E, iH = (int)h->H, iI = (int)h->I, in = (int)n, iK = (int)K;
-  bool token_down = n <= kQGemmMinPairs && K <= kDownMaxK && q_lpr_fits(iH, iI, iE, in, iK, true, lmax);
+  const bool token_down = n <= kQGemmMinPairs && K <= kDownMaxK && q_lpr_fits(iH, iI, iE, in, iK, true, lmax);
   const bool lpr_small = n <= kQGemmMinPairs && (token_down || q_lpr_fits(iH, iI, iE, in, iK, false, lmax));
-  if (q_gemm_ok(iH, iI) && !lpr_small) {
+  const bool gemm = q_gemm_ok(iH, iI) && !lpr_small;
+  if (!gemm && !q_lpr_fits(iH, iI, iE, in, iK, token_down, lmax))
+    return fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 call of %lld routed pairs does not fit the device's LDS", (long long)n);
+  Work w;
+  int rc = get_work(h, T, n, gemm || !token_down, noalloc, st, w);
+  if (rc) return rc;
+  QArgs a;
+  std::memset(&a, 0, sizeof(a));
+  fill_sched(h, a.c, x, y, tw, ids, T, K, w);
+  a.w13 = h->w13.p; a.w13_d = (const uint16_t*)h->w13_s.p;
+  a.w2 = h->w2.p; a.w2_d = (const uint16_t*)h->w2_s.p;
+  a.act_q = (int8_t*)w.act;
+  a.act_d = w.act_d;
+  if (gemm) {
     // sorted path: Q8_0 activations once per token, routing with row tiles,
     // the two int8 grouped GEMMs, the combine
-    a.xq = (const int8_t*)h->xq.p;
-    a.xd = (const float*)h->xd.p;
-    HIPCHK(launch_quant_act(x, act, T, h->H, (int8_t*)h->xq.p, (float*)h->xd.p, st));
+    a.xq = w.xq;
+    a.xd = w.xd;
+    HIPCHK(launch_quant_act(x, act, T, h->H, w.xq, w.xd, st));
     HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
     HIPCHK(launch_qint_gemm(a, h->quant, h->scale_dtype, (int)gemm_tiles_max(n, (int)h->E), st));
     HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
@@ -293,10 +393,24 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
   const int64_t umax = n < h->E ? n : h->E;
   const int64_t grid1 = (n <= kQBallotMaxPairs ? n : umax) * (h->I / 32), grid2 = umax * (h->H / 64);
-  if (!q_lpr_fits(iH, iI, iE, in, iK, token_down, lmax))
-    return fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 call of %lld routed pairs does not fit the device's LDS", (long long)n);
   HIPCHK(launch_qint(a, h->quant, act, h->scale_dtype, (int)grid1, (int)grid2, token_down, st));
   if (!token_down) HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
+  return MI_MOE_OK;
+}
+
+// Argument checks shared by mi_moe_forward and mi_moe_forward_noalloc.
+int check_forward_args(mi_moe_handle* h, const void* x, void* y, const float* topk_w, const int32_t* topk_ids,
+                       int64_t T, int64_t K, int act_dtype) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  if (!h->loaded) return fail(MI_MOE_ENOTLOADED, "weights not stored");
+  if (act_dtype != MI_MOE_F16 && act_dtype != MI_MOE_BF16)
+    return fail(MI_MOE_EINVAL, "hidden dtype must be fp16 or bf16");
+  if (T < 0 || K < 1 || K > 64) return fail(MI_MOE_EINVAL, "bad T=%lld / top_k=%lld", (long long)T, (long long)K);
+  if (T == 0) return MI_MOE_OK;
+  if ((int64_t)T * K > (int64_t)1 << 24) return fail(MI_MOE_EINVAL, "T*top_k too large");
+  if (!x || !y || !topk_w || !topk_ids) return fail(MI_MOE_EINVAL, "null data pointer");
+  if (!aligned16(x) || !aligned16(y)) return fail(MI_MOE_EINVAL, "hidden/out must be 16-byte aligned");
   return MI_MOE_OK;
 }
 
@@ -367,6 +481,12 @@ MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe
       hipEventCreate(&h->evmid) != hipSuccess) {
     delete h;
     return fail(MI_MOE_EHIP, "HIP device query / event creation failed");
+  }
+  // the no-alloc entry point's scratch address on this device (once per device)
+  if (init_scratch(h->device) != MI_MOE_OK) {
+    const std::string msg = g_err;
+    mi_moe_destroy(h);
+    return fail(MI_MOE_EHIP, "%s", msg.c_str());
   }
   *out = h;
   return MI_MOE_OK;
@@ -553,27 +673,29 @@ MI_API int mi_moe_block_dots_mfma(mi_moe_handle* h, int64_t expert, int proj, co
 MI_API int mi_moe_forward(mi_moe_handle* h, const void* x, void* y, const float* topk_w,
                           const int32_t* topk_ids, int64_t T, int64_t K, int act_dtype,
                           void* stream) {
-  int rc = check_handle(h);
-  if (rc) return rc;
-  if (!h->loaded) return fail(MI_MOE_ENOTLOADED, "weights not stored");
-  if (act_dtype != MI_MOE_F16 && act_dtype != MI_MOE_BF16)
-    return fail(MI_MOE_EINVAL, "hidden dtype must be fp16 or bf16");
-  if (T < 0 || K < 1 || K > 64) return fail(MI_MOE_EINVAL, "bad T=%lld / top_k=%lld", (long long)T, (long long)K);
-  if (T == 0) return MI_MOE_OK;
-  if ((int64_t)T * K > (int64_t)1 << 24) return fail(MI_MOE_EINVAL, "T*top_k too large");
-  if (!x || !y || !topk_w || !topk_ids) return fail(MI_MOE_EINVAL, "null data pointer");
-  if (!aligned16(x) || !aligned16(y)) return fail(MI_MOE_EINVAL, "hidden/out must be 16-byte aligned");
+  int rc = check_forward_args(h, x, y, topk_w, topk_ids, T, K, act_dtype);
+  if (rc || T == 0) return rc;
   hipStream_t st = (hipStream_t)stream;
   if (h->timing) HIPCHK(hipEventRecord(h->ev0, st));
   h->mid_recorded = false;
-  if (h->quant == MI_MOE_W4A16) rc = forward_w4a16(h, x, y, topk_w, topk_ids, T, K, act_dtype, st);
-  else rc = forward_q(h, x, y, topk_w, topk_ids, T, K, act_dtype, st);
+  if (h->quant == MI_MOE_W4A16) rc = forward_w4a16(h, x, y, topk_w, topk_ids, T, K, act_dtype, false, st);
+  else rc = forward_q(h, x, y, topk_w, topk_ids, T, K, act_dtype, false, st);
   if (rc) return rc;
   if (h->timing) {
     HIPCHK(hipEventRecord(h->ev1, st));
     h->timed_once = true;
   }
   return MI_MOE_OK;
+}
+
+MI_API int mi_moe_forward_noalloc(mi_moe_handle* h, const void* x, void* y, const float* topk_w,
+                                  const int32_t* topk_ids, int64_t T, int64_t K, int act_dtype,
+                                  void* stream) {
+  int rc = check_forward_args(h, x, y, topk_w, topk_ids, T, K, act_dtype);
+  if (rc || T == 0) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (h->quant == MI_MOE_W4A16) return forward_w4a16(h, x, y, topk_w, topk_ids, T, K, act_dtype, true, st);
+  return forward_q(h, x, y, topk_w, topk_ids, T, K, act_dtype, true, st);
 }
 
 MI_API int mi_moe_topk_softmax(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t K,

@@ -34,7 +34,7 @@ _capi = None
 C_SYMBOLS = (
     "mi_moe_last_error", "mi_moe_version", "mi_moe_create", "mi_moe_destroy",
     "mi_moe_get_info", "mi_moe_store_quantized", "mi_moe_quantize_and_store_expert",
-    "mi_moe_store_awq", "mi_moe_forward", "mi_moe_get_last_run_time_ms",
+    "mi_moe_store_awq", "mi_moe_forward", "mi_moe_forward_noalloc", "mi_moe_get_last_run_time_ms",
     "mi_moe_set_timing", "mi_moe_quantize_act_q8_0", "mi_moe_route", "mi_moe_block_dots",
     "mi_moe_block_dots_mfma",
     "mi_moe_get_last_phase_times_ms", "mi_moe_topk_softmax", "mi_moe_forward_logits",
@@ -83,6 +83,7 @@ def capi():
     L.mi_moe_quantize_and_store_expert.argtypes = [P, I64, I, P, I, I, P]
     L.mi_moe_store_awq.argtypes = [P, P, P, P, P, P, P, I64, I, I, P]
     L.mi_moe_forward.argtypes = [P, P, P, P, P, I64, I64, I, P]
+    L.mi_moe_forward_noalloc.argtypes = [P, P, P, P, P, I64, I64, I, P]
     L.mi_moe_get_last_run_time_ms.restype = ctypes.c_double
     L.mi_moe_get_last_run_time_ms.argtypes = [P]
     L.mi_moe_set_timing.argtypes = [P, I]
