@@ -220,6 +220,66 @@ int mi_moe_forward_logits(mi_moe_handle* h, const void* x, void* y,
                           float* topk_w_out, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Host (CPU) engine of the Q8_0 / Q4_0 layer: the reference's CPU algorithm
+ * (moe_forward_ptr_impl, Int8-gemm/q8_gemm.cpp:276-646) on x86 cores.  It is
+ * the CPU dispatch key of nanovllm::moe_forward (the reference's only key,
+ * Int8-gemm/nanovllm_ops.cpp:410-412) and the CPU baseline of the benchmark.
+ * Stage A Q8_0 activations, tasks of 32 routed rows of one expert (2 threads
+ * per task -- gate / up rows, then halves of the down rows -- when there are
+ * at most half as many tasks as threads), exact int32 block dots, the
+ * reference's per-block scaling order, Q8_0 intermediate, combine in k order,
+ * tp shards of I over the NUMA nodes of the threads (partials summed in shard
+ * order).  All pointers are host memory; calls are synchronous.  The
+ * MoEInfer counterpart for this path is Int8-gemm/moe_infer.cpp:18-84. */
+typedef struct mi_moe_cpu mi_moe_cpu;
+
+/* Instruction sets of the int8 dot products (mi_moe_cpu_get_info's isa). */
+#define MI_MOE_ISA_SCALAR 0
+#define MI_MOE_ISA_AVX2 1
+#define MI_MOE_ISA_AVX_VNNI 2
+#define MI_MOE_ISA_AVX512_VNNI 3
+
+/* num_threads 0: every CPU of the process affinity mask, else at most that
+ * many (whole NUMA nodes first); tp 0: one shard per NUMA node holding
+ * threads, else exactly tp shards (I/tp a multiple of 32).  quant_type 0 / 1. */
+int mi_moe_cpu_create(int64_t num_experts, int64_t hidden, int64_t intermediate,
+                      int quant_type, int num_threads, int tp, mi_moe_cpu** out);
+int mi_moe_cpu_destroy(mi_moe_cpu* c);
+
+/* Wire layout as mi_moe_store_quantized (store_quantized_weights_repack,
+ * Int8-gemm/moe_infer.cpp:96-282), host memory; each shard's threads repack
+ * their shard (first touch places it on their node). */
+int mi_moe_cpu_store_quantized(mi_moe_cpu* c, const void* gate_up_qs,
+                               const void* gate_up_d, const void* down_qs,
+                               const void* down_d, int scale_dtype);
+
+/* Online Q8_0 of one projection (as mi_moe_quantize_and_store_expert;
+ * Int8-gemm/moe_infer.cpp:284-360), host memory; Q8_0 only. */
+int mi_moe_cpu_quantize_and_store_expert(mi_moe_cpu* c, int64_t expert, int proj,
+                                         const void* w, int w_dtype);
+
+/* The fused layer on host memory: arguments as mi_moe_forward (ids outside
+ * [0,E) dropped; a token with no valid id gets zeros).  Replaces
+ * MoEInfer::execute_on_cpu_routed_from_pointers (Int8-gemm/moe_infer.cpp:
+ * 430-456); wall time of the call in mi_moe_cpu_get_info's last_ms. */
+int mi_moe_cpu_forward(mi_moe_cpu* c, const void* x, void* y, const float* topk_w,
+                       const int32_t* topk_ids, int64_t T, int64_t K, int act_dtype);
+
+/* Threads, shards, instruction set (MI_MOE_ISA_*), CPUs and NUMA nodes of the
+ * affinity mask, and the last forward's wall time in ms.  Any output may be
+ * NULL. */
+int mi_moe_cpu_get_info(mi_moe_cpu* c, int* threads, int* tp, int* isa,
+                        int* affinity_cpus, int* affinity_nodes, double* last_ms);
+
+/* Run the dots with another instruction set the host supports (results are
+ * the same bit for bit; for testing each form).  MI_MOE_EUNSUPPORTED if the
+ * host lacks it. */
+int mi_moe_cpu_set_isa(mi_moe_cpu* c, int isa);
+
+/* Name of an MI_MOE_ISA_* value. */
+const char* mi_moe_cpu_isa_name(int isa);
+
+/* ------------------------------------------------------------------------
  * Hybrid CPU-offload executor.  The reference's NPU op runs the whole layer
  * in a host callback between device->host and host->device copies
  * (moe_forward_npu_stream, Int8-gemm/nanovllm_ops.cpp:244-305); its roadmap

@@ -1,0 +1,117 @@
+// cpu_moe.hpp -- host (CPU) engine of the Q8_0 / Q4_0 fused MoE layer: the
+// reference CPU algorithm (moe_forward_ptr_impl, Int8-gemm/q8_gemm.cpp:276-646)
+// on x86 cores with VNNI / AVX2 int8 dot products, tp shards over NUMA nodes.
+// Plain C++ (no HIP); bound by the mi_moe_cpu_* entry points of the C ABI.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#include <atomic>
+#include <condition_variable>
+#include <functional>
+#include <memory>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+namespace mimoe_cpu {
+
+// fp16 (dt 0) / bf16 (dt 1) bits -> fp32, exact
+float half_to_f32(uint16_t v, int dt);
+
+enum class Isa : int { kScalar = 0, kAvx2 = 1, kAvxVnni = 2, kAvx512Vnni = 3 };
+Isa detect_isa();               // the widest form the host runs
+bool isa_supported(Isa i);
+const char* isa_name(Isa i);
+
+constexpr int kNR = 16;       // weight rows per panel
+constexpr int kMBlock = 32;   // routed rows per task (M_BLOCK, Int8-gemm/q8_gemm.cpp:335)
+
+// One weight matrix (N rows x K, N % 16 == 0, K % 32 == 0) in 16-row panels.
+struct PackedMat {
+  int qt = 0;
+  int64_t N = 0, K = 0, blk = 0;
+  std::vector<uint8_t> qs;   // [N/16][K/32][blk]
+  std::vector<float> d;      // [N/16][K/32][16]
+  std::vector<int32_t> ws;   // Q8_0: [N/16][K/32][16] = 128 * sum of the block's weights
+  void init(int qt, int64_t N, int64_t K);
+  void set_row(int64_t n, const int8_t* w, const float* dw);   // values (Q4_0: n - 8) and block scales
+};
+
+// The host's CPUs as used: affinity size, NUMA nodes among them, and the
+// CPUs chosen (at most max_threads, whole nodes first) grouped by node.
+struct Topology {
+  int affinity_cpus = 0, affinity_nodes = 0;
+  std::vector<int> node_ids;
+  std::vector<std::vector<int>> node_cpus;
+};
+Topology host_topology(int max_threads);
+
+// A pool of threads pinned to the given CPUs; run(n, f) calls f(i) for
+// i < n on the workers and the caller, dynamically.  One run at a time.
+class NodePool {
+ public:
+  explicit NodePool(const std::vector<int>& cpus);
+  ~NodePool();
+  NodePool(const NodePool&) = delete;
+  NodePool& operator=(const NodePool&) = delete;
+  int size() const { return (int)th_.size() + 1; }
+  void run(int64_t n, const std::function<void(int64_t)>& f);
+  void pin(int i);   // pin the calling thread to CPU i of the pool
+
+ private:
+  void work();
+  std::vector<int> cpus_;
+  std::vector<std::thread> th_;
+  std::mutex m_;
+  std::condition_variable cv_, done_;
+  const std::function<void(int64_t)>* fn_ = nullptr;
+  int64_t n_ = 0;
+  std::atomic<int64_t> next_{0};
+  int busy_ = 0;
+  uint64_t gen_ = 0;
+  bool stop_ = false;
+};
+
+class Engine {
+ public:
+  // max_threads 0: every CPU of the affinity mask; tp 0: one shard per NUMA
+  // node holding chosen CPUs.
+  Engine(int64_t E, int64_t H, int64_t I, int quant, int max_threads, int tp);
+  ~Engine();
+  bool shape_ok() const;
+  // wire layout of store_quantized_weights_repack (Int8-gemm/moe_infer.cpp:96-282)
+  void store(const void* gate_up_qs, const uint16_t* gate_up_d, const void* down_qs, const uint16_t* down_d,
+             int scale_dtype);
+  // one projection (0 gate [I,H], 1 up [I,H], 2 down [H,I]) of expert e, fp32 values
+  void quantize_and_store(int64_t e, int proj, const float* w);
+  int forward(const uint16_t* x, uint16_t* y, const float* topk_w, const int32_t* topk_ids, int64_t T, int64_t K,
+              int act_dtype);
+  bool loaded() const { return loaded_; }
+  int threads() const { return threads_; }
+  int tp() const { return tp_; }
+  Isa isa() const { return isa_; }
+  void set_isa(Isa i) { isa_ = i; }
+  double last_ms() const { return last_ms_; }
+  const Topology& topology() const { return topo_; }
+  int64_t E() const { return E_; }
+  int64_t H() const { return H_; }
+  int64_t I() const { return I_; }
+  int quant() const { return qt_; }
+
+ private:
+  struct Shard {
+    std::vector<PackedMat> w13, w2;   // per expert: [gate shard | up shard] rows x H; H rows x shard
+  };
+  int64_t E_, H_, I_;
+  int qt_;
+  Isa isa_;
+  Topology topo_;
+  int tp_ = 1, threads_ = 1;
+  std::vector<std::unique_ptr<NodePool>> pools_;
+  std::vector<Shard> shards_;
+  bool loaded_ = false;
+  double last_ms_ = -1.0;
+};
+
+}  // namespace mimoe_cpu

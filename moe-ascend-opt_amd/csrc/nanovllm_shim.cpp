@@ -6,7 +6,10 @@
 // moe_forward_out, and the router step the reference runs in its Python
 // harness (make_topk_from_logits_cpu, Int8-gemm/test/fused_moe_cpu.py:20-37)
 // as moe_topk_softmax / moe_forward_logits.  Only this file sees torch types; it calls the C ABI of
-// include/mi_moe.h on the current HIP stream.
+// include/mi_moe.h: HIP tensors run the device kernels on the current HIP stream; CPU tensors run the
+// host engine (the reference's CPU algorithm for Q8_0 / Q4_0; every expert on the host executor for
+// W4A16), which needs weights stored from host tensors (kept by default when no HIP device is present,
+// or with MIMOE_HOST_WEIGHTS=1; never with MIMOE_HOST_WEIGHTS=0).
 #include <c10/hip/HIPStream.h>
 #include <torch/custom_class.h>
 #include <tuple>
@@ -14,7 +17,11 @@
 #include <torch/library.h>
 #include <ATen/ATen.h>
 
+#include <cstdlib>
 #include <string>
+#include <chrono>
+#include <algorithm>
+#include <cmath>
 
 #include "mi_moe.h"
 
@@ -35,33 +42,70 @@ void* stream_of(const at::Tensor& ref) {
   return (void*)c10::hip::getCurrentHIPStream().stream();
 }
 
+// Host threads of the CPU path: MIMOE_CPU_THREADS, else OMP_NUM_THREADS, else
+// every CPU of the affinity mask (0).
+int host_threads() {
+  for (const char* v : {"MIMOE_CPU_THREADS", "OMP_NUM_THREADS"}) {
+    const char* s = getenv(v);
+    if (s && atoi(s) > 0) return atoi(s);
+  }
+  return 0;
+}
+
+bool hip_device_present() {
+  int n = 0;
+  return hipGetDeviceCount(&n) == hipSuccess && n > 0;
+}
+
 struct MoEInferHandle : torch::CustomClassHolder {
-  int64_t quant_type;
-  mi_moe_handle* h = nullptr;
+  int64_t E, H, I, quant_type;
+  mi_moe_handle* h = nullptr;      // device weights (when a HIP device is present)
+  mi_moe_cpu* cpu = nullptr;       // host engine, Q8_0 / Q4_0
+  mi_moe_hybrid* hcpu = nullptr;   // W4A16 with every expert on the host executor
+  bool keep_host = false;          // weights stored from host tensors also fill the host path
+  bool last_cpu = false;           // the last forward ran on the host
+  double last_cpu_ms = -1.0;
 
   // Int8-gemm/nanovllm_ops.cpp:28-30 (quant_type: 0 Q8_0, 1 Q4_0; 2 W4A16)
-  MoEInferHandle(int64_t E, int64_t H, int64_t I, int64_t qt) : quant_type(qt) {
-    check_status(mi_moe_create(E, H, I, (int)qt, &h), "MoEInfer");
+  MoEInferHandle(int64_t E_, int64_t H_, int64_t I_, int64_t qt) : E(E_), H(H_), I(I_), quant_type(qt) {
+    TORCH_CHECK(qt >= 0 && qt <= 2, "quant_type must be 0 (Q8_0), 1 (Q4_0) or 2 (W4A16)");
+    const bool dev = hip_device_present();
+    if (dev) check_status(mi_moe_create(E, H, I, (int)qt, &h), "MoEInfer");
+    const char* kh = getenv("MIMOE_HOST_WEIGHTS");
+    keep_host = kh ? atoi(kh) != 0 : !dev;
+    if (!dev) TORCH_CHECK(keep_host, "MoEInfer: no HIP device and MIMOE_HOST_WEIGHTS=0: nowhere to keep the weights");
   }
   ~MoEInferHandle() override {
     if (h) mi_moe_destroy(h);
+    if (cpu) mi_moe_cpu_destroy(cpu);
+    if (hcpu) mi_moe_hybrid_destroy(hcpu);
   }
   std::string get_quant_type() const {
     return quant_type == 1 ? "Q4_0" : (quant_type == 2 ? "W4A16" : "Q8_0");
   }
-  int64_t info(int which) const {
-    int64_t E = 0, H = 0, I = 0;
-    check_status(mi_moe_get_info(h, &E, &H, &I, nullptr, nullptr), "get_info");
-    return which == 0 ? E : (which == 1 ? H : I);
+  int64_t info(int which) const { return which == 0 ? E : (which == 1 ? H : I); }
+  mi_moe_handle* dev() const {
+    TORCH_CHECK(h != nullptr, "MoEInfer: no HIP device for this call");
+    return h;
+  }
+  mi_moe_cpu* host_engine() {
+    if (!cpu) check_status(mi_moe_cpu_create(E, H, I, (int)quant_type, host_threads(), 0, &cpu), "MoEInfer (host)");
+    return cpu;
+  }
+  mi_moe_hybrid* host_w4() {
+    if (!hcpu) {
+      std::vector<uint8_t> all((size_t)E, 1);
+      check_status(mi_moe_hybrid_create(E, H, I, MI_MOE_W4A16, all.data(), std::min(host_threads(), 16), &hcpu),
+                   "MoEInfer (host)");
+    }
+    return hcpu;
   }
 };
 
 at::Tensor contig(const at::Tensor& t) { return t.is_contiguous() ? t : t.contiguous(); }
 
-void forward_into(const at::Tensor& hidden, const at::Tensor& topk_ids, const at::Tensor& topk_w,
-                  const c10::intrusive_ptr<MoEInferHandle>& moe, at::Tensor& out) {
-  TORCH_CHECK(hidden.is_cuda(), "moe_forward: hidden must be a HIP (cuda) tensor on MI355X; "
-              "this build has no CPU path");
+void check_forward_tensors(const at::Tensor& hidden, const at::Tensor& topk_ids, const at::Tensor& topk_w,
+                           const c10::intrusive_ptr<MoEInferHandle>& moe, const at::Tensor& out) {
   TORCH_CHECK(hidden.dim() == 2 && topk_ids.dim() == 2 && topk_w.dim() == 2,
               "moe_forward: expected hidden [T,H], topk_ids [T,K], topk_w [T,K]");
   TORCH_CHECK(topk_ids.scalar_type() == at::kInt, "topk_ids must be int32");
@@ -77,11 +121,49 @@ void forward_into(const at::Tensor& hidden, const at::Tensor& topk_ids, const at
   TORCH_CHECK(out.sizes() == hidden.sizes() && out.scalar_type() == hidden.scalar_type() &&
                   out.is_contiguous(),
               "out must be a contiguous tensor like hidden");
+}
+
+void forward_into(const at::Tensor& hidden, const at::Tensor& topk_ids, const at::Tensor& topk_w,
+                  const c10::intrusive_ptr<MoEInferHandle>& moe, at::Tensor& out) {
+  TORCH_CHECK(hidden.is_cuda(), "moe_forward: expected HIP tensors here");
+  check_forward_tensors(hidden, topk_ids, topk_w, moe, out);
   at::Tensor x = contig(hidden), ids = contig(topk_ids), w = contig(topk_w);
-  check_status(mi_moe_forward(moe->h, x.data_ptr(), out.data_ptr(), w.data_ptr<float>(),
+  check_status(mi_moe_forward(moe->dev(), x.data_ptr(), out.data_ptr(), w.data_ptr<float>(),
                               ids.data_ptr<int32_t>(), x.size(0), ids.size(1), act_code(x),
                               stream_of(x)),
                "moe_forward");
+  moe->last_cpu = false;
+}
+
+// The CPU key: the host engine (Q8_0 / Q4_0: the reference algorithm,
+// Int8-gemm/nanovllm_ops.cpp:219-236 -> moe_infer.cpp:430-456) or, for W4A16,
+// every expert on the host executor.
+void forward_into_cpu(const at::Tensor& hidden, const at::Tensor& topk_ids, const at::Tensor& topk_w,
+                      const c10::intrusive_ptr<MoEInferHandle>& moe, at::Tensor& out) {
+  check_forward_tensors(hidden, topk_ids, topk_w, moe, out);
+  at::Tensor x = contig(hidden), ids = contig(topk_ids), w = contig(topk_w);
+  const int64_t T = x.size(0), K = ids.size(1);
+  if (moe->quant_type == 2) {
+    TORCH_CHECK(moe->hcpu != nullptr, "moe_forward (CPU): no host weights; store the weights from host tensors "
+                "(with MIMOE_HOST_WEIGHTS=1 where a HIP device is present)");
+    at::Tensor part = at::empty({T, moe->H}, x.options().dtype(at::kFloat));
+    const auto t0 = std::chrono::steady_clock::now();
+    check_status(mi_moe_hybrid_host_forward(moe->hcpu, x.data_ptr(), w.data_ptr<float>(), ids.data_ptr<int32_t>(),
+                                            T, K, act_code(x), part.data_ptr<float>()),
+                 "moe_forward (CPU)");
+    out.copy_(part);   // fp32 -> the hidden dtype, round to nearest even
+    moe->last_cpu_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  } else {
+    TORCH_CHECK(moe->cpu != nullptr, "moe_forward (CPU): no host weights; store the weights from host tensors "
+                "(with MIMOE_HOST_WEIGHTS=1 where a HIP device is present)");
+    check_status(mi_moe_cpu_forward(moe->cpu, x.data_ptr(), out.data_ptr(), w.data_ptr<float>(),
+                                    ids.data_ptr<int32_t>(), T, K, act_code(x)),
+                 "moe_forward (CPU)");
+    double ms = -1.0;
+    check_status(mi_moe_cpu_get_info(moe->cpu, nullptr, nullptr, nullptr, nullptr, nullptr, &ms), "get_info");
+    moe->last_cpu_ms = ms;
+  }
+  moe->last_cpu = true;
 }
 
 // Int8-gemm/nanovllm_ops.cpp:219-236
@@ -93,10 +175,17 @@ at::Tensor moe_forward_hip(const at::Tensor& hidden, const at::Tensor& topk_ids,
   return out;
 }
 
-at::Tensor moe_forward_cpu_reject(const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                                  const c10::intrusive_ptr<MoEInferHandle>&) {
-  TORCH_CHECK(false, "nanovllm::moe_forward: this MI355X build runs on HIP tensors only "
-              "(move hidden/topk_ids/topk_w to cuda)");
+// Int8-gemm/nanovllm_ops.cpp:219-236 (CPU key, :410-412)
+at::Tensor moe_forward_cpu(const at::Tensor& hidden, const at::Tensor& topk_ids, const at::Tensor& topk_w,
+                           const c10::intrusive_ptr<MoEInferHandle>& moe) {
+  at::Tensor out = at::empty_like(hidden, hidden.options().memory_format(at::MemoryFormat::Contiguous));
+  forward_into_cpu(hidden, topk_ids, topk_w, moe, out);
+  return out;
+}
+
+void moe_forward_out_cpu(const at::Tensor& hidden, const at::Tensor& topk_ids, const at::Tensor& topk_w,
+                         const c10::intrusive_ptr<MoEInferHandle>& moe, at::Tensor out) {
+  forward_into_cpu(hidden, topk_ids, topk_w, moe, out);
 }
 
 void moe_forward_out_hip(const at::Tensor& hidden, const at::Tensor& topk_ids,
@@ -125,8 +214,40 @@ std::tuple<at::Tensor, at::Tensor> moe_topk_softmax_hip(const at::Tensor& logits
   return {ids, w};
 }
 
-std::tuple<at::Tensor, at::Tensor> moe_topk_softmax_cpu_reject(const at::Tensor&, int64_t, bool) {
-  TORCH_CHECK(false, "nanovllm::moe_topk_softmax: this MI355X build runs on HIP tensors only");
+// Router top-k + softmax on host tensors, the semantics of the device kernel
+// (make_topk_from_logits_cpu, Int8-gemm/test/fused_moe_cpu.py:20-37): the K
+// largest logits in descending order, equal logits lower expert id first,
+// softmax over the K values (renormalize) or the full softmax gathered.
+std::tuple<at::Tensor, at::Tensor> moe_topk_softmax_cpu(const at::Tensor& logits, int64_t top_k, bool renormalize) {
+  TORCH_CHECK(logits.dim() == 2, "moe_topk_softmax: logits must be [T,E]");
+  at::Tensor x = contig(logits).to(at::kFloat);
+  const int64_t T = x.size(0), E = x.size(1);
+  TORCH_CHECK(top_k >= 1 && top_k <= E && top_k <= 64, "top_k=", top_k, " must be in [1, min(E, 64)]");
+  at::Tensor ids = at::empty({T, top_k}, x.options().dtype(at::kInt));
+  at::Tensor w = at::empty({T, top_k}, x.options().dtype(at::kFloat));
+  const float* g = x.data_ptr<float>();
+  int32_t* oi = ids.data_ptr<int32_t>();
+  float* ow = w.data_ptr<float>();
+  std::vector<int32_t> ord((size_t)E);
+  for (int64_t t = 0; t < T; ++t) {
+    const float* row = g + t * E;
+    for (int64_t e = 0; e < E; ++e) ord[(size_t)e] = (int32_t)e;
+    std::partial_sort(ord.begin(), ord.begin() + top_k, ord.end(), [&](int32_t a, int32_t b) {
+      return row[a] > row[b] || (row[a] == row[b] && a < b);
+    });
+    const float mx = row[ord[0]];
+    double den = 0.0;
+    if (renormalize) {
+      for (int64_t k = 0; k < top_k; ++k) den += std::exp((double)row[ord[(size_t)k]] - mx);
+    } else {
+      for (int64_t e = 0; e < E; ++e) den += std::exp((double)row[e] - mx);
+    }
+    for (int64_t k = 0; k < top_k; ++k) {
+      oi[t * top_k + k] = ord[(size_t)k];
+      ow[t * top_k + k] = (float)(std::exp((double)row[ord[(size_t)k]] - mx) / den);
+    }
+  }
+  return {ids, w};
 }
 
 at::Tensor moe_forward_logits_hip(const at::Tensor& hidden, const at::Tensor& router_logits, int64_t top_k,
@@ -140,16 +261,22 @@ at::Tensor moe_forward_logits_hip(const at::Tensor& hidden, const at::Tensor& ro
   TORCH_CHECK(hidden.size(1) == moe->info(1), "hidden size ", hidden.size(1), " != handle H ", moe->info(1));
   at::Tensor x = contig(hidden), g = contig(router_logits);
   at::Tensor out = at::empty_like(x);
-  check_status(mi_moe_forward_logits(moe->h, x.data_ptr(), out.data_ptr(), g.data_ptr(), logits_code(g),
+  check_status(mi_moe_forward_logits(moe->dev(), x.data_ptr(), out.data_ptr(), g.data_ptr(), logits_code(g),
                                      x.size(0), top_k, renormalize ? 1 : 0, act_code(x), nullptr, nullptr,
                                      stream_of(x)),
                "moe_forward_logits");
+  moe->last_cpu = false;
   return out;
 }
 
-at::Tensor moe_forward_logits_cpu_reject(const at::Tensor&, const at::Tensor&, int64_t, bool,
-                                         const c10::intrusive_ptr<MoEInferHandle>&) {
-  TORCH_CHECK(false, "nanovllm::moe_forward_logits: this MI355X build runs on HIP tensors only");
+at::Tensor moe_forward_logits_cpu(const at::Tensor& hidden, const at::Tensor& router_logits, int64_t top_k,
+                                  bool renormalize, const c10::intrusive_ptr<MoEInferHandle>& moe) {
+  TORCH_CHECK(hidden.dim() == 2 && router_logits.dim() == 2 && router_logits.size(0) == hidden.size(0),
+              "moe_forward_logits: expected hidden [T,H], router_logits [T,E]");
+  TORCH_CHECK(router_logits.size(1) == moe->info(0), "router_logits has ", router_logits.size(1),
+              " experts, handle has ", moe->info(0));
+  auto picks = moe_topk_softmax_cpu(router_logits, top_k, renormalize);
+  return moe_forward_cpu(hidden, std::get<0>(picks), std::get<1>(picks), moe);
 }
 
 int scale_code(const at::Tensor& d) {
@@ -184,9 +311,14 @@ TORCH_LIBRARY_FRAGMENT(nanovllm, m) {
              } else {
                TORCH_CHECK(wc.size(0) == H && wc.size(1) == I, "down weight must be [H,I]");
              }
-             check_status(mi_moe_quantize_and_store_expert(self->h, expert_idx, proj, wc.data_ptr(),
-                                                           wd, wc.is_cuda() ? 1 : 0, stream_of(wc)),
-                          "quantize_and_store_expert");
+             if (self->h)
+               check_status(mi_moe_quantize_and_store_expert(self->h, expert_idx, proj, wc.data_ptr(),
+                                                             wd, wc.is_cuda() ? 1 : 0, stream_of(wc)),
+                            "quantize_and_store_expert");
+             if (!wc.is_cuda() && self->keep_host)
+               check_status(mi_moe_cpu_quantize_and_store_expert(self->host_engine(), expert_idx, proj,
+                                                                 wc.data_ptr(), wd),
+                            "quantize_and_store_expert (host)");
            })
       // Int8-gemm/nanovllm_ops.cpp:366-371
       .def("store_quantized_repack",
@@ -219,9 +351,14 @@ TORCH_LIBRARY_FRAGMENT(nanovllm, m) {
              const bool dev = a.is_cuda();
              TORCH_CHECK(b.is_cuda() == dev && c.is_cuda() == dev && d.is_cuda() == dev,
                          "all weight tensors must be on one device");
-             check_status(mi_moe_store_quantized(self->h, a.data_ptr(), b.data_ptr(), c.data_ptr(),
-                                                 d.data_ptr(), scale_code(b), dev ? 1 : 0, stream_of(a)),
-                          "store_quantized_repack");
+             if (self->h)
+               check_status(mi_moe_store_quantized(self->h, a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                                                   d.data_ptr(), scale_code(b), dev ? 1 : 0, stream_of(a)),
+                            "store_quantized_repack");
+             if (!dev && self->keep_host)
+               check_status(mi_moe_cpu_store_quantized(self->host_engine(), a.data_ptr(), b.data_ptr(),
+                                                       c.data_ptr(), d.data_ptr(), scale_code(b)),
+                            "store_quantized_repack (host)");
            })
       // build-defined W4A16 (AWQ layout) loader; see include/mi_moe.h
       .def("store_awq_repack",
@@ -251,25 +388,32 @@ TORCH_LIBRARY_FRAGMENT(nanovllm, m) {
              TORCH_CHECK(b.is_cuda() == dev && c.is_cuda() == dev && d.is_cuda() == dev &&
                              e.is_cuda() == dev && f.is_cuda() == dev,
                          "all weight tensors must be on one device");
-             check_status(mi_moe_store_awq(self->h, a.data_ptr<int32_t>(), b.data_ptr<int32_t>(),
-                                           c.data_ptr(), d.data_ptr<int32_t>(), e.data_ptr<int32_t>(),
-                                           f.data_ptr(), g, scale_code(c), dev ? 1 : 0, stream_of(a)),
-                          "store_awq_repack");
+             if (self->h)
+               check_status(mi_moe_store_awq(self->h, a.data_ptr<int32_t>(), b.data_ptr<int32_t>(),
+                                             c.data_ptr(), d.data_ptr<int32_t>(), e.data_ptr<int32_t>(),
+                                             f.data_ptr(), g, scale_code(c), dev ? 1 : 0, stream_of(a)),
+                            "store_awq_repack");
+             if (!dev && self->keep_host)
+               check_status(mi_moe_hybrid_store_awq(self->host_w4(), a.data_ptr<int32_t>(), b.data_ptr<int32_t>(),
+                                                    c.data_ptr(), d.data_ptr<int32_t>(), e.data_ptr<int32_t>(),
+                                                    f.data_ptr(), g, scale_code(c), 0, nullptr),
+                            "store_awq_repack (host)");
            })
       .def("get_last_run_time_ms",
            [](const c10::intrusive_ptr<MoEInferHandle>& self) {
+             if (self->last_cpu || !self->h) return self->last_cpu_ms;
              return mi_moe_get_last_run_time_ms(self->h);
            })
       .def("get_last_phase_times_ms",
            [](const c10::intrusive_ptr<MoEInferHandle>& self) {
              double ms[2] = {0.0, 0.0};
-             const int n = mi_moe_get_last_phase_times_ms(self->h, ms, 2);
+             const int n = mi_moe_get_last_phase_times_ms(self->dev(), ms, 2);
              TORCH_CHECK(n > 0, "get_last_phase_times_ms: ", mi_moe_last_error());
              return std::vector<double>(ms, ms + n);
            })
       .def("set_timing",
            [](const c10::intrusive_ptr<MoEInferHandle>& self, bool enable) {
-             check_status(mi_moe_set_timing(self->h, enable ? 1 : 0), "set_timing");
+             if (self->h) check_status(mi_moe_set_timing(self->h, enable ? 1 : 0), "set_timing");
            })
       .def("get_quant_type",
            [](const c10::intrusive_ptr<MoEInferHandle>& self) { return self->get_quant_type(); })
@@ -297,7 +441,8 @@ TORCH_LIBRARY_IMPL(nanovllm, CUDA, m) {
 }
 
 TORCH_LIBRARY_IMPL(nanovllm, CPU, m) {
-  m.impl("moe_forward", &moe_forward_cpu_reject);
-  m.impl("moe_topk_softmax", &moe_topk_softmax_cpu_reject);
-  m.impl("moe_forward_logits", &moe_forward_logits_cpu_reject);
+  m.impl("moe_forward", &moe_forward_cpu);
+  m.impl("moe_forward_out", &moe_forward_out_cpu);
+  m.impl("moe_topk_softmax", &moe_topk_softmax_cpu);
+  m.impl("moe_forward_logits", &moe_forward_logits_cpu);
 }

@@ -40,7 +40,9 @@ C_SYMBOLS = (
     "mi_moe_get_last_phase_times_ms", "mi_moe_topk_softmax", "mi_moe_forward_logits",
     "mi_moe_hybrid_create", "mi_moe_hybrid_destroy", "mi_moe_hybrid_store_quantized",
     "mi_moe_hybrid_store_awq", "mi_moe_hybrid_forward", "mi_moe_hybrid_host_forward",
-    "mi_moe_hybrid_get_stats",
+    "mi_moe_hybrid_get_stats", "mi_moe_cpu_create", "mi_moe_cpu_destroy", "mi_moe_cpu_store_quantized",
+    "mi_moe_cpu_quantize_and_store_expert", "mi_moe_cpu_forward", "mi_moe_cpu_get_info", "mi_moe_cpu_set_isa",
+    "mi_moe_cpu_isa_name",
 )
 
 
@@ -101,10 +103,19 @@ def capi():
     L.mi_moe_hybrid_forward.argtypes = [P, P, P, P, P, I64, I64, I, P]
     L.mi_moe_hybrid_host_forward.argtypes = [P, P, P, P, I64, I64, I, P]
     L.mi_moe_hybrid_get_stats.argtypes = [P, P, P, P, P, P, P]
+    L.mi_moe_cpu_create.argtypes = [I64, I64, I64, I, I, I, ctypes.POINTER(P)]
+    L.mi_moe_cpu_destroy.argtypes = [P]
+    L.mi_moe_cpu_store_quantized.argtypes = [P, P, P, P, P, I]
+    L.mi_moe_cpu_quantize_and_store_expert.argtypes = [P, I64, I, P, I]
+    L.mi_moe_cpu_forward.argtypes = [P, P, P, P, P, I64, I64, I]
+    L.mi_moe_cpu_get_info.argtypes = [P, P, P, P, P, P, P]
+    L.mi_moe_cpu_set_isa.argtypes = [P, I]
+    L.mi_moe_cpu_isa_name.restype = ctypes.c_char_p
+    L.mi_moe_cpu_isa_name.argtypes = [I]
     for name in C_SYMBOLS:
         fn = getattr(L, name)
         if fn.restype is ctypes.c_int or fn.restype is None:
-            if name not in ("mi_moe_last_error", "mi_moe_get_last_run_time_ms"):
+            if name not in ("mi_moe_last_error", "mi_moe_get_last_run_time_ms", "mi_moe_cpu_isa_name"):
                 fn.restype = I
     _capi = L
     return L

@@ -24,11 +24,12 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["capi.hip", "common_kernels.hip", "w4a16.hip", "qint.hip", "hybrid.hip"]
-# Host-only C++ (no HIP): the host executor of the hybrid offload path.  Its
-# inner loops are compiled for AVX2 and baseline x86-64 and picked at
-# load time (target_clones); -ffp-contract=off keeps the stated fp32 order.
+# Host-only C++ (no HIP): the host executor of the hybrid offload path and the
+# CPU engine of the Q8_0 / Q4_0 layer (its C ABI too).  Inner loops are
+# compiled per instruction set (target attributes) and picked at run time;
+# -ffp-contract=off keeps the stated fp32 order.
 CXX = os.environ.get("CXX", "g++")
-CPP_SOURCES = ["host_experts.cpp"]
+CPP_SOURCES = ["host_experts.cpp", "cpu_moe.cpp", "capi_cpu.cpp"]
 CPP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-ffp-contract=off", "-fvisibility=hidden"]
 # Packed-FP32 instructions are disabled for all device code (only scalar /
 # float2 source is written; the compiler must not form v_pk_* fp32 ops).

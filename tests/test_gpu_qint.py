@@ -284,3 +284,22 @@ def test_large_shape_parity(cuda, qt, E, H, I, T, K):
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(T + 2)).to(torch.bfloat16)
     y = _run(h, x, ids, tw, cuda)
     assert max_rel_err(y, _oracle(qt, x, ids, tw, w, E, I)) <= TOL
+
+
+@pytest.mark.parametrize("qt", [0, 1])
+def test_cpu_and_hip_keys_agree(cuda, qt, monkeypatch):
+    """One handle with both copies (MIMOE_HOST_WEIGHTS=1): the CPU key (the
+    reference algorithm on host cores) and the HIP key agree to the parity
+    tolerance on the Qwen3 shape at the reference benchmark's decode sizes."""
+    monkeypatch.setenv("MIMOE_HOST_WEIGHTS", "1")
+    E, H, I = 128, 2048, 768
+    w = _weights(qt, E, H, I, seed=17)
+    h = _handle(qt, E, H, I, w, False, cuda)
+    for T in (1, 4):
+        ids, tw = topk_routing(T, E, 8, seed=40 + T)
+        x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
+        y_cpu = torch.ops.nanovllm.moe_forward(x, ids, tw, h)
+        y_gpu = _run(h, x, ids, tw, cuda)
+        assert y_cpu.device.type == "cpu"
+        assert max_rel_err(y_gpu, y_cpu) <= TOL
+        assert max_rel_err(y_cpu, _oracle(qt, x, ids, tw, w, E, I)) <= TOL
