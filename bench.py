@@ -20,8 +20,10 @@ size (K consecutive layer calls captured on the stream the kernels run on,
 HIP events around each replay), so the times are GPU work without the
 per-call Python dispatch cost; the eager per-call time is reported beside it.  Algorithmic bytes per call =
 U*bytes_per_expert + 4*T*H + 8*T*K with U the distinct experts of that call.
-Times are HIP events on the stream the kernel runs on.  cpu_baseline is the
-CPU restatement (oracle/) timed on this host on a bounded sample.
+Times are HIP events on the stream the kernel runs on.  cpu_baseline times
+this library's host paths on this machine's cores: the W4A16 layer on the
+host executor (same inputs and bytes formula), and the reference CPU
+algorithm (Q8_0 host engine) on config 1 with the reference's method.
 """
 from __future__ import annotations
 
@@ -61,53 +63,131 @@ def algo_bytes(ids_cpu, bs, fmt):
     return U * fmt.bytes_per_expert(2, H, I, GROUP) + 4 * bs * H + 8 * bs * TOPK, U
 
 
-def cpu_baseline(torch, fmt, wire_cpu, inputs_cpu, batches=BATCHES):
-    """Oracle W4A16 forward (scalar C, OpenMP over routed rows) on a bounded
-    sample: one call per batch size on the first routing."""
-    import numpy as np
-    import oracle
-    oracle.build()
-    cores = len(os.sched_getaffinity(0))
-    nthreads = min(cores, 16)
-    w13_q, w13_z, w13_s, w2_q, w2_z, w2_s = [t.numpy() if t.dtype != torch.bfloat16 else
-                                             t.view(torch.int16).numpy().view(np.uint16)
-                                             for t in wire_cpu]
-    tot_bytes, tot_s = 0, 0.0
+def host_threads():
+    """Threads of the host paths: OMP_NUM_THREADS (the GPU box's CPU share)
+    when set, else the affinity mask."""
+    v = os.environ.get("MIMOE_CPU_THREADS") or os.environ.get("OMP_NUM_THREADS")
+    return int(v) if v and int(v) > 0 else len(os.sched_getaffinity(0))
+
+
+def cpu_reference_config1(torch, fmt, nsets=4, warmup=5, runs=50, tokens=(1, 4, 8)):
+    """The reference's CPU benchmark method on BASELINE config 1 (Q8_0,
+    H=2048, I=768, E=128, top-8), run by the host engine of this library (the
+    reference CPU algorithm on x86; mi_moe_cpu_*): 4 weight sets cycled per
+    call, 5 warmup and 50 timed runs, op wall time per call, GB/s = unique
+    experts x per-expert weight bytes / time
+    (Int8-gemm/test/benchmark_fused_moe_cpu.py:20,78-116,171-194), for the
+    config's seeded routing (N(0,1) logits, top-8, softmax) and the
+    reference's round-robin routing ids[t,k] = (t*K + k) % E, w = 1/K.
+    Weights: uniform int8 codes and fp16 scales of the config's shape (the
+    timing does not depend on the values)."""
+    import ctypes
+    import nanovllm_moe as nm
+    L = nm.capi()
+    nthr = host_threads()
+    handles = []
+    for s_ in range(nsets):
+        g = torch.Generator().manual_seed(50 + s_)
+        gq = torch.randint(-127, 128, (E, 2 * I, H), generator=g, dtype=torch.int8)
+        dq = torch.randint(-127, 128, (E, H, I), generator=g, dtype=torch.int8)
+        gd = (torch.rand(E, 2 * I, H // 32, generator=g) * 1e-3).half()
+        dd = (torch.rand(E, H, I // 32, generator=g) * 1e-3).half()
+        c = ctypes.c_void_p()
+        nm.check(L.mi_moe_cpu_create(E, H, I, 0, nthr, 0, ctypes.byref(c)), "cpu_create")
+        nm.check(L.mi_moe_cpu_store_quantized(c, gq.data_ptr(), gd.data_ptr(), dq.data_ptr(), dd.data_ptr(), 0),
+                 "cpu_store")
+        del gq, dq, gd, dd
+        handles.append(c)
+    th, tp, isa, acpu, anodes = (ctypes.c_int() for _ in range(5))
+    last = ctypes.c_double()
+    nm.check(L.mi_moe_cpu_get_info(handles[0], ctypes.byref(th), ctypes.byref(tp), ctypes.byref(isa),
+                                   ctypes.byref(acpu), ctypes.byref(anodes), None), "cpu_info")
+    per_expert = fmt.bytes_per_expert(0, H, I)
+    out = {}
+    for routing in ("seeded", "round_robin"):
+        for T in tokens:
+            g = torch.Generator().manual_seed(7 + T)
+            x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+            if routing == "seeded":
+                val, ids = torch.topk(torch.randn(T, E, generator=g), TOPK, dim=-1)
+                w = torch.softmax(val, dim=-1).float().contiguous()
+                ids = ids.to(torch.int32).contiguous()
+            else:
+                base = torch.arange(T, dtype=torch.int64)[:, None] * TOPK + torch.arange(TOPK)[None, :]
+                ids = (base % E).to(torch.int32).contiguous()
+                w = torch.full((T, TOPK), 1.0 / TOPK)
+            y = torch.empty_like(x)
+            U = int(torch.unique(ids).numel())
+            call = lambda i: L.mi_moe_cpu_forward(handles[i % nsets], x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                                  ids.data_ptr(), T, TOPK, 1)
+            for i in range(warmup):
+                nm.check(call(i), "cpu_forward")
+            tot = 0.0
+            for i in range(runs):
+                nm.check(call(i), "cpu_forward")
+                nm.check(L.mi_moe_cpu_get_info(handles[i % nsets], None, None, None, None, None,
+                                               ctypes.byref(last)), "cpu_info")
+                tot += last.value
+            ms = tot / runs
+            out[f"{routing}_T{T}"] = {"ms": round(ms, 4), "GB_per_s": round(U * per_expert / (ms * 1e-3) / 1e9, 2),
+                                      "unique_experts": U}
+    for c in handles:
+        L.mi_moe_cpu_destroy(c)
+    return {
+        "workload": "config 1: Q8_0 fused MoE, H=2048 I=768 E=128 top-8, bf16 tokens",
+        "method": f"{nsets} weight sets cycled, {warmup} warmup + {runs} timed calls, op wall time, "
+                  "GB/s = unique experts x 5,013,504 B / ms (Int8-gemm/test/benchmark_fused_moe_cpu.py)",
+        "threads": th.value, "tp_shards": tp.value, "isa": L.mi_moe_cpu_isa_name(isa.value).decode(),
+        "affinity_cpus": acpu.value, "numa_nodes": anodes.value,
+        "results": out,
+        "reference_published_kunpeng920": {"T1_ms": 0.29, "T4_ms": 0.83, "T8_ms": 1.45,
+                                           "note": "2 CPUs, TP=4, 80 threads, README.md:69-79"},
+    }
+
+
+def cpu_baseline(torch, fmt, wire_cpu, inputs_cpu, batches=BATCHES, reps=20, warmup=3):
+    """The headline workload on the host: the W4A16 layer with every expert on
+    the host executor (AVX-512 / AVX2 group kernels, mi_moe_hybrid_host_forward)
+    over the same bs 1/2/4/8 inputs as the GPU sweep, GB/s with the same
+    algorithmic-bytes formula; plus the reference CPU algorithm on config 1
+    (cpu_reference_config1)."""
+    import ctypes
+    import nanovllm_moe as nm
+    L = nm.capi()
+    nthr = min(host_threads(), 16)
+    hh = ctypes.c_void_p()
+    mask = (ctypes.c_uint8 * E)(*([1] * E))
+    nm.check(L.mi_moe_hybrid_create(E, H, I, 2, mask, nthr, ctypes.byref(hh)), "hybrid_create")
+    ts = [t.contiguous() for t in wire_cpu]
+    nm.check(L.mi_moe_hybrid_store_awq(hh, *[t.data_ptr() for t in ts], GROUP, 1, 0, None), "hybrid_store")
+    tot_bytes, tot_s, per = 0, 0.0, {}
     for bs in batches:
         x, ids, w = inputs_cpu[bs]
-        xb = x.view(torch.int16).numpy().view(np.uint16)
+        part = torch.empty(bs, H, dtype=torch.float32)
+        call = lambda: L.mi_moe_hybrid_host_forward(hh, x.data_ptr(), w.data_ptr(), ids.data_ptr(), bs, TOPK, 1,
+                                                    part.data_ptr())
+        for _ in range(warmup):
+            nm.check(call(), "host_forward")
         t0 = time.perf_counter()
-        oracle.moe_forward_w4a16(1, 1, xb, w.numpy(), ids.numpy(), w13_q, w13_z, w13_s,
-                                 w2_q, w2_z, w2_s, E, I, GROUP, nthreads=nthreads)
-        tot_s += time.perf_counter() - t0
-        tot_bytes += algo_bytes(ids, bs, fmt)[0]
-    # the reference CPU algorithm itself (Q8_0, config 1: T=1) for context
-    g = torch.Generator().manual_seed(5)
-    q13 = torch.randint(-127, 128, (E, 2 * I, H), generator=g, dtype=torch.int8).numpy()
-    q2 = torch.randint(-127, 128, (E, H, I), generator=g, dtype=torch.int8).numpy()
-    d13 = (torch.rand(E, 2 * I, H // 32, generator=g) * 1e-3).half().view(torch.int16).numpy().view(np.uint16)
-    d2 = (torch.rand(E, H, I // 32, generator=g) * 1e-3).half().view(torch.int16).numpy().view(np.uint16)
-    x, ids, w = inputs_cpu[1]
-    t0 = time.perf_counter()
-    oracle.moe_forward_q(0, 1, 0, x.view(torch.int16).numpy().view(np.uint16), w.numpy(),
-                         ids.numpy(), q13, d13, q2, d2, E, I)
-    q8_s = time.perf_counter() - t0
-    q8_bytes = 8 * fmt.bytes_per_expert(0, H, I)
+        for _ in range(reps):
+            nm.check(call(), "host_forward")
+        dt = (time.perf_counter() - t0) / reps
+        b = algo_bytes(ids, bs, fmt)[0]
+        per[bs] = {"us_per_layer": round(dt * 1e6, 1), "GB_per_s": round(b / dt / 1e9, 2)}
+        tot_bytes += b
+        tot_s += dt
+    L.mi_moe_hybrid_destroy(hh)
+    ref = cpu_reference_config1(torch, fmt)
     return {
         "value": round(tot_bytes / tot_s / 1e9, 3),
         "unit": "GB/s",
-        "cores": nthreads,
+        "cores": nthr,
         "kind": "port",
-        "sample": "oracle/ W4A16 fp32 restatement, one layer call at each of bs 1,2,4,8 "
-                  f"(routing #0, weight set 0); {tot_s * 1e3:.1f} ms total; scalar C, "
-                  f"OpenMP over routed rows ({nthreads} threads)",
-        "us_per_layer_by_bs_sum": round(tot_s * 1e6, 1),
-        "q8_0_reference_algorithm_config1": {
-            "ms_per_layer": round(q8_s * 1e3, 3),
-            "GB_per_s": round(q8_bytes / q8_s / 1e9, 3),
-            "threads": 1,
-            "note": "orc_moe_forward_q (restatement of Int8-gemm/q8_gemm.cpp:276-646), T=1, scalar",
-        },
+        "sample": f"W4A16 layer, every expert on the host executor of this library, bs 1,2,4,8 on routing #0 "
+                  f"of the GPU sweep, {warmup} warmup + {reps} timed calls each ({tot_s * reps * 1e3:.0f} ms "
+                  f"timed); {nthr} threads of {len(os.sched_getaffinity(0))} affinity CPUs",
+        "per_batch": per,
+        "reference_algorithm_config1": ref,
     }
 
 
