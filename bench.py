@@ -272,9 +272,12 @@ def run_config(cfg, steps, warmup, eager=False):
     headline line): 1 = Q8_0, Qwen3 shape, T = 1 (the reference CPU
     configuration, here on the GPU; bs 2/4/8 beside it); 3 = Q4_0 prefill, Qwen3 shape, T 32..4096; 4 = MiniMax-M2
     W4A16, bs 1/8/64; 5 = Zipf-skewed routing (p ~ r^-1.2), T = 512, Qwen3
-    W4A16.  Weights are random in the format (timing does not depend on the
-    values); enough copies rotate that the 256 MB Infinity Cache cannot hold
-    what a call reads."""
+    W4A16; 6 = Q4_0 at the reference's own int4 benchmark shape (H=2048,
+    I=512, E=128, top-10, T 1..8, round-robin routing ids[t,k] = (t*K+k) % E
+    with weights 1/K; Int8-gemm/test/benchmark_fused_moe_int4.py:12-15,
+    Int8-gemm/test/benchmark_fused_moe_cpu.py:171-178).  Weights are random in
+    the format (timing does not depend on the values); enough copies rotate
+    that the 256 MB Infinity Cache cannot hold what a call reads."""
     import torch
     import nanovllm_moe
     from nanovllm_moe import formats as fmt
@@ -293,6 +296,8 @@ def run_config(cfg, steps, warmup, eager=False):
         E_, H_, I_, K_, quant, Ts, copies = 128, 2048, 768, 8, 1, (32, 128, 1024, 4096), 2
     elif cfg == 4:
         E_, H_, I_, K_, quant, Ts, copies = 256, 3072, 1536, 8, 2, (1, 8, 64), 4
+    elif cfg == 6:
+        E_, H_, I_, K_, quant, Ts, copies = 128, 2048, 512, 10, 1, (1, 2, 3, 4, 5, 6, 7, 8), 6
     else:
         E_, H_, I_, K_, quant, Ts, copies = 128, 2048, 768, 8, 2, (512,), 4
     handles = []
@@ -329,6 +334,9 @@ def run_config(cfg, steps, warmup, eager=False):
             x = torch.randn(T, H_, generator=gg).to(torch.bfloat16).to(dev)
             if cfg == 5:
                 ids, w = zipf_routing(T, E_, K_, seed=i)
+            elif cfg == 6:
+                ids = (torch.arange(T)[:, None] * K_ + torch.arange(K_)[None, :] + 37 * i) % E_
+                w = torch.full((T, K_), 1.0 / K_)
             else:
                 val, ids = torch.topk(torch.randn(T, E_, generator=gg), K_, dim=-1)
                 w = torch.softmax(val, dim=-1)
@@ -353,7 +361,9 @@ def run_config(cfg, steps, warmup, eager=False):
     names = {1: "Q8_0 (fp16 d per 32), Qwen3-30B-A3B shape (H=2048, I=768, E=128, top-8), Q8_0 activations",
              3: "Q4_0 prefill, Qwen3-30B-A3B shape (H=2048, I=768, E=128, top-8), Q8_0 activations",
              4: "W4A16, MiniMax-M2 shape (H=3072, I=1536, E=256, top-8, group 128)",
-             5: "W4A16, Qwen3-30B-A3B shape, Zipf-skewed routing (p ~ r^-1.2, distinct top-8)"}
+             5: "W4A16, Qwen3-30B-A3B shape, Zipf-skewed routing (p ~ r^-1.2, distinct top-8)",
+             6: "Q4_0 decode, the reference int4 benchmark shape (H=2048, I=512, E=128, top-10), "
+                "round-robin routing"}
     print(json.dumps({"config_id": cfg, "workload": names[cfg], "unit": "us/layer and GB/s",
                       "timing": "eager calls" if eager else "HIP-graph replay", "weight_copies": copies, "routings": nroutes,
                       "per_T": per}), flush=True)
@@ -538,9 +548,10 @@ def main():
     ap.add_argument("--traffic-file", type=str,
                     default=os.path.join(ROOT, "profiles", "w4a16_decode_traffic_qwen3_bs8.txt"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6),
                     help="BASELINE configuration: 2 (default) is the headline line; 1/3/4/5 print a "
-                         "measurement line for Q8_0 decode / Q4_0 prefill / MiniMax / Zipf routing")
+                         "measurement line for Q8_0 decode / Q4_0 prefill / MiniMax / Zipf routing; 6 "
+                         "is the reference's Q4_0 top-10 benchmark shape")
     ap.add_argument("--offload", type=int, default=0, metavar="NCOLD",
                     help="hybrid CPU-offload executor with NCOLD experts on the host (one JSON line)")
     ap.add_argument("--host-threads", type=int, default=0)

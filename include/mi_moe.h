@@ -181,7 +181,7 @@ int mi_moe_block_dots(mi_moe_handle* h, int64_t expert, int proj,
                       void* stream);
 
 /* The same block dots through the int8-MFMA block routine of the grouped
- * GEMMs (the path of Q8_0 / Q4_0 calls above 64 routed pairs), for bit-exact
+ * GEMMs (the path of Q8_0 / Q4_0 calls above 96 / 160 routed pairs), for bit-exact
  * checking of its two exact rewrites: acc[m][n][kb] int32 = the MFMA result
  * less its 1.5*2^23 bias (Q8_0: isum; Q4_0: 16*isum, the nibbles enter as
  * bytes 16*(n-8)), prod[m][n][kb] fp32 = the first scaled product the GEMMs

@@ -359,13 +359,14 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   const int64_t n = T * K;
   // decode sizes: the lane-per-row kernels, with the down projection and the
   // combine token-major in one launch (no eout round trip) where it fits;
-  // above kQGemmMinPairs routed pairs, or where the lane-per-row LDS does not
+  // above q_lpr_max_pairs routed pairs, or where the lane-per-row LDS does not
   // fit, the int8 grouped GEMMs (mi_moe_create checked that one of the two
   // serves every call)
   const size_t lmax = device_max_lds();
   const int iE = (int)h->E, iH = (int)h->H, iI = (int)h->I, in = (int)n, iK = (int)K;
-  const bool token_down = n <= kQGemmMinPairs && K <= kDownMaxK && q_lpr_fits(iH, iI, iE, in, iK, true, lmax);
-  const bool lpr_small = n <= kQGemmMinPairs && (token_down || q_lpr_fits(iH, iI, iE, in, iK, false, lmax));
+  const bool small = n <= q_lpr_max_pairs(h->quant);
+  const bool token_down = small && K <= kDownMaxK && q_lpr_fits(iH, iI, iE, in, iK, true, lmax);
+  const bool lpr_small = small && (token_down || q_lpr_fits(iH, iI, iE, in, iK, false, lmax));
   const bool gemm = q_gemm_ok(iH, iI) && !lpr_small;
   if (!gemm && !q_lpr_fits(iH, iI, iE, in, iK, token_down, lmax))
     return fail(MI_MOE_EUNSUPPORTED, "Q8_0/Q4_0 call of %lld routed pairs does not fit the device's LDS", (long long)n);

@@ -33,8 +33,12 @@ __host__ __device__ constexpr int route_chunks(int n) { return (n + kRouteChunk 
 
 // Row tile of the grouped GEMMs of the sorted path: routed rows of one expert.
 constexpr int kGemmRows = 64;
-// Q8_0 / Q4_0: above this many routed pairs the int8 grouped GEMMs run
-constexpr int kQGemmMinPairs = 64;
+// Q8_0 / Q4_0: up to this many routed pairs the lane-per-row kernels run,
+// above it the int8 grouped GEMMs (the measured crossover on the H=2048,
+// E=128, I=512/768 layers, top-8 and top-10: a Q4_0 weight byte holds two
+// values, so its lane-per-row dots stay ahead of the GEMMs' per-block VALU
+// scaling to more pairs than Q8_0's).
+inline int q_lpr_max_pairs(int quant) { return quant == 1 ? 160 : 96; }
 // Q8_0 / Q4_0 lane-per-row gate_up: up to this many routed pairs the work
 // items are pairs routed by one ballot per wave (grid = pairs x slices).
 constexpr int kQBallotMaxPairs = 64;
@@ -85,7 +89,7 @@ constexpr size_t kMaxLds = 65536;
 size_t device_max_lds();
 
 // The decode down kernel runs a wave per routed expert of a token.
-constexpr int kDownMaxK = 8;
+constexpr int kDownMaxK = 16;
 
 // LDS bytes of the W4A16 decode kernels.
 // Phase-1 cross-wave reduction buffer of one slice: [NW waves][gate,up][64][4] f32.

@@ -60,10 +60,12 @@ def test_small_parity(cuda, small, T, K):
     assert max_rel_err(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("T,K", [(3, 10), (64, 1), (5, 7)])
+@pytest.mark.parametrize("T,K", [(3, 10), (4, 16), (7, 10), (64, 1), (5, 7)])
 def test_decode_boundary_shapes(cuda, T, K):
-    """K > 8 leaves the decode path for the sorted one; K = 1 runs single-wave
-    down workgroups; odd K exercises the per-token wave count."""
+    """Top-10 and top-16 at up to 64 routed pairs run the decode path (16
+    waves per down workgroup at K = 16); 70 pairs leave it for the sorted
+    one; K = 1 runs single-wave down workgroups; odd K exercises the
+    per-token wave count."""
     E, H, I = 16, 512, 256
     w = w4a16_random(E, H, I, seed=400 + K)
     h = _handle(E, H, I, w, True, cuda)
