@@ -215,6 +215,11 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];
 
+// mi_moe_route's per-device routing arrays (grown on demand, kept until the
+// process ends; calls on one process serialize on the mutex).
+std::mutex g_route_mu;
+DevBuf g_route_buf[kMaxDevices];
+
 int init_scratch(int dev) {
   if (dev < 0 || dev >= kMaxDevices) return MI_MOE_OK;   // the no-alloc entry point then reports it
   std::lock_guard<std::mutex> lk(g_scratch_mu);
@@ -785,16 +790,21 @@ MI_API int mi_moe_route(const int32_t* ids, int64_t T, int64_t K, int64_t E, int
     return MI_MOE_OK;
   }
   if (!ids || !token_map || !scatter) return fail(MI_MOE_EINVAL, "null pointer");
-  DevBuf active, U, chunk;
-  HIPCHK(active.alloc((size_t)E * sizeof(int32_t)));
-  HIPCHK(U.alloc(sizeof(int32_t)));
-  HIPCHK(chunk.alloc((size_t)route_chunks((int)(T * K)) * E * sizeof(int32_t)));
-  RouteGlobal rg{counts, starts, (int32_t*)active.p, token_map, scatter, (int32_t*)U.p, nullptr, nullptr,
-                 (int32_t*)chunk.p};
+  // the routing kernels' own arrays (active experts, their count, per-chunk
+  // histograms) live in a per-device buffer that grows to the largest call
+  // and is reused; the call holds it until its stream has finished
+  int dev = 0;
+  HIPCHK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MI_MOE_EUNSUPPORTED, "device index %d out of range", dev);
+  const size_t a_bytes = ((size_t)E * sizeof(int32_t) + 255) & ~(size_t)255;
+  const size_t need = a_bytes + 256 + (size_t)route_chunks((int)(T * K)) * E * sizeof(int32_t);
+  std::lock_guard<std::mutex> lock(g_route_mu);
+  DevBuf& buf = g_route_buf[dev];
+  if (buf.bytes < need) HIPCHK(buf.alloc(need));
+  unsigned char* base = (unsigned char*)buf.p;
+  RouteGlobal rg{counts, starts, (int32_t*)base, token_map, scatter, (int32_t*)(base + a_bytes), nullptr, nullptr,
+                 (int32_t*)(base + a_bytes + 256)};
   HIPCHK(launch_route_global(ids, (int)(T * K), (int)K, (int)E, rg, st, 1));
   HIPCHK(hipStreamSynchronize(st));
-  active.release();
-  U.release();
-  chunk.release();
   return MI_MOE_OK;
 }

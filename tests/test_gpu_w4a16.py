@@ -113,8 +113,8 @@ def test_repeat_calls_deterministic(cuda, small, T, K):
 @pytest.mark.parametrize("T,K", [(4, 8), (40, 8)])
 def test_graph_replay_matches_eager(cuda, small, T, K):
     """Calls captured into a HIP graph give the eager results bit for bit on
-    every replay, with eager calls on the same handle between the replays (the
-    workspace arrival counters must come back to zero after each call)."""
+    every replay, with eager calls on the same handle between the replays
+    (they share the handle's workspace)."""
     w, h = small
     E, H, I = SMALL["E"], SMALL["H"], SMALL["I"]
     cases = []
