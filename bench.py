@@ -444,15 +444,17 @@ def run_router(steps, warmup):
                       "per_bs": per}), flush=True)
 
 
-def run_offload(steps, warmup, ncold=16, threads=0):
-    """Hybrid CPU-offload executor (mi_moe_hybrid_forward) on the headline
-    W4A16 shape: experts E-ncold..E-1 stay in host memory and run on host
-    threads, the others on the device; seeded uniform top-8 routing.  Per batch
-    size: the hybrid call (wall clock around synchronized calls, since its host
-    half runs on host threads), the all-device call on the same inputs, and
-    the host pass alone (its own timer) with the cold experts' weight bytes it
-    streams.  The reference runs the whole layer on the host in such a callback
-    (moe_forward_npu_stream, Int8-gemm/nanovllm_ops.cpp:244-305)."""
+def run_offload(steps, warmup, ncold=16, threads=0, quant=2):
+    """Hybrid CPU-offload executor (mi_moe_hybrid_forward) on the Qwen3 shape
+    (W4A16 by default; quant 0 / 1 = Q8_0 / Q4_0, whose cold experts run on
+    the host engine of the reference CPU algorithm): experts E-ncold..E-1 stay
+    in host memory and run on host threads, the others on the device; seeded
+    uniform top-8 routing.  Per batch size: the hybrid call (wall clock around
+    synchronized calls, since its host half runs on host threads; and one HIP
+    graph replaying the same calls), the all-device call on the same inputs,
+    and the host pass alone (its own timer) with the cold experts' weight
+    bytes it streams.  The reference runs the whole layer on the host in such
+    a callback (moe_forward_npu_stream, Int8-gemm/nanovllm_ops.cpp:244-305)."""
     import torch
     import nanovllm_moe
     from nanovllm_moe import HybridMoE, formats
@@ -465,19 +467,32 @@ def run_offload(steps, warmup, ncold=16, threads=0):
         return torch.where(v >= 2**31, v - 2**32, v).to(torch.int32)
 
     E_, H_, I_, K_ = 128, 2048, 768, 8
-    s13 = (torch.rand(E_, H_ // GROUP, 2 * I_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
-    s2 = (torch.rand(E_, I_ // GROUP, H_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
-    ws = (rint32(E_, H_, 2 * I_ // 8), rint32(E_, H_ // GROUP, 2 * I_ // 8), s13,
-          rint32(E_, I_, H_ // 8), rint32(E_, I_ // GROUP, H_ // 8), s2)
     cold = list(range(E_ - ncold, E_))
-    hm = HybridMoE(E_, H_, I_, nanovllm_moe.W4A16, host_experts=cold, num_threads=threads)
-    hm.store_awq(*ws)
-    h = torch.classes.nanovllm.MoEInfer(E_, H_, I_, 2)
-    h.store_awq_repack(*ws, GROUP)
+    hm = HybridMoE(E_, H_, I_, quant, host_experts=cold, num_threads=threads)
+    h = torch.classes.nanovllm.MoEInfer(E_, H_, I_, quant)
+    if quant == 2:
+        s13 = (torch.rand(E_, H_ // GROUP, 2 * I_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
+        s2 = (torch.rand(E_, I_ // GROUP, H_, generator=g, device=dev) * 0.004 + 0.001).bfloat16()
+        ws = (rint32(E_, H_, 2 * I_ // 8), rint32(E_, H_ // GROUP, 2 * I_ // 8), s13,
+              rint32(E_, I_, H_ // 8), rint32(E_, I_ // GROUP, H_ // 8), s2)
+        hm.store_awq(*ws)
+        h.store_awq_repack(*ws, GROUP)
+    else:
+        if quant == 0:
+            q13 = torch.randint(-127, 128, (E_, 2 * I_, H_), generator=g, dtype=torch.int8, device=dev)
+            q2 = torch.randint(-127, 128, (E_, H_, I_), generator=g, dtype=torch.int8, device=dev)
+            d13 = (torch.rand(E_, 2 * I_, H_ // 32, generator=g, device=dev) * 1e-3).half()
+            d2 = (torch.rand(E_, H_, I_ // 32, generator=g, device=dev) * 1e-3).half()
+        else:
+            q13, d13 = formats.q4_0_random((E_, 2 * I_), H_, generator=g, device=dev)
+            q2, d2 = formats.q4_0_random((E_, H_), I_, generator=g, device=dev)
+        ws = (q13, d13, q2, d2)
+        hm.store_quantized(*ws)
+        h.store_quantized_repack(*ws)
     h.set_timing(False)
     del ws
     torch.cuda.synchronize()
-    per_expert = formats.bytes_per_expert(2, H_, I_)
+    per_expert = formats.bytes_per_expert(quant, H_, I_, GROUP)
     st0 = hm.stats()
     per = {}
     n = max(steps // 8, 8)
@@ -506,6 +521,21 @@ def run_offload(steps, warmup, ncold=16, threads=0):
 
         t_h = wall(lambda i: hm.forward(*calls[i % 8][:3]))
         t_d = wall(lambda i: torch.ops.nanovllm.moe_forward(*calls[i % 8][:3], h))
+        # the same calls replayed from one HIP graph (host callback nodes included)
+        outs = [torch.empty(bs, H_, dtype=torch.bfloat16, device=dev) for _ in range(8)]
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(8):
+                hm.forward(*calls[i][:3], out=outs[i])
+        gr.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reps = max(n // 8, 2)
+        for _ in range(reps):
+            gr.replay()
+        torch.cuda.synchronize()
+        t_g = (time.perf_counter() - t0) * 1e6 / (8 * reps)
+        del gr
         host_ms, queue_ms, pairs, cold_bytes = [], [], [], []
         for i in range(8):
             x, ids, w, ids_cpu = calls[i]
@@ -519,16 +549,18 @@ def run_offload(steps, warmup, ncold=16, threads=0):
             cold_bytes.append(len(used) * per_expert)
         hms = sum(host_ms) / len(host_ms)
         gbs = sum(cold_bytes) / len(cold_bytes) / (hms * 1e-3) / 1e9 if hms > 0 else None
-        per[str(bs)] = {"hybrid_us_per_call": round(t_h, 1), "device_only_us_per_call": round(t_d, 1),
+        per[str(bs)] = {"hybrid_us_per_call": round(t_h, 1), "hybrid_graph_us_per_call": round(t_g, 1),
+                        "device_only_us_per_call": round(t_d, 1),
                         "host_pass_ms": round(hms, 3), "callback_queue_ms": round(sum(queue_ms) / len(queue_ms), 3),
                         "cold_pairs_per_call": sum(pairs) / len(pairs),
                         "cold_weight_MB_per_call": round(sum(cold_bytes) / len(cold_bytes) / 1e6, 2),
                         "host_weight_GB_per_s": round(gbs, 2) if gbs else None}
-        log(f"[bench offload] bs={bs}: hybrid {t_h:.1f} us, device-only {t_d:.1f} us, host pass {hms:.3f} ms "
+        log(f"[bench offload] bs={bs}: hybrid {t_h:.1f} us (graph {t_g:.1f}), device-only {t_d:.1f} us, host pass {hms:.3f} ms "
             f"({sum(pairs) / len(pairs):.1f} cold pairs, {per[str(bs)]['host_weight_GB_per_s']} GB/s of host weights)")
-    print(json.dumps({"workload": f"hybrid CPU-offload W4A16 layer, Qwen3-30B-A3B shape (H=2048, I=768, E=128, "
-                                  f"top-8), {ncold} experts on the host", "unit": "us per call",
-                      "timing": "wall clock around synchronized eager calls",
+    fmt_name = {0: "Q8_0", 1: "Q4_0", 2: "W4A16"}[quant]
+    print(json.dumps({"workload": f"hybrid CPU-offload {fmt_name} layer, Qwen3-30B-A3B shape (H=2048, I=768, "
+                                  f"E=128, top-8), {ncold} experts on the host", "unit": "us per call",
+                      "timing": "wall clock around synchronized eager calls; graph = one HIP graph of 8 calls",
                       "host_threads": threads or "default (hardware threads, at most 16)",
                       "device_experts": st0["device_experts"], "host_experts": st0["host_experts"],
                       "host_weight_bytes": st0["host_weight_bytes"], "per_bs": per}), flush=True)
@@ -552,6 +584,8 @@ def main():
                     help="BASELINE configuration: 2 (default) is the headline line; 1/3/4/5 print a "
                          "measurement line for Q8_0 decode / Q4_0 prefill / MiniMax / Zipf routing; 6 "
                          "is the reference's Q4_0 top-10 benchmark shape")
+    ap.add_argument("--offload-quant", type=int, default=2, choices=(0, 1, 2),
+                    help="weight format of the --offload layer: 0 Q8_0, 1 Q4_0, 2 W4A16")
     ap.add_argument("--offload", type=int, default=0, metavar="NCOLD",
                     help="hybrid CPU-offload executor with NCOLD experts on the host (one JSON line)")
     ap.add_argument("--host-threads", type=int, default=0)
@@ -571,7 +605,7 @@ def main():
         run_router(args.steps, args.warmup)
         return
     if args.offload:
-        run_offload(args.steps, args.warmup, args.offload, args.host_threads)
+        run_offload(args.steps, args.warmup, args.offload, args.host_threads, args.offload_quant)
         return
     if args.config != 2:
         run_config(args.config, args.steps, args.warmup, args.eager)

@@ -701,7 +701,7 @@ void Engine::quantize_and_store(int64_t e, int proj, const float* w) {
 }
 
 int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const int32_t* topk_ids, int64_t T,
-                    int64_t K, int act_dtype) {
+                    int64_t K, int act_dtype, float* y_f32) {
   const auto t0 = std::chrono::steady_clock::now();
   const int64_t E = E_, H = H_, Ish = I_ / tp_, HB = H / 32, IB = Ish / 32;
   // routing: stable counting sort by expert (Int8-gemm/moe_common.cpp:146-216)
@@ -721,7 +721,8 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
     scat[(size_t)i] = pos;
   }
   if (total == 0) {   // Int8-gemm/q8_gemm.cpp:328-333
-    memset(y, 0, sizeof(uint16_t) * (size_t)(T * H));
+    if (y_f32) memset(y_f32, 0, sizeof(float) * (size_t)(T * H));
+    else memset(y, 0, sizeof(uint16_t) * (size_t)(T * H));
     last_ms_ = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return 0;
   }
@@ -734,6 +735,16 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
   const int64_t ntasks = (int64_t)tasks.size();
 
   std::vector<float> part((size_t)(tp_ * T * H));
+  // per-token stages (Stage A, C1, C2) of a few tokens run on the calling
+  // thread: waking the pool costs more than the work
+  const bool few = T * H <= (int64_t)16 * 2048;
+  auto per_token = [&](NodePool& pool, const std::function<void(int64_t)>& f) {
+    if (few) {
+      for (int64_t t = 0; t < T; ++t) f(t);
+    } else {
+      pool.run(T, f);
+    }
+  };
   auto run_shard = [&](int s) {
     NodePool& pool = *pools_[(size_t)s];
     const Shard& sh = shards_[(size_t)s];
@@ -742,7 +753,7 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
     std::vector<uint8_t> xb((size_t)(T * H));
     std::vector<float> xd((size_t)(T * HB));
     std::vector<int32_t> xs((size_t)(T * HB));
-    pool.run(T, [&](int64_t t) {
+    per_token(pool, [&](int64_t t) {
       float v[32];
       for (int64_t b = 0; b < HB; ++b) {
         for (int j = 0; j < 32; ++j) v[j] = half_f32(x[t * H + 32 * b + j], act_dtype);
@@ -800,30 +811,42 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
         }
     };
     std::vector<float> inter((size_t)(total * 2 * Ish)), eout((size_t)(total * H));
-    if (ntasks * 2 <= pool.size()) {
-      // 2 threads per task: gate rows / up rows, then halves of the down rows
-      pool.run(2 * ntasks, [&](int64_t i) {
-        const Task& tk = tasks[(size_t)(i / 2)];
-        const int half = (int)(i % 2);
+    // with few tasks, P threads per task (the reference's 2-way split,
+    // Int8-gemm/q8_gemm.cpp:382-488: gate rows / up rows, then halves of the
+    // down rows; up to split_max_ parts of whole 16-row panels where set):
+    // every output row is computed the same way whatever the split
+    const int P = ntasks * 2 <= pool.size() ? std::max(2, std::min<int>(split_max_, pool.size() / (int)ntasks)) : 1;
+    auto part_rows = [&](int64_t N, int part, int64_t& a, int64_t& b) {
+      const int64_t panels = N / kNR;
+      a = panels * part / P * kNR;
+      b = panels * (part + 1) / P * kNR;
+    };
+    if (P >= 2) {
+      pool.run(P * ntasks, [&](int64_t i) {
+        const Task& tk = tasks[(size_t)(i / P)];
+        const int part = (int)(i % P);
         std::vector<int8_t> a;
         std::vector<uint8_t> ab;
         std::vector<float> ad;
         std::vector<int32_t> as;
         gather(tk, a, ab, ad, as);
         const ARows A{a.data(), ab.data(), ad.data(), as.data(), H};
-        gemm_rows(isa_, sh.w13[(size_t)tk.e], A, tk.count, half * Ish, (half + 1) * Ish,
-                  inter.data() + (size_t)tk.start * 2 * Ish, 2 * Ish);
+        int64_t n0, n1;
+        part_rows(2 * Ish, part, n0, n1);
+        gemm_rows(isa_, sh.w13[(size_t)tk.e], A, tk.count, n0, n1, inter.data() + (size_t)tk.start * 2 * Ish,
+                  2 * Ish);
       });
-      pool.run(2 * ntasks, [&](int64_t i) {
-        const Task& tk = tasks[(size_t)(i / 2)];
-        const int half = (int)(i % 2);
+      pool.run(P * ntasks, [&](int64_t i) {
+        const Task& tk = tasks[(size_t)(i / P)];
+        const int part = (int)(i % P);
         std::vector<int8_t> a;
         std::vector<uint8_t> ab;
         std::vector<float> ad;
         std::vector<int32_t> as;
         activate(tk.count, inter.data() + (size_t)tk.start * 2 * Ish, a, ab, ad, as);
         const ARows A{a.data(), ab.data(), ad.data(), as.data(), Ish};
-        const int64_t h0 = half == 0 ? 0 : (H / 2) / kNR * kNR, h1 = half == 0 ? (H / 2) / kNR * kNR : H;
+        int64_t h0, h1;
+        part_rows(H, part, h0, h1);
         gemm_rows(isa_, sh.w2[(size_t)tk.e], A, tk.count, h0, h1, eout.data() + (size_t)tk.start * H, H);
       });
     } else {
@@ -844,7 +867,7 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
     }
     // Stage C1 (Int8-gemm/q8_gemm.cpp:593-613)
     float* yp = part.data() + (size_t)s * T * H;
-    pool.run(T, [&](int64_t t) {
+    per_token(pool, [&](int64_t t) {
       float* acc = yp + t * H;
       for (int64_t j = 0; j < H; ++j) acc[j] = 0.0f;
       for (int64_t k = 0; k < K; ++k) {
@@ -871,11 +894,12 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
     for (auto& th : launch) th.join();
   }
   // Stage C2 (Int8-gemm/q8_gemm.cpp:621-641): shard order, then the cast
-  pools_[0]->run(T, [&](int64_t t) {
+  per_token(*pools_[0], [&](int64_t t) {
     for (int64_t j = 0; j < H; ++j) {
       float acc = part[(size_t)(t * H + j)];
       for (int s = 1; s < tp_; ++s) acc = acc + part[(size_t)(s * T * H + t * H + j)];
-      y[t * H + j] = f32_half(acc, act_dtype);
+      if (y_f32) y_f32[t * H + j] = acc;
+      else y[t * H + j] = f32_half(acc, act_dtype);
     }
   });
   last_ms_ = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();

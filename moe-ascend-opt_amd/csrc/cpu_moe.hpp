@@ -85,13 +85,19 @@ class Engine {
              int scale_dtype);
   // one projection (0 gate [I,H], 1 up [I,H], 2 down [H,I]) of expert e, fp32 values
   void quantize_and_store(int64_t e, int proj, const float* w);
+  // y [T,H] in act_dtype; or, with y_f32, the fp32 sums before the cast
+  // (Stage C2 without its rounding) into y_f32 and y unused
   int forward(const uint16_t* x, uint16_t* y, const float* topk_w, const int32_t* topk_ids, int64_t T, int64_t K,
-              int act_dtype);
+              int act_dtype, float* y_f32 = nullptr);
   bool loaded() const { return loaded_; }
   int threads() const { return threads_; }
   int tp() const { return tp_; }
   Isa isa() const { return isa_; }
   void set_isa(Isa i) { isa_ = i; }
+  // Threads per task when there are fewer than half as many tasks as threads:
+  // 2 (default) is the reference's split; more parts of whole 16-row panels
+  // keep every thread busy when few experts are routed (same results).
+  void set_split_max(int p) { split_max_ = p < 2 ? 2 : p; }
   double last_ms() const { return last_ms_; }
   const Topology& topology() const { return topo_; }
   int64_t E() const { return E_; }
@@ -111,6 +117,7 @@ class Engine {
   std::vector<std::unique_ptr<NodePool>> pools_;
   std::vector<Shard> shards_;
   bool loaded_ = false;
+  int split_max_ = 2;
   double last_ms_ = -1.0;
 };
 

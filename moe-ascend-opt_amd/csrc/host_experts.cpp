@@ -4,6 +4,7 @@
 // one thread, for all the routed rows of its expert.
 #include "host_experts.hpp"
 
+#include <immintrin.h>
 #include <math.h>
 #include <string.h>
 
@@ -211,14 +212,57 @@ __attribute__((always_inline)) inline void awq_group_t(const int32_t* __restrict
   if (p < P) awq_group_pc<VU, VI, VF, 1>(q, NW, k0, xf + p, accg + p * stride);
 }
 
+// AVX-512 form of a 16-word group: a nibble slot becomes 16 floats with one
+// shift and one vpermps from the table 0..15 (vpermps reads only the low 4
+// bits of each index) instead of shift, mask and convert.  The multiply and
+// the add stay separate, as in awq_group_pc, so every task width (and so
+// every thread count) gives the same bits.  Same accg layout as awq_group_pc.
+template <int PC>
+__attribute__((target("avx512f"), always_inline)) inline void awq_group16_512_pc(
+    const int32_t* __restrict__ q, int64_t NW, int64_t k0, const float* const* xf, float* __restrict__ accg) {
+  const __m512 tab = _mm512_setr_ps(0.f, 1.f, 2.f, 3.f, 4.f, 5.f, 6.f, 7.f, 8.f, 9.f, 10.f, 11.f, 12.f, 13.f,
+                                    14.f, 15.f);
+  __m512 acc[PC][8];
+  for (int pp = 0; pp < PC; ++pp)
+    for (int sl = 0; sl < 8; ++sl) acc[pp][sl] = _mm512_setzero_ps();
+  for (int64_t k = k0; k < k0 + 128; ++k) {
+    const __m512i w = _mm512_loadu_si512(reinterpret_cast<const void*>(q + k * NW));
+    __m512 xv[PC];
+    for (int pp = 0; pp < PC; ++pp) xv[pp] = _mm512_set1_ps(xf[pp][k]);
+#pragma GCC unroll 8
+    for (int sl = 0; sl < 8; ++sl) {
+      const __m512i idx = sl == 0 ? w : _mm512_srli_epi32(w, 4 * sl);
+      const __m512 v = _mm512_permutexvar_ps(idx, tab);
+      for (int pp = 0; pp < PC; ++pp) acc[pp][sl] = _mm512_add_ps(acc[pp][sl], _mm512_mul_ps(xv[pp], v));
+    }
+  }
+  for (int pp = 0; pp < PC; ++pp)
+    for (int sl = 0; sl < 8; ++sl) _mm512_storeu_ps(accg + (pp * 8 + sl) * 16, acc[pp][sl]);
+}
+
+__attribute__((target("avx512f"))) void awq_group16_512(const int32_t* q, int64_t NW, int64_t k0,
+                                                        const float* const* xf, int64_t P, float* accg) {
+  int64_t p = 0;
+  for (; p + 2 <= P; p += 2) awq_group16_512_pc<2>(q, NW, k0, xf + p, accg + p * 128);
+  if (p < P) awq_group16_512_pc<1>(q, NW, k0, xf + p, accg + p * 128);
+}
+
+const bool kHostAvx512 = __builtin_cpu_supports("avx512f");
+
 __attribute__((target_clones("avx512f", "avx2", "default")))
-void awq_group(int nww, const int32_t* q, int64_t NW, int64_t k0, const float* const* xf, int64_t P, float* accg) {
+void awq_group_generic(int nww, const int32_t* q, int64_t NW, int64_t k0, const float* const* xf, int64_t P,
+                       float* accg) {
   switch (nww) {
     case 16: awq_group_t<vu16, vi16, vf16>(q, NW, k0, xf, P, accg); break;
     case 8: awq_group_t<vu8, vi8, vf8>(q, NW, k0, xf, P, accg); break;
     case 4: awq_group_t<vu4, vi4, vf4>(q, NW, k0, xf, P, accg); break;
     default: awq_group_t<vu2, vi2, vf2>(q, NW, k0, xf, P, accg); break;
   }
+}
+
+void awq_group(int nww, const int32_t* q, int64_t NW, int64_t k0, const float* const* xf, int64_t P, float* accg) {
+  if (nww == 16 && kHostAvx512) awq_group16_512(q, NW, k0, xf, P, accg);
+  else awq_group_generic(nww, q, NW, k0, xf, P, accg);
 }
 
 // Columns [8*j0, 8*j1) of an AWQ matrix (qweight [K][N/8], qzeros [K/128][N/8],
@@ -348,7 +392,16 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
     act.resize((size_t)(P * I));
     if (awq) xs.assign((size_t)(P * G2), 0.0f);
     else { aq.resize((size_t)(P * I)); ad.resize((size_t)(P * (I / 32))); }
-    pool.run(P, [&](int64_t p) {
+    // per-pair and per-token stages of a few rows run on the calling thread
+    // (waking the pool costs more than the work)
+    auto small_run = [&](int64_t n, const std::function<void(int64_t)>& f) {
+      if (n <= 16) {
+        for (int64_t i = 0; i < n; ++i) f(i);
+      } else {
+        pool.run(n, f);
+      }
+    };
+    small_run(P, [&](int64_t p) {
       float* a = &act[p * I];
       const float* g = &gu[p * N13];
       for (int64_t j = 0; j < I; ++j) a[j] = silu_mul(g[j], g[I + j]);
@@ -381,7 +434,7 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
       }
     });
     // weighted sum over k in ascending order
-    pool.run(nT, [&](int64_t t) {
+    small_run(nT, [&](int64_t t) {
       float* yr = y_part + (t0 + t) * H;
       for (int64_t k = 0; k < K; ++k) {
         const int64_t pos = pos_of[t * K + k];

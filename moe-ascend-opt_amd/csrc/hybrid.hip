@@ -1,7 +1,9 @@
 // hybrid.hip -- the hybrid CPU-offload executor (mi_moe_hybrid_* in
 // include/mi_moe.h).  Hot experts live compacted in a device handle; cold
-// experts keep their wire-format weights in host memory and run on host
-// threads (host_experts.cpp).
+// experts keep their weights in host memory and run on host threads: Q8_0 /
+// Q4_0 on the host engine of the reference CPU algorithm (cpu_moe.cpp, VNNI /
+// AVX2 int8 dots, bit-equal to the oracle), W4A16 on the host executor
+// (host_experts.cpp, wire-format bytes).
 //
 // One forward on the caller's stream S, with a side stream D owned by the
 // handle (both at the default priority):
@@ -29,6 +31,7 @@
 #include <new>
 #include <vector>
 
+#include "cpu_moe.hpp"
 #include "host_experts.hpp"
 #include "mi_moe.h"
 #include "mi_moe_device.hpp"
@@ -138,6 +141,17 @@ int default_threads() {
 
 using namespace mimoe;
 
+// Arguments of one host callback.  An eager call's context is freed by its
+// callback; a call captured into a graph keeps its context in the handle
+// (graph_ctx), since every replay of the graph runs the callback on it.
+struct CallCtx {
+  struct mi_moe_hybrid* hh;
+  int64_t T, K;
+  int act;
+  std::chrono::steady_clock::time_point enqueued;
+  bool eager;
+};
+
 struct mi_moe_hybrid {
   int64_t E = 0, H = 0, I = 0;
   int quant = 0;
@@ -147,7 +161,9 @@ struct mi_moe_hybrid {
   int64_t Eg = 0;
   std::vector<int32_t> slot_of;      // [E]: device slot, or -1 for a cold expert
   mimoe_host::ColdSet cold;
-  std::unique_ptr<mimoe_host::Pool> pool;
+  std::unique_ptr<mimoe_host::Pool> pool;            // W4A16 host executor
+  std::unique_ptr<mimoe_cpu::Engine> qeng;           // Q8_0 / Q4_0: the cold experts on the host engine
+  std::vector<int32_t> qids;                         // host pass: ids mapped to cold experts (-1 otherwise)
   std::mutex host_mu;                // host forwards run one at a time
   DBuf slot_dev, ids_dev;
   PinBuf x_h, ids_h, w_h, part_h;
@@ -158,22 +174,30 @@ struct mi_moe_hybrid {
   std::atomic<double> last_queue_ms{-1.0};   // forward call -> start of its host callback
   std::atomic<int64_t> last_pairs{0};
   std::atomic<int> host_error{0};    // a host callback failed (reported by the next call)
+  std::vector<std::unique_ptr<CallCtx>> graph_ctx;   // arguments of callbacks captured in graphs
 };
 
 namespace {
-
-struct CallCtx {
-  mi_moe_hybrid* hh;
-  int64_t T, K;
-  int act;
-  std::chrono::steady_clock::time_point enqueued;
-};
 
 void run_host(mi_moe_hybrid* hh, const uint16_t* x, int act, const int32_t* ids, const float* w, int64_t T,
               int64_t K, float* part) {
   std::lock_guard<std::mutex> lk(hh->host_mu);
   const auto t0 = std::chrono::steady_clock::now();
-  const int64_t np = mimoe_host::forward(hh->cold, *hh->pool, x, act, ids, w, T, K, part);
+  int64_t np = 0;
+  if (hh->quant == 2) {
+    np = mimoe_host::forward(hh->cold, *hh->pool, x, act, ids, w, T, K, part);
+  } else if (!hh->qeng) {   // no cold expert
+    std::memset(part, 0, sizeof(float) * (size_t)(T * hh->H));
+  } else {
+    hh->qids.resize((size_t)(T * K));
+    for (int64_t i = 0; i < T * K; ++i) {
+      const int32_t e = ids[i];
+      const int32_t c = (e >= 0 && e < hh->E) ? hh->cold.cold_of[(size_t)e] : -1;
+      hh->qids[(size_t)i] = c;
+      np += c >= 0;
+    }
+    hh->qeng->forward(x, nullptr, w, hh->qids.data(), T, K, act, part);
+  }
   const auto t1 = std::chrono::steady_clock::now();
   hh->last_pairs.store(np);
   hh->last_host_ms.store(std::chrono::duration<double, std::milli>(t1 - t0).count());
@@ -181,10 +205,12 @@ void run_host(mi_moe_hybrid* hh, const uint16_t* x, int act, const int32_t* ids,
 
 // Stream host callback: no HIP calls in here.
 void host_callback(void* arg) {
-  std::unique_ptr<CallCtx> ctx(static_cast<CallCtx*>(arg));
+  CallCtx* ctx = static_cast<CallCtx*>(arg);
+  std::unique_ptr<CallCtx> own(ctx->eager ? ctx : nullptr);
   mi_moe_hybrid* hh = ctx->hh;
-  hh->last_queue_ms.store(
-      std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - ctx->enqueued).count());
+  if (ctx->eager)
+    hh->last_queue_ms.store(
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - ctx->enqueued).count());
   try {
     run_host(hh, (const uint16_t*)hh->x_h.p, ctx->act, (const int32_t*)hh->ids_h.p, (const float*)hh->w_h.p,
              ctx->T, ctx->K, (float*)hh->part_h.p);
@@ -302,7 +328,12 @@ MI_API int mi_moe_hybrid_create(int64_t E, int64_t H, int64_t I, int quant_type,
        hipEventCreateWithFlags(&hh->ev_part, hipEventDisableTiming) != hipSuccess))
     return bail(hfail(MI_MOE_EHIP, "stream / event creation failed"));
   try {
-    hh->pool.reset(new mimoe_host::Pool(num_threads ? num_threads : default_threads()));
+    const int nt = num_threads ? num_threads : default_threads();
+    if (quant_type == MI_MOE_W4A16) hh->pool.reset(new mimoe_host::Pool(nt));
+    else if (hh->cold.Ec > 0) {
+      hh->qeng.reset(new mimoe_cpu::Engine(hh->cold.Ec, H, I, quant_type, nt, 1));
+      hh->qeng->set_split_max(nt);   // few cold experts per call: every host thread on them
+    }
   } catch (...) {
     return bail(hfail(MI_MOE_EINVAL, "host thread pool creation failed"));
   }
@@ -341,6 +372,15 @@ MI_API int mi_moe_hybrid_store_quantized(mi_moe_hybrid* hh, const void* gate_up_
   if (hh->dev) {
     rc = mi_moe_store_quantized(hh->dev, hot[0].p, hot[1].p, hot[2].p, hot[3].p, scale_dtype, 1, stream);
     if (rc) return rc;
+  }
+  if (hh->qeng) {   // the engine keeps its own packed copy; the wire bytes are not needed after
+    try {
+      hh->qeng->store(hh->cold.arr[0].data(), (const uint16_t*)hh->cold.arr[1].data(), hh->cold.arr[2].data(),
+                      (const uint16_t*)hh->cold.arr[3].data(), scale_dtype);
+    } catch (...) {
+      return hfail(MI_MOE_EINVAL, "out of host memory");
+    }
+    for (auto& v : hh->cold.arr) std::vector<uint8_t>().swap(v);
   }
   hh->cold.scale_dtype = scale_dtype;
   hh->loaded = true;
@@ -388,6 +428,15 @@ MI_API int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y, cons
   if (hh->cold.Ec == 0) return mi_moe_forward(hh->dev, x, y, topk_w, topk_ids, T, K, act_dtype, stream);
   hipStream_t st = (hipStream_t)stream;
   const int64_t n = T * K, H = hh->H;
+  // Under graph capture nothing may synchronize or allocate: the staging
+  // buffers (and the device handle's workspace) must already hold this call,
+  // i.e. a call of at least this size was made before the capture.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HCHK(hipStreamIsCapturing(st, &cap));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  if (capturing && (T > hh->cap_T || n > hh->cap_n))
+    return hfail(MI_MOE_EINVAL, "hybrid call of T=%lld, %lld pairs under graph capture needs larger staging buffers: "
+                 "make one call of this size before capturing", (long long)T, (long long)n);
   rc = grow(hh, T, n, st);
   if (rc) return rc;
   // inputs to the host buffers on the caller's stream (after the previous
@@ -403,13 +452,14 @@ MI_API int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y, cons
   HCHK(hipGetLastError());
   HCHK(hipEventRecord(hh->ev_in, st));
   HCHK(hipStreamWaitEvent(hh->side, hh->ev_in, 0));
-  CallCtx* ctx = new (std::nothrow) CallCtx{hh, T, K, act_dtype, std::chrono::steady_clock::now()};
+  CallCtx* ctx = new (std::nothrow) CallCtx{hh, T, K, act_dtype, std::chrono::steady_clock::now(), !capturing};
   if (!ctx) return hfail(MI_MOE_EINVAL, "out of host memory");
   hipError_t e = hipLaunchHostFunc(hh->side, host_callback, ctx);
   if (e != hipSuccess) {
     delete ctx;
     return hfail(MI_MOE_EHIP, "hipLaunchHostFunc failed: %s", hipGetErrorString(e));
   }
+  if (capturing) hh->graph_ctx.emplace_back(ctx);
   HCHK(hipEventRecord(hh->ev_part, hh->side));
   // caller stream: the hot experts on the device
   if (hh->dev) {
@@ -456,9 +506,10 @@ MI_API int mi_moe_hybrid_get_stats(mi_moe_hybrid* hh, int64_t* device_experts, i
   if (!hh) return hfail(MI_MOE_EINVAL, "null hybrid handle");
   if (device_experts) *device_experts = hh->Eg;
   if (host_experts) *host_experts = hh->cold.Ec;
-  if (host_weight_bytes) {
+  if (host_weight_bytes) {   // wire-format bytes of the cold experts once stored
     int64_t b = 0;
-    for (int a = 0; a < 6; ++a) b += (int64_t)hh->cold.arr[a].size();
+    for (int a = 0; hh->loaded && a < mimoe_host::num_arrays(hh->quant); ++a)
+      b += hh->cold.Ec * (int64_t)mimoe_host::expert_bytes(hh->quant, hh->H, hh->I, a);
     *host_weight_bytes = b;
   }
   if (last_host_ms) *last_host_ms = hh->last_host_ms.load();

@@ -129,3 +129,48 @@ def test_q_hybrid_parity(cuda, qt, T):
     x = _x(T, H, 411 + T)
     y = _fwd(hm, x, ids, tw, cuda)
     assert max_rel_err(y, _oracle_q(qt, x, ids, tw, ws, E, I)) <= TOL
+
+
+@pytest.mark.parametrize("kind", ["w4a16", "q8_0", "q4_0"])
+def test_hybrid_graph_replay_matches_eager(cuda, w4w, kind):
+    """Hybrid calls captured into a HIP graph (after one eager call of the
+    size, which sizes the staging buffers and the device workspace): the
+    device kernels, the staging kernel, the host callback node and the add
+    kernel replay bit-identical to the eager calls, with eager calls on the
+    same handle between the replays."""
+    if kind == "w4a16":
+        E, H, I = W4["E"], W4["H"], W4["I"]
+        hm = HybridMoE(E, H, I, nm.W4A16, host_experts=COLD, num_threads=4)
+        hm.store_awq(*w4w)
+    else:
+        qt = 0 if kind == "q8_0" else 1
+        E, H, I = Q["E"], Q["H"], Q["I"]
+        ws = _q_weights(qt, E, H, I, 420 + qt, torch.float16)
+        hm = HybridMoE(E, H, I, qt, host_experts=COLD, num_threads=4)
+        hm.store_quantized(torch.from_numpy(np.ascontiguousarray(ws[0])), ws[1],
+                           torch.from_numpy(np.ascontiguousarray(ws[2])), ws[3])
+    cases = []
+    for s, T in enumerate((6, 3)):
+        ids, tw = topk_routing(T, E, 8, seed=430 + s)
+        cases.append((_x(T, H, 440 + s).to(cuda), ids.to(cuda), tw.to(cuda)))
+    outs = [torch.empty(x.shape, dtype=torch.bfloat16, device=cuda) for x, _, _ in cases]
+    for (x, ids, tw), o in zip(cases, outs):
+        hm.forward(x, ids, tw, out=o)
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for (x, ids, tw), o in zip(cases, outs):
+            hm.forward(x, ids, tw, out=o)
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep}"
+        x, ids, tw = cases[rep % 2]
+        y = hm.forward(x, ids, tw)
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager[rep % 2])
+    del g
