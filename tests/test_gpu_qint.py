@@ -121,6 +121,31 @@ def test_gemm_path_tiles_and_invalid_ids(cuda, qt):
 
 
 @pytest.mark.parametrize("qt", [0, 1])
+def test_gemm_many_rows_per_expert(cuda, qt):
+    """Int8 GEMM row tiles of experts with 16 to 257 routed rows (a tile of
+    64 rows is followed by a ragged one of 6, 36, 1 or 1 rows; 64 + 64 exact),
+    ids outside [0, E), an expert absent."""
+    E, H, I, T, K = 8, 256, 128, 90, 8          # 720 pairs >= 64 * E
+    w = _weights(qt, E, H, I, seed=70 + qt, sdt=torch.bfloat16)
+    h = _handle(qt, E, H, I, w, True, cuda)
+    g = torch.Generator().manual_seed(71)
+    ids = torch.full((T, K), 7, dtype=torch.int32)   # expert 7 absent unless written below
+    flat = ids.view(-1)
+    order = torch.randperm(T * K, generator=g)
+    sizes = {0: 70, 1: 100, 2: 128, 3: 129, 4: 257, 5: 17, 6: 16}
+    pos = 0
+    for e, cnt in sizes.items():
+        flat[order[pos:pos + cnt]] = e
+        pos += cnt
+    flat[order[pos:]] = -1                       # dropped pairs
+    flat[order[pos]] = E + 5                     # out of range
+    tw = torch.softmax(torch.randn(T, K, generator=g), dim=-1)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(72)).to(torch.bfloat16)
+    y = _run(h, x, ids, tw, cuda)
+    assert max_rel_err(y, _oracle(qt, x, ids, tw, w, E, I)) <= TOL
+
+
+@pytest.mark.parametrize("qt", [0, 1])
 @pytest.mark.parametrize("bs", [1, 8, 64])   # 64: 512 pairs, the int8 grouped-GEMM path
 def test_qwen_shape(cuda, qt, bs):
     E, H, I = 128, 2048, 768
