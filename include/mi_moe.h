@@ -320,8 +320,12 @@ int mi_moe_hybrid_store_awq(mi_moe_hybrid* hh, const int32_t* w13_qweight,
  * the handle runs the cold experts in a stream host callback into a pinned
  * fp32 partial, which a device kernel then reads: y = round(y_hot + y_cold), with
  * y_hot already rounded to the activation dtype.  Calls that overlap on one handle race, as for
- * mi_moe_forward.  Growing the staging buffers synchronizes the streams, so
- * the call is not for graph capture. */
+ * mi_moe_forward.  Growing the staging buffers synchronizes the streams; a
+ * call can be captured into a HIP graph once a call of at least its size has
+ * been made (under capture a call that would grow returns MI_MOE_EINVAL), and
+ * the graph must not outlive the handle.  If a host pass fails (out of host
+ * memory) its partial is filled with NaN, so that call's y is NaN, and the
+ * next mi_moe_hybrid_forward on the handle returns MI_MOE_EDEVICE. */
 int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y,
                           const float* topk_w, const int32_t* topk_ids,
                           int64_t T, int64_t K, int act_dtype, void* stream);

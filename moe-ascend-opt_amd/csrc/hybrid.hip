@@ -214,8 +214,10 @@ void host_callback(void* arg) {
   try {
     run_host(hh, (const uint16_t*)hh->x_h.p, ctx->act, (const int32_t*)hh->ids_h.p, (const float*)hh->w_h.p,
              ctx->T, ctx->K, (float*)hh->part_h.p);
-  } catch (...) {
-    std::memset(hh->part_h.p, 0, sizeof(float) * (size_t)(ctx->T * hh->H));
+  } catch (...) {   // poison the partial: the call's y must not look valid
+    float* part = (float*)hh->part_h.p;
+    const float qnan = __builtin_nanf("");
+    for (int64_t i = 0; i < ctx->T * hh->H; ++i) part[i] = qnan;
     hh->host_error.store(1);
   }
 }
