@@ -145,6 +145,14 @@ double mi_moe_get_last_run_time_ms(mi_moe_handle* h);
 /* Enable (1) / disable (0) the per-call HIP-event timing (default 1). */
 int mi_moe_set_timing(mi_moe_handle* h, int enable);
 
+/* Grow the handle's device workspace to hold a call of T tokens at top_k K
+ * (synchronizes `stream` if it grows), so that later calls up to that size
+ * allocate nothing and can be captured into a HIP graph.  Replaces the buffer
+ * preallocation of MoEGraphContext's constructor
+ * (Int8-gemm/nanovllm_ops.cpp:160-201), which sizes the graph-mode op's
+ * staging for num_tokens x top_k. */
+int mi_moe_reserve(mi_moe_handle* h, int64_t T, int64_t K, void* stream);
+
 /* Per-launch-phase times of the last timed mi_moe_forward, in ms: W4A16
  * fills ms[0] = routing + gate_up (+SiLU) launch(es), ms[1] = down (+combine)
  * launch(es) and returns 2; the integer path returns 1 (whole call).

@@ -524,6 +524,14 @@ MI_API int mi_moe_get_info(const mi_moe_handle* h, int64_t* E, int64_t* H, int64
   return MI_MOE_OK;
 }
 
+MI_API int mi_moe_reserve(mi_moe_handle* h, int64_t T, int64_t K, void* stream) {
+  int rc = check_handle(h);
+  if (rc) return rc;
+  if (T < 0 || K < 1 || K > 64) return fail(MI_MOE_EINVAL, "bad T=%lld / top_k=%lld", (long long)T, (long long)K);
+  if (T * K > ((int64_t)1 << 24)) return fail(MI_MOE_EINVAL, "T*top_k too large");
+  return ensure_workspace(h, T, T * K, (hipStream_t)stream);
+}
+
 MI_API int mi_moe_set_timing(mi_moe_handle* h, int enable) {
   if (!h) return fail(MI_MOE_EINVAL, "null handle");
   h->timing = enable != 0;

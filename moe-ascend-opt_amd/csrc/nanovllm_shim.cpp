@@ -287,6 +287,49 @@ int scale_code(const at::Tensor& d) {
 
 }  // namespace
 
+// The graph-mode context of the reference's device op
+// (MoEGraphContext, Int8-gemm/nanovllm_ops.cpp:160-201): built for a number
+// of tokens, a top_k and an activation dtype (0 fp16, 1 bf16).  Here it
+// grows the handle's device workspace to that size up front, so calls of at
+// most num_tokens tokens at this top_k allocate nothing and can be captured
+// into a HIP graph.  Any top_k >= 1 is accepted (the reference: 1, 8, 10).
+struct MoEGraphContext : torch::CustomClassHolder {
+  int64_t num_tokens, top_k, dtype;
+  MoEGraphContext(const c10::intrusive_ptr<MoEInferHandle>& moe, int64_t T, int64_t K, int64_t dt)
+      : num_tokens(T), top_k(K), dtype(dt) {
+    TORCH_CHECK(T >= 0 && K >= 1, "MoEGraphContext: num_tokens >= 0 and top_k >= 1");
+    TORCH_CHECK(dt == 0 || dt == 1, "MoEGraphContext: dtype must be 0 (float16) or 1 (bfloat16)");
+    if (moe->h) check_status(mi_moe_reserve(moe->h, T, K, (void*)c10::hip::getCurrentHIPStream().stream()),
+                             "MoEGraphContext");
+  }
+};
+
+// The reference's callback report thread (NpuCallbackManager,
+// Int8-gemm/nanovllm_ops.cpp:38-138) serves its host-callback op; the device
+// op here needs none, so the class holds nothing (constructible, for callers
+// that create one).
+struct NpuCallbackManager : torch::CustomClassHolder {
+  NpuCallbackManager(int64_t, int64_t) {}
+};
+
+// moe_forward_npu_graph_out (Int8-gemm/nanovllm_ops.cpp:308-342,406): the
+// layer into `out` for the context's shape.
+void moe_forward_graph_out_impl(const at::Tensor& hidden, const at::Tensor& topk_ids, const at::Tensor& topk_w,
+                                const c10::intrusive_ptr<MoEInferHandle>& moe,
+                                const c10::intrusive_ptr<MoEGraphContext>& ctx, at::Tensor out) {
+  TORCH_CHECK(hidden.dim() == 2 && hidden.size(0) <= ctx->num_tokens,
+              "moe_forward_npu_graph_out: more tokens than the MoEGraphContext was built for");
+  TORCH_CHECK(topk_ids.dim() == 2 && topk_ids.size(1) == ctx->top_k,
+              "moe_forward_npu_graph_out: top_k differs from the MoEGraphContext's");
+  TORCH_CHECK((ctx->dtype == 1) == (hidden.scalar_type() == at::kBFloat16),
+              "moe_forward_npu_graph_out: hidden dtype differs from the MoEGraphContext's");
+  if (hidden.is_cuda()) {
+    forward_into(hidden, topk_ids, topk_w, moe, out);
+  } else {
+    moe_forward_out_cpu(hidden, topk_ids, topk_w, moe, out);
+  }
+}
+
 TORCH_LIBRARY_FRAGMENT(nanovllm, m) {
   m.class_<MoEInferHandle>("MoEInfer")
       .def(torch::init<int64_t, int64_t, int64_t, int64_t>())
@@ -429,6 +472,16 @@ TORCH_LIBRARY_FRAGMENT(nanovllm, m) {
   m.def("moe_forward_out(Tensor hidden, Tensor topk_ids, Tensor topk_w, "
         "__torch__.torch.classes.nanovllm.MoEInfer moe, Tensor(a!) out) -> ()");
   m.def("moe_topk_softmax(Tensor logits, int top_k, bool renormalize=True) -> (Tensor, Tensor)");
+  // the reference's device-op names (Int8-gemm/nanovllm_ops.cpp:393-407): the
+  // stream op is moe_forward, the graph op writes into out
+  m.class_<NpuCallbackManager>("NpuCallbackManager").def(torch::init<int64_t, int64_t>());
+  m.class_<MoEGraphContext>("MoEGraphContext")
+      .def(torch::init<const c10::intrusive_ptr<MoEInferHandle>&, int64_t, int64_t, int64_t>());
+  m.def("moe_forward_npu_stream(Tensor hidden, Tensor topk_ids, Tensor topk_w, "
+        "__torch__.torch.classes.nanovllm.MoEInfer moe) -> Tensor");
+  m.def("moe_forward_npu_graph_out(Tensor hidden, Tensor topk_ids, Tensor topk_w, "
+        "__torch__.torch.classes.nanovllm.MoEInfer moe, __torch__.torch.classes.nanovllm.MoEGraphContext ctx, "
+        "Tensor(a!) out) -> ()");
   m.def("moe_forward_logits(Tensor hidden, Tensor router_logits, int top_k, bool renormalize, "
         "__torch__.torch.classes.nanovllm.MoEInfer moe) -> Tensor");
 }
@@ -438,6 +491,8 @@ TORCH_LIBRARY_IMPL(nanovllm, CUDA, m) {
   m.impl("moe_forward_out", &moe_forward_out_hip);
   m.impl("moe_topk_softmax", &moe_topk_softmax_hip);
   m.impl("moe_forward_logits", &moe_forward_logits_hip);
+  m.impl("moe_forward_npu_stream", &moe_forward_hip);
+  m.impl("moe_forward_npu_graph_out", &moe_forward_graph_out_impl);
 }
 
 TORCH_LIBRARY_IMPL(nanovllm, CPU, m) {
@@ -445,4 +500,6 @@ TORCH_LIBRARY_IMPL(nanovllm, CPU, m) {
   m.impl("moe_forward_out", &moe_forward_out_cpu);
   m.impl("moe_topk_softmax", &moe_topk_softmax_cpu);
   m.impl("moe_forward_logits", &moe_forward_logits_cpu);
+  m.impl("moe_forward_npu_stream", &moe_forward_cpu);
+  m.impl("moe_forward_npu_graph_out", &moe_forward_graph_out_impl);
 }

@@ -35,7 +35,7 @@ C_SYMBOLS = (
     "mi_moe_last_error", "mi_moe_version", "mi_moe_create", "mi_moe_destroy",
     "mi_moe_get_info", "mi_moe_store_quantized", "mi_moe_quantize_and_store_expert",
     "mi_moe_store_awq", "mi_moe_forward", "mi_moe_forward_noalloc", "mi_moe_get_last_run_time_ms",
-    "mi_moe_set_timing", "mi_moe_quantize_act_q8_0", "mi_moe_route", "mi_moe_block_dots",
+    "mi_moe_set_timing", "mi_moe_reserve", "mi_moe_quantize_act_q8_0", "mi_moe_route", "mi_moe_block_dots",
     "mi_moe_block_dots_mfma",
     "mi_moe_get_last_phase_times_ms", "mi_moe_topk_softmax", "mi_moe_forward_logits",
     "mi_moe_hybrid_create", "mi_moe_hybrid_destroy", "mi_moe_hybrid_store_quantized",
@@ -89,6 +89,7 @@ def capi():
     L.mi_moe_get_last_run_time_ms.restype = ctypes.c_double
     L.mi_moe_get_last_run_time_ms.argtypes = [P]
     L.mi_moe_set_timing.argtypes = [P, I]
+    L.mi_moe_reserve.argtypes = [P, I64, I64, P]
     L.mi_moe_get_last_phase_times_ms.argtypes = [P, ctypes.POINTER(ctypes.c_double), I]
     L.mi_moe_quantize_act_q8_0.argtypes = [P, I, I64, I64, P, P, P]
     L.mi_moe_route.argtypes = [P, I64, I64, I64, P, P, P, P, P]

@@ -123,3 +123,34 @@ def test_cpu_key_argument_errors():
         torch.ops.nanovllm.moe_forward(torch.zeros(2, H + 32, dtype=torch.bfloat16), ids, w, h)
     with pytest.raises(RuntimeError, match="int32"):
         torch.ops.nanovllm.moe_forward(x, ids.long(), w, h)
+
+
+def test_reference_device_op_names_on_cpu():
+    """The reference's device-op names (Int8-gemm/nanovllm_ops.cpp:393-407):
+    moe_forward_npu_stream is moe_forward; moe_forward_npu_graph_out writes
+    into out for a MoEGraphContext(moe, num_tokens, top_k, dtype) and rejects
+    calls past the context's shape; NpuCallbackManager constructs."""
+    E, H, I, T, K = 8, 256, 128, 5, 8
+    ws = _q_weights(1, E, H, I, 95, torch.float16)
+    h = torch.classes.nanovllm.MoEInfer(E, H, I, 1)
+    h.store_quantized_repack(*[torch.from_numpy(np.ascontiguousarray(t)) if isinstance(t, np.ndarray) else t
+                               for t in ws])
+    torch.classes.nanovllm.NpuCallbackManager(0, 0)
+    ids, tw = topk_routing(T, E, K, seed=96)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(97)).to(torch.bfloat16)
+    y = torch.ops.nanovllm.moe_forward(x, ids, tw, h)
+    assert torch.equal(torch.ops.nanovllm.moe_forward_npu_stream(x, ids, tw, h), y)
+    ctx = torch.classes.nanovllm.MoEGraphContext(h, 8, K, 1)
+    out = torch.empty_like(x)
+    torch.ops.nanovllm.moe_forward_npu_graph_out(x, ids, tw, h, ctx, out)
+    assert torch.equal(out, y)
+    with pytest.raises(RuntimeError, match="more tokens"):
+        big = torch.zeros(9, H, dtype=torch.bfloat16)
+        torch.ops.nanovllm.moe_forward_npu_graph_out(big, torch.zeros(9, K, dtype=torch.int32),
+                                                     torch.zeros(9, K), h, ctx, torch.empty_like(big))
+    with pytest.raises(RuntimeError, match="top_k"):
+        torch.ops.nanovllm.moe_forward_npu_graph_out(x, ids[:, :4].contiguous(), tw[:, :4].contiguous(), h, ctx, out)
+    with pytest.raises(RuntimeError, match="dtype"):
+        torch.ops.nanovllm.moe_forward_npu_graph_out(x.half(), ids, tw, h, ctx, out.half())
+    with pytest.raises(RuntimeError, match="dtype must be"):
+        torch.classes.nanovllm.MoEGraphContext(h, 8, K, 2)

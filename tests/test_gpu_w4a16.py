@@ -265,3 +265,30 @@ def test_large_intermediate_parity(cuda, T, K):
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
     y = _run(h, x, ids, tw, cuda)
     assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, torch.bfloat16)) <= TOL
+
+
+def test_graph_context_capture_without_warmup(cuda):
+    """MoEGraphContext(moe, num_tokens, top_k, dtype) grows the workspace up
+    front (mi_moe_reserve): moe_forward_npu_graph_out captured on a fresh
+    handle with no eager call first replays bit-identical to eager calls."""
+    E, H, I, T, K = 8, 512, 256, 48, 8            # 384 pairs: the sorted path
+    w = w4a16_random(E, H, I, seed=600)
+    h = _handle(E, H, I, w, True, cuda)
+    ctx = torch.classes.nanovllm.MoEGraphContext(h, T, K, 1)
+    ids, tw = topk_routing(T, E, K, seed=601)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(602)).to(torch.bfloat16).to(cuda)
+    ids, tw = ids.to(cuda), tw.to(cuda)
+    out = torch.empty_like(x)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        torch.ops.nanovllm.moe_forward_npu_graph_out(x, ids, tw, h, ctx, out)
+    for rep in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        y = torch.ops.nanovllm.moe_forward_npu_stream(x, ids, tw, h)
+        torch.cuda.synchronize()
+        assert torch.equal(out, y), f"replay {rep}"
+    assert max_rel_err(out.cpu(), _oracle(x.cpu(), ids.cpu(), tw.cpu(), w, E, I, torch.bfloat16)) <= TOL
+    del g
