@@ -89,9 +89,10 @@ int mi_moe_quantize_and_store_expert(mi_moe_handle* h, int64_t expert,
 
 /* W4A16 AWQ-layout weights -> device layout.  No reference counterpart in
  * the checkout: the W4A16 grouped_gemv loader lives in the absent
- * sgl-kernel-npu submodule (README.md:19-30,152).  Layout: see formats.py /
- * INTEGRATION.md (w13_* [E,H,2I/8],[E,H/g,2I/8],[E,H/g,2I]; w2_* [E,I,H/8],
- * [E,I/g,H/8],[E,I/g,H]).  group must be 128. */
+ * sgl-kernel-npu submodule (README.md:19-30,152).  Layout (AWQ, as
+ * nanovllm_moe/formats.py writes it; nibble slot {0,4,1,5,2,6,3,7}[n%8] of
+ * each int32): w13_* [E,H,2I/8], [E,H/g,2I/8], [E,H/g,2I] with w13 = gate||up
+ * along N; w2_* [E,I,H/8], [E,I/g,H/8], [E,I/g,H].  group must be 128. */
 int mi_moe_store_awq(mi_moe_handle* h, const int32_t* w13_qweight,
                      const int32_t* w13_qzeros, const void* w13_scales,
                      const int32_t* w2_qweight, const int32_t* w2_qzeros,
