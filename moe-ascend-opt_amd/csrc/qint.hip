@@ -97,9 +97,10 @@ __device__ __forceinline__ int block_isum(const int (&wd)[8], const int* xv, int
 // Integer decode path (lane-per-row kernels): the NW waves of a workgroup
 // split K, and a wave's first batch of weight groups is issued before the
 // activations are staged.  NW = 8 for the smallest calls (kQDecWideMaxPairs
-// routed pairs or fewer: few workgroups, each wave's chain is shorter), 4
-// above (occupancy).
-constexpr int kQDecWideMaxPairs = 8;
+// routed pairs or fewer: few workgroups, each wave's chain is shorter; a
+// top-10 token is 10 pairs), 4 above (occupancy; 8 waves at 16 pairs measured
+// slower).
+constexpr int kQDecWideMaxPairs = 12;
 
 // One lane's row weights (whole 4-block layout groups, as 16-byte loads) and
 // the blocks' raw scale bits for up to NG_ groups (Q8_0: 32 VGPRs of weights
