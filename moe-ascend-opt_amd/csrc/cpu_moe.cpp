@@ -81,6 +81,11 @@ float f16_f32(uint16_t h) {
   if (e == 31) return bits_f32(s | 0x7f800000u | (m << 13));
   return bits_f32(s | ((e + 112u) << 23) | (m << 13));
 }
+template <class V>
+void grow(V& v, size_t n) {   // size at least n; existing contents need not survive
+  if (v.size() < n) v.resize(n);
+}
+
 float half_f32(uint16_t v, int dt) { return dt == 1 ? bits_f32((uint32_t)v << 16) : f16_f32(v); }
 
 uint16_t f32_bf16(float f) {
@@ -146,9 +151,187 @@ float quant_block(const float* v, int8_t* q) {
   return d;
 }
 
+// ---------------------------------------------------------------- row quantizers
+// Q8_0 of a hidden row (Stage A) and of SiLU(gate) * up (the intermediate),
+// with the biased bytes q ^ 0x80 and the int32 block sums the dot kernels
+// take.  The AVX2 + FMA forms do the scalar forms' operations lane by lane:
+// the same absolute maximum (NaN lanes ignored), d = amax / 127 and 1 / d,
+// RNE rounding (vroundps in place of nearbyintf), the exp's fma chain and
+// exponent scaling, the same division for the sigmoid -- so both write the
+// same bytes and scales.
+void finish_block(const int8_t* q, uint8_t* qb, int32_t* s) {
+  int32_t sum = 0;
+  for (int j = 0; j < 32; ++j) {
+    qb[j] = (uint8_t)(q[j] ^ 0x80);
+    sum += q[j];
+  }
+  *s = sum;
+}
+
+void quant_hidden_scalar(const uint16_t* x, int64_t n, int dt, int8_t* q, uint8_t* qb, float* d, int32_t* s) {
+  float v[32];
+  for (int64_t b = 0; b < n / 32; ++b) {
+    for (int j = 0; j < 32; ++j) v[j] = half_f32(x[32 * b + j], dt);
+    d[b] = quant_block(v, q + 32 * b);
+    finish_block(q + 32 * b, qb + 32 * b, s + b);
+  }
+}
+
+void quant_act_scalar(const float* gate, const float* up, int64_t n, int8_t* q, uint8_t* qb, float* d, int32_t* s) {
+  float v[32];
+  for (int64_t b = 0; b < n / 32; ++b) {
+    for (int j = 0; j < 32; ++j) {
+      const float g = gate[32 * b + j], u = up[32 * b + j];
+      const float eg = expf_cw(-g);
+      const float denom = 1.0f + eg;
+      const float sig = g / denom;
+      v[j] = u * sig;
+    }
+    d[b] = quant_block(v, q + 32 * b);
+    finish_block(q + 32 * b, qb + 32 * b, s + b);
+  }
+}
+
+#define MIMOE_AVX2 __attribute__((target("avx2,fma,f16c")))
+
+MIMOE_AVX2 inline __m256i round_q8(__m256 x, __m256 vid) {
+  const __m256 t = _mm256_mul_ps(x, vid);
+  __m256 r = _mm256_round_ps(t, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+  r = _mm256_andnot_ps(_mm256_cmp_ps(t, t, _CMP_UNORD_Q), r);   // NaN -> 0
+  r = _mm256_min_ps(_mm256_max_ps(r, _mm256_set1_ps(-128.0f)), _mm256_set1_ps(127.0f));
+  return _mm256_cvttps_epi32(r);
+}
+
+// one block of 32 values in x0..x3 (elements 0-7, 8-15, 16-23, 24-31)
+MIMOE_AVX2 inline void quant32_avx2(__m256 x0, __m256 x1, __m256 x2, __m256 x3, int8_t* q, uint8_t* qb, float* d,
+                                    int32_t* s) {
+  const __m256 mag = _mm256_castsi256_ps(_mm256_set1_epi32(0x7fffffff));
+  // max(|x|, m): a NaN in the first operand returns the second, so NaN lanes
+  // are skipped as in the scalar loop
+  __m256 m = _mm256_max_ps(_mm256_and_ps(x0, mag), _mm256_setzero_ps());
+  m = _mm256_max_ps(_mm256_and_ps(x1, mag), m);
+  m = _mm256_max_ps(_mm256_and_ps(x2, mag), m);
+  m = _mm256_max_ps(_mm256_and_ps(x3, mag), m);
+  __m128 h = _mm_max_ps(_mm256_castps256_ps128(m), _mm256_extractf128_ps(m, 1));
+  h = _mm_max_ps(h, _mm_movehl_ps(h, h));
+  h = _mm_max_ss(h, _mm_shuffle_ps(h, h, 1));
+  const float amax = _mm_cvtss_f32(h);
+  const float dd = amax / 127.0f, id = dd != 0.0f ? 1.0f / dd : 0.0f;
+  *d = dd;
+  const __m256 vid = _mm256_set1_ps(id);
+  const __m256i q0 = round_q8(x0, vid), q1 = round_q8(x1, vid), q2 = round_q8(x2, vid), q3 = round_q8(x3, vid);
+  __m256i t = _mm256_add_epi32(_mm256_add_epi32(q0, q1), _mm256_add_epi32(q2, q3));
+  __m128i t4 = _mm_add_epi32(_mm256_castsi256_si128(t), _mm256_extracti128_si256(t, 1));
+  t4 = _mm_add_epi32(t4, _mm_shuffle_epi32(t4, 0x4e));
+  t4 = _mm_add_epi32(t4, _mm_shuffle_epi32(t4, 0xb1));
+  *s = _mm_cvtsi128_si32(t4);
+  // packs work per 128-bit lane: 4-byte groups come out as q0 lo, q1 lo,
+  // q2 lo, q3 lo, q0 hi, ...; the permute restores element order
+  const __m256i p = _mm256_packs_epi16(_mm256_packs_epi32(q0, q1), _mm256_packs_epi32(q2, q3));
+  const __m256i o = _mm256_permutevar8x32_epi32(p, _mm256_setr_epi32(0, 4, 1, 5, 2, 6, 3, 7));
+  _mm256_storeu_si256(reinterpret_cast<__m256i*>(q), o);
+  _mm256_storeu_si256(reinterpret_cast<__m256i*>(qb), _mm256_xor_si256(o, _mm256_set1_epi8((char)0x80)));
+}
+
+MIMOE_AVX2 inline __m256 load_half8(const uint16_t* x, int dt) {
+  const __m128i h = _mm_loadu_si128(reinterpret_cast<const __m128i*>(x));
+  if (dt == 1) return _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(h), 16));
+  return _mm256_cvtph_ps(h);   // exact (NaN payloads aside, and NaN lanes quantize to 0)
+}
+
+MIMOE_AVX2 void quant_hidden_avx2(const uint16_t* x, int64_t n, int dt, int8_t* q, uint8_t* qb, float* d, int32_t* s) {
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const uint16_t* xb = x + 32 * b;
+    quant32_avx2(load_half8(xb, dt), load_half8(xb + 8, dt), load_half8(xb + 16, dt), load_half8(xb + 24, dt),
+                 q + 32 * b, qb + 32 * b, d + b, s + b);
+  }
+}
+
+// expf_cw on 8 lanes
+MIMOE_AVX2 inline __m256 expf_cw8(__m256 x) {
+  const __m256 xc = _mm256_min_ps(_mm256_max_ps(x, _mm256_set1_ps(-87.0f)), _mm256_set1_ps(88.5f));
+  const __m256 n = _mm256_round_ps(_mm256_mul_ps(xc, _mm256_set1_ps(1.44269504088896341f)),
+                                   _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+  __m256 r = _mm256_fnmadd_ps(n, _mm256_set1_ps(0.693359375f), xc);     // fmaf(-n, C1, x)
+  r = _mm256_fnmadd_ps(n, _mm256_set1_ps(-2.12194440e-4f), r);          // fmaf(-n, C2, r)
+  __m256 p = _mm256_set1_ps(1.98412698412698413e-4f);
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.38888888888888889e-3f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(8.33333333333333333e-3f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(4.16666666666666667e-2f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.66666666666666667e-1f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(0.5f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f));
+  p = _mm256_fmadd_ps(p, r, _mm256_set1_ps(1.0f));
+  __m256i ni = _mm256_cvttps_epi32(n);
+  const __m256i hi = _mm256_cmpgt_epi32(ni, _mm256_set1_epi32(127));
+  p = _mm256_blendv_ps(p, _mm256_mul_ps(p, _mm256_set1_ps(2.0f)), _mm256_castsi256_ps(hi));
+  ni = _mm256_add_epi32(ni, hi);   // hi = -1 where taken
+  const __m256i lo = _mm256_cmpgt_epi32(_mm256_set1_epi32(-126), ni);
+  p = _mm256_blendv_ps(p, _mm256_mul_ps(p, _mm256_set1_ps(bits_f32(0x00800000u))), _mm256_castsi256_ps(lo));
+  ni = _mm256_add_epi32(ni, _mm256_and_si256(lo, _mm256_set1_epi32(126)));
+  __m256 e = _mm256_mul_ps(p, _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_add_epi32(ni, _mm256_set1_epi32(127)), 23)));
+  e = _mm256_blendv_ps(e, _mm256_set1_ps(bits_f32(0x7f800000u)), _mm256_cmp_ps(x, _mm256_set1_ps(88.5f), _CMP_GT_OQ));
+  e = _mm256_blendv_ps(e, _mm256_setzero_ps(), _mm256_cmp_ps(x, _mm256_set1_ps(-87.0f), _CMP_LT_OQ));
+  return _mm256_blendv_ps(e, x, _mm256_cmp_ps(x, x, _CMP_UNORD_Q));
+}
+
+MIMOE_AVX2 inline __m256 silu_mul8(const float* gate, const float* up) {
+  const __m256 g = _mm256_loadu_ps(gate), u = _mm256_loadu_ps(up);
+  const __m256 eg = expf_cw8(_mm256_xor_ps(g, _mm256_set1_ps(-0.0f)));
+  const __m256 denom = _mm256_add_ps(_mm256_set1_ps(1.0f), eg);
+  return _mm256_mul_ps(u, _mm256_div_ps(g, denom));
+}
+
+MIMOE_AVX2 void quant_act_avx2(const float* gate, const float* up, int64_t n, int8_t* q, uint8_t* qb, float* d,
+                               int32_t* s) {
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const float* g = gate + 32 * b;
+    const float* u = up + 32 * b;
+    quant32_avx2(silu_mul8(g, u), silu_mul8(g + 8, u + 8), silu_mul8(g + 16, u + 16), silu_mul8(g + 24, u + 24),
+                 q + 32 * b, qb + 32 * b, d + b, s + b);
+  }
+}
+
+// acc[j] = acc[j] + w * row[j]: a product, then a sum (no fused multiply-add)
+MIMOE_AVX2 void axpy_avx2(float w, const float* row, float* acc, int64_t n) {
+  const __m256 vw = _mm256_set1_ps(w);
+  int64_t j = 0;
+  for (; j + 8 <= n; j += 8)
+    _mm256_storeu_ps(acc + j, _mm256_add_ps(_mm256_loadu_ps(acc + j), _mm256_mul_ps(vw, _mm256_loadu_ps(row + j))));
+  for (; j < n; ++j) {
+    const float prod = w * row[j];
+    acc[j] = acc[j] + prod;
+  }
+}
+
+#undef MIMOE_AVX2
+
+void axpy_row(bool simd, float w, const float* row, float* acc, int64_t n) {
+  if (simd) {
+    axpy_avx2(w, row, acc, n);
+    return;
+  }
+  for (int64_t j = 0; j < n; ++j) {
+    const float prod = w * row[j];
+    acc[j] = acc[j] + prod;
+  }
+}
+
 }  // namespace
 
 float half_to_f32(uint16_t v, int dt) { return half_f32(v, dt); }
+
+void quant_hidden_row(bool simd, const uint16_t* x, int64_t n, int dt, int8_t* q, uint8_t* qb, float* d,
+                      int32_t* s) {
+  if (simd) quant_hidden_avx2(x, n, dt, q, qb, d, s);
+  else quant_hidden_scalar(x, n, dt, q, qb, d, s);
+}
+
+void quant_act_row(bool simd, const float* gate, const float* up, int64_t n, int8_t* q, uint8_t* qb, float* d,
+                   int32_t* s) {
+  if (simd) quant_act_avx2(gate, up, n, q, qb, d, s);
+  else quant_act_scalar(gate, up, n, q, qb, d, s);
+}
 
 // ---------------------------------------------------------------- ISA
 Isa detect_isa() {
@@ -538,17 +721,7 @@ Topology host_topology(int max_threads) {
 
 // ---------------------------------------------------------------- pool
 NodePool::NodePool(const std::vector<int>& cpus) : cpus_(cpus) {
-  const int n = std::max(1, (int)cpus_.size());
-  for (int i = 1; i < n; ++i) th_.emplace_back([this, i] { pin(i); work(); });
-}
-
-NodePool::~NodePool() {
-  {
-    std::lock_guard<std::mutex> lk(m_);
-    stop_ = true;
-  }
-  cv_.notify_all();
-  for (auto& t : th_) t.join();
+  pool_.reset(new mimoe_pool::WorkerPool(std::max(1, (int)cpus_.size()), [this](int i) { pin(i); }));
 }
 
 void NodePool::pin(int i) {
@@ -557,42 +730,6 @@ void NodePool::pin(int i) {
   CPU_ZERO(&s);
   CPU_SET(cpus_[(size_t)i], &s);
   (void)pthread_setaffinity_np(pthread_self(), sizeof(s), &s);
-}
-
-void NodePool::run(int64_t n, const std::function<void(int64_t)>& f) {
-  if (n <= 0) return;
-  if (th_.empty() || n == 1) {
-    for (int64_t i = 0; i < n; ++i) f(i);
-    return;
-  }
-  std::unique_lock<std::mutex> lk(m_);
-  fn_ = &f;
-  n_ = n;
-  next_.store(0);
-  busy_ = (int)th_.size();
-  ++gen_;
-  lk.unlock();
-  cv_.notify_all();
-  for (int64_t i; (i = next_.fetch_add(1)) < n;) f(i);
-  lk.lock();
-  done_.wait(lk, [&] { return busy_ == 0; });
-  fn_ = nullptr;
-}
-
-void NodePool::work() {
-  uint64_t seen = 0;
-  for (;;) {
-    std::unique_lock<std::mutex> lk(m_);
-    cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
-    if (stop_) return;
-    seen = gen_;
-    const std::function<void(int64_t)>* f = fn_;
-    const int64_t n = n_;
-    lk.unlock();
-    for (int64_t i; (i = next_.fetch_add(1)) < n;) (*f)(i);
-    lk.lock();
-    if (--busy_ == 0) done_.notify_one();
-  }
 }
 
 // ---------------------------------------------------------------- engine
@@ -614,6 +751,7 @@ Engine::Engine(int64_t E, int64_t H, int64_t I, int qt, int max_threads, int tp)
   threads_ = 0;
   for (auto& p : pools_) threads_ += p->size();
   shards_.resize((size_t)tp_);
+  scratch_.resize((size_t)tp_);
 }
 
 Engine::~Engine() = default;
@@ -734,38 +872,41 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
       tasks.push_back({(int)e, std::min(kMBlock, counts[(size_t)e] - off), starts[(size_t)e] + off});
   const int64_t ntasks = (int64_t)tasks.size();
 
-  std::vector<float> part((size_t)(tp_ * T * H));
-  // per-token stages (Stage A, C1, C2) of a few tokens run on the calling
-  // thread: waking the pool costs more than the work
-  const bool few = T * H <= (int64_t)16 * 2048;
-  auto per_token = [&](NodePool& pool, const std::function<void(int64_t)>& f) {
-    if (few) {
-      for (int64_t t = 0; t < T; ++t) f(t);
+  // tokens with a routed pair: the only rows Stage A needs (a token with no
+  // valid id gets a zero row in Stage C1 without reading its hidden row)
+  std::vector<int32_t> live;
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t k = 0; k < K; ++k)
+      if (scat[(size_t)(t * K + k)] >= 0) {
+        live.push_back((int32_t)t);
+        break;
+      }
+  const int64_t nlive = (int64_t)live.size();
+  grow(part_, (size_t)(tp_ * T * H));
+  float* const part = part_.data();
+  const bool simd = isa_ != Isa::kScalar;
+  // per-token stages of a few tokens run on the calling thread: waking the
+  // pool costs more than the work
+  auto per_token = [&](NodePool& pool, int64_t n, const std::function<void(int64_t)>& f) {
+    if (n * H <= (int64_t)16 * 2048) {
+      for (int64_t i = 0; i < n; ++i) f(i);
     } else {
-      pool.run(T, f);
+      pool.run(n, f);
     }
   };
   auto run_shard = [&](int s) {
     NodePool& pool = *pools_[(size_t)s];
     const Shard& sh = shards_[(size_t)s];
+    Scratch& sc = scratch_[(size_t)s];
     // Stage A (Int8-gemm/q8_gemm.cpp:360-377), this shard's replica
-    std::vector<int8_t> xq((size_t)(T * H));
-    std::vector<uint8_t> xb((size_t)(T * H));
-    std::vector<float> xd((size_t)(T * HB));
-    std::vector<int32_t> xs((size_t)(T * HB));
-    per_token(pool, [&](int64_t t) {
-      float v[32];
-      for (int64_t b = 0; b < HB; ++b) {
-        for (int j = 0; j < 32; ++j) v[j] = half_f32(x[t * H + 32 * b + j], act_dtype);
-        int8_t* q = xq.data() + t * H + 32 * b;
-        xd[(size_t)(t * HB + b)] = quant_block(v, q);
-        int32_t sum = 0;
-        for (int j = 0; j < 32; ++j) {
-          xb[(size_t)(t * H + 32 * b + j)] = (uint8_t)(q[j] ^ 0x80);
-          sum += q[j];
-        }
-        xs[(size_t)(t * HB + b)] = sum;
-      }
+    grow(sc.xq, (size_t)(T * H));
+    grow(sc.xb, (size_t)(T * H));
+    grow(sc.xd, (size_t)(T * HB));
+    grow(sc.xs, (size_t)(T * HB));
+    per_token(pool, nlive, [&](int64_t i) {
+      const int64_t t = live[(size_t)i];
+      quant_hidden_row(simd, x + t * H, H, act_dtype, sc.xq.data() + t * H, sc.xb.data() + t * H,
+                       sc.xd.data() + t * HB, sc.xs.data() + t * HB);
     });
     // the task's rows gathered (pack_A_q8_0_from_quantized_indirect, Int8-gemm/gemm_kernels.cpp:427-464)
     auto gather = [&](const Task& tk, std::vector<int8_t>& a, std::vector<uint8_t>& ab, std::vector<float>& ad,
@@ -776,78 +917,78 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
       as.resize((size_t)(tk.count * HB));
       for (int m = 0; m < tk.count; ++m) {
         const int64_t t = tok[(size_t)(tk.start + m)];
-        memcpy(&a[(size_t)(m * H)], &xq[(size_t)(t * H)], (size_t)H);
-        memcpy(&ab[(size_t)(m * H)], &xb[(size_t)(t * H)], (size_t)H);
-        memcpy(&ad[(size_t)(m * HB)], &xd[(size_t)(t * HB)], sizeof(float) * (size_t)HB);
-        memcpy(&as[(size_t)(m * HB)], &xs[(size_t)(t * HB)], sizeof(int32_t) * (size_t)HB);
+        memcpy(&a[(size_t)(m * H)], &sc.xq[(size_t)(t * H)], (size_t)H);
+        memcpy(&ab[(size_t)(m * H)], &sc.xb[(size_t)(t * H)], (size_t)H);
+        memcpy(&ad[(size_t)(m * HB)], &sc.xd[(size_t)(t * HB)], sizeof(float) * (size_t)HB);
+        memcpy(&as[(size_t)(m * HB)], &sc.xs[(size_t)(t * HB)], sizeof(int32_t) * (size_t)HB);
       }
     };
-    // SiLU(gate) * up of a task's rows, then Q8_0 of the result
-    // (silu_and_mul, Int8-gemm/vec_simd.h:36-64; pack_A_q8_0, Int8-gemm/gemm_kernels.cpp:394-425)
-    auto activate = [&](int count, const float* inter, std::vector<int8_t>& a, std::vector<uint8_t>& ab,
-                        std::vector<float>& ad, std::vector<int32_t>& as) {
-      a.resize((size_t)(count * Ish));
-      ab.resize((size_t)(count * Ish));
-      ad.resize((size_t)(count * IB));
-      as.resize((size_t)(count * IB));
-      float v[32];
-      for (int m = 0; m < count; ++m)
-        for (int64_t b = 0; b < IB; ++b) {
-          for (int j = 0; j < 32; ++j) {
-            const float g = inter[m * 2 * Ish + 32 * b + j], up = inter[m * 2 * Ish + Ish + 32 * b + j];
-            const float eg = expf_cw(-g);
-            const float denom = 1.0f + eg;
-            const float sig = g / denom;
-            v[j] = up * sig;
-          }
-          int8_t* q = &a[(size_t)(m * Ish + 32 * b)];
-          ad[(size_t)(m * IB + b)] = quant_block(v, q);
-          int32_t sum = 0;
-          for (int j = 0; j < 32; ++j) {
-            ab[(size_t)(m * Ish + 32 * b + j)] = (uint8_t)(q[j] ^ 0x80);
-            sum += q[j];
-          }
-          as[(size_t)(m * IB + b)] = sum;
-        }
+    // gate_up outputs [total][2 * Ish], the intermediate's Q8_0 [total][Ish]
+    // (SiLU(gate) * up, Int8-gemm/vec_simd.h:36-64, then pack_A_q8_0,
+    // Int8-gemm/gemm_kernels.cpp:394-425), expert outputs [total][H]
+    grow(sc.inter, (size_t)(total * 2 * Ish));
+    grow(sc.aq, (size_t)(total * Ish));
+    grow(sc.ab, (size_t)(total * Ish));
+    grow(sc.ad, (size_t)(total * IB));
+    grow(sc.as, (size_t)(total * IB));
+    grow(sc.eout, (size_t)(total * H));
+    float* const inter = sc.inter.data();
+    float* const eout = sc.eout.data();
+    // activation of rows [start, start + count), intermediate columns [c0, c1)
+    auto activate = [&](const Task& tk, int64_t c0, int64_t c1) {
+      for (int m = 0; m < tk.count; ++m) {
+        const int64_t r = tk.start + m;
+        const float* in = inter + r * 2 * Ish;
+        quant_act_row(simd, in + c0, in + Ish + c0, c1 - c0, sc.aq.data() + r * Ish + c0, sc.ab.data() + r * Ish + c0,
+                      sc.ad.data() + r * IB + c0 / 32, sc.as.data() + r * IB + c0 / 32);
+      }
     };
-    std::vector<float> inter((size_t)(total * 2 * Ish)), eout((size_t)(total * H));
-    // with few tasks, P threads per task (the reference's 2-way split,
-    // Int8-gemm/q8_gemm.cpp:382-488: gate rows / up rows, then halves of the
-    // down rows; up to split_max_ parts of whole 16-row panels where set):
-    // every output row is computed the same way whatever the split
-    const int P = ntasks * 2 <= pool.size() ? std::max(2, std::min<int>(split_max_, pool.size() / (int)ntasks)) : 1;
-    auto part_rows = [&](int64_t N, int part, int64_t& a, int64_t& b) {
-      const int64_t panels = N / kNR;
-      a = panels * part / P * kNR;
-      b = panels * (part + 1) / P * kNR;
+    auto down_rows = [&](const Task& tk) {
+      return ARows{sc.aq.data() + (size_t)tk.start * Ish, sc.ab.data() + (size_t)tk.start * Ish,
+                   sc.ad.data() + (size_t)tk.start * IB, sc.as.data() + (size_t)tk.start * IB, Ish};
+    };
+    // P parts per task.  split_max_ 2 is the reference's rule
+    // (Int8-gemm/q8_gemm.cpp:379-591): two parts per task when
+    // tasks * 2 <= threads, else one.  A larger split_max_ cuts tasks into
+    // about 4 parts per thread in all (at most split_max_ and one Q8_0 block
+    // of intermediate columns each), which the dynamic hand-out balances.
+    // Part p of gate_up takes the intermediate columns [c0, c1) (whole Q8_0
+    // blocks): gate rows c0..c1 and up rows Ish + c0..c1, then activates and
+    // quantizes those columns for the task's rows, so each intermediate value
+    // is activated once.  Part p of down takes a range of whole 16-row panels.
+    // Every output row is computed the same way whatever the split.
+    int P = ntasks * 2 <= pool.size() ? 2 : 1;
+    if (split_max_ > 2) {
+      const int64_t want = (4 * (int64_t)pool.size() + ntasks - 1) / ntasks;
+      P = (int)std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(split_max_, Ish / 32)));
+    }
+    auto part_range = [&](int64_t units, int64_t unit, int part, int64_t& a, int64_t& b) {
+      a = units * part / P * unit;
+      b = units * (part + 1) / P * unit;
     };
     if (P >= 2) {
       pool.run(P * ntasks, [&](int64_t i) {
         const Task& tk = tasks[(size_t)(i / P)];
-        const int part = (int)(i % P);
+        int64_t c0, c1;
+        part_range(Ish / 32, 32, (int)(i % P), c0, c1);
+        if (c0 == c1) return;
         std::vector<int8_t> a;
         std::vector<uint8_t> ab;
         std::vector<float> ad;
         std::vector<int32_t> as;
         gather(tk, a, ab, ad, as);
         const ARows A{a.data(), ab.data(), ad.data(), as.data(), H};
-        int64_t n0, n1;
-        part_rows(2 * Ish, part, n0, n1);
-        gemm_rows(isa_, sh.w13[(size_t)tk.e], A, tk.count, n0, n1, inter.data() + (size_t)tk.start * 2 * Ish,
-                  2 * Ish);
+        float* in = inter + (size_t)tk.start * 2 * Ish;
+        gemm_rows(isa_, sh.w13[(size_t)tk.e], A, tk.count, c0, c1, in, 2 * Ish);
+        gemm_rows(isa_, sh.w13[(size_t)tk.e], A, tk.count, Ish + c0, Ish + c1, in, 2 * Ish);
+        activate(tk, c0, c1);
       });
       pool.run(P * ntasks, [&](int64_t i) {
         const Task& tk = tasks[(size_t)(i / P)];
-        const int part = (int)(i % P);
-        std::vector<int8_t> a;
-        std::vector<uint8_t> ab;
-        std::vector<float> ad;
-        std::vector<int32_t> as;
-        activate(tk.count, inter.data() + (size_t)tk.start * 2 * Ish, a, ab, ad, as);
-        const ARows A{a.data(), ab.data(), ad.data(), as.data(), Ish};
         int64_t h0, h1;
-        part_rows(H, part, h0, h1);
-        gemm_rows(isa_, sh.w2[(size_t)tk.e], A, tk.count, h0, h1, eout.data() + (size_t)tk.start * H, H);
+        part_range(H / kNR, kNR, (int)(i % P), h0, h1);
+        if (h0 == h1) return;
+        gemm_rows(isa_, sh.w2[(size_t)tk.e], down_rows(tk), tk.count, h0, h1, eout + (size_t)tk.start * H, H);
       });
     } else {
       pool.run(ntasks, [&](int64_t ti) {
@@ -858,29 +999,30 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
         std::vector<int32_t> as;
         gather(tk, a, ab, ad, as);
         const ARows A1{a.data(), ab.data(), ad.data(), as.data(), H};
-        float* in = inter.data() + (size_t)tk.start * 2 * Ish;
-        gemm_rows(isa_, sh.w13[(size_t)tk.e], A1, tk.count, 0, 2 * Ish, in, 2 * Ish);
-        activate(tk.count, in, a, ab, ad, as);
-        const ARows A2{a.data(), ab.data(), ad.data(), as.data(), Ish};
-        gemm_rows(isa_, sh.w2[(size_t)tk.e], A2, tk.count, 0, H, eout.data() + (size_t)tk.start * H, H);
+        gemm_rows(isa_, sh.w13[(size_t)tk.e], A1, tk.count, 0, 2 * Ish, inter + (size_t)tk.start * 2 * Ish, 2 * Ish);
+        activate(tk, 0, Ish);
+        gemm_rows(isa_, sh.w2[(size_t)tk.e], down_rows(tk), tk.count, 0, H, eout + (size_t)tk.start * H, H);
       });
     }
-    // Stage C1 (Int8-gemm/q8_gemm.cpp:593-613)
-    float* yp = part.data() + (size_t)s * T * H;
-    per_token(pool, [&](int64_t t) {
-      float* acc = yp + t * H;
-      for (int64_t j = 0; j < H; ++j) acc[j] = 0.0f;
+    // Stage C1 (Int8-gemm/q8_gemm.cpp:593-613), in column chunks of 512 when
+    // there are more than 16 routed rows to add
+    float* yp = part + (size_t)s * T * H;
+    const int64_t chunk = std::min<int64_t>(H, 512), nchunks = (H + chunk - 1) / chunk;
+    auto combine = [&](int64_t i) {
+      const int64_t t = i / nchunks, j0 = i % nchunks * chunk, n = std::min(chunk, H - j0);
+      float* acc = yp + t * H + j0;
+      for (int64_t j = 0; j < n; ++j) acc[j] = 0.0f;
       for (int64_t k = 0; k < K; ++k) {
         const int32_t src = scat[(size_t)(t * K + k)];
         if (src < 0) continue;
-        const float w = topk_w[t * K + k];
-        const float* row = eout.data() + (size_t)src * H;
-        for (int64_t j = 0; j < H; ++j) {
-          const float prod = w * row[j];
-          acc[j] = acc[j] + prod;
-        }
+        axpy_row(simd, topk_w[t * K + k], eout + (size_t)src * H + j0, acc, n);
       }
-    });
+    };
+    if (total <= 16) {
+      for (int64_t i = 0; i < T * nchunks; ++i) combine(i);
+    } else {
+      pool.run(T * nchunks, combine);
+    }
   };
   if (tp_ == 1) {
     run_shard(0);
@@ -894,7 +1036,7 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
     for (auto& th : launch) th.join();
   }
   // Stage C2 (Int8-gemm/q8_gemm.cpp:621-641): shard order, then the cast
-  per_token(*pools_[0], [&](int64_t t) {
+  per_token(*pools_[0], T, [&](int64_t t) {
     for (int64_t j = 0; j < H; ++j) {
       float acc = part[(size_t)(t * H + j)];
       for (int s = 1; s < tp_; ++s) acc = acc + part[(size_t)(s * T * H + t * H + j)];

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "worker_pool.hpp"
+
 #include <atomic>
 #include <condition_variable>
 #include <functional>
@@ -18,6 +20,13 @@ namespace mimoe_cpu {
 
 // fp16 (dt 0) / bf16 (dt 1) bits -> fp32, exact
 float half_to_f32(uint16_t v, int dt);
+
+// Q8_0 of n values (n % 32 == 0) into q, q ^ 0x80, block scales d and int32
+// block sums s: a hidden row of fp16 / bf16 bits (Stage A), or SiLU(gate) * up
+// (the intermediate).  simd picks the AVX2 + FMA form (same bytes and scales).
+void quant_hidden_row(bool simd, const uint16_t* x, int64_t n, int dt, int8_t* q, uint8_t* qb, float* d, int32_t* s);
+void quant_act_row(bool simd, const float* gate, const float* up, int64_t n, int8_t* q, uint8_t* qb, float* d,
+                   int32_t* s);
 
 enum class Isa : int { kScalar = 0, kAvx2 = 1, kAvxVnni = 2, kAvx512Vnni = 3 };
 Isa detect_isa();               // the widest form the host runs
@@ -52,25 +61,15 @@ Topology host_topology(int max_threads);
 class NodePool {
  public:
   explicit NodePool(const std::vector<int>& cpus);
-  ~NodePool();
   NodePool(const NodePool&) = delete;
   NodePool& operator=(const NodePool&) = delete;
-  int size() const { return (int)th_.size() + 1; }
-  void run(int64_t n, const std::function<void(int64_t)>& f);
+  int size() const { return pool_->size(); }
+  void run(int64_t n, const std::function<void(int64_t)>& f) { pool_->run(n, f); }
   void pin(int i);   // pin the calling thread to CPU i of the pool
 
  private:
-  void work();
   std::vector<int> cpus_;
-  std::vector<std::thread> th_;
-  std::mutex m_;
-  std::condition_variable cv_, done_;
-  const std::function<void(int64_t)>* fn_ = nullptr;
-  int64_t n_ = 0;
-  std::atomic<int64_t> next_{0};
-  int busy_ = 0;
-  uint64_t gen_ = 0;
-  bool stop_ = false;
+  std::unique_ptr<mimoe_pool::WorkerPool> pool_;
 };
 
 class Engine {
@@ -86,7 +85,8 @@ class Engine {
   // one projection (0 gate [I,H], 1 up [I,H], 2 down [H,I]) of expert e, fp32 values
   void quantize_and_store(int64_t e, int proj, const float* w);
   // y [T,H] in act_dtype; or, with y_f32, the fp32 sums before the cast
-  // (Stage C2 without its rounding) into y_f32 and y unused
+  // (Stage C2 without its rounding) into y_f32 and y unused.  One call at a
+  // time per engine (the call's buffers belong to the engine).
   int forward(const uint16_t* x, uint16_t* y, const float* topk_w, const int32_t* topk_ids, int64_t T, int64_t K,
               int act_dtype, float* y_f32 = nullptr);
   bool loaded() const { return loaded_; }
@@ -94,9 +94,9 @@ class Engine {
   int tp() const { return tp_; }
   Isa isa() const { return isa_; }
   void set_isa(Isa i) { isa_ = i; }
-  // Threads per task when there are fewer than half as many tasks as threads:
-  // 2 (default) is the reference's split; more parts of whole 16-row panels
-  // keep every thread busy when few experts are routed (same results).
+  // Largest number of parts a task is cut into: 2 (default) is the
+  // reference's split (two parts when tasks * 2 <= threads); more lets few
+  // routed experts keep every thread busy (same results).
   void set_split_max(int p) { split_max_ = p < 2 ? 2 : p; }
   double last_ms() const { return last_ms_; }
   const Topology& topology() const { return topo_; }
@@ -109,6 +109,15 @@ class Engine {
   struct Shard {
     std::vector<PackedMat> w13, w2;   // per expert: [gate shard | up shard] rows x H; H rows x shard
   };
+  // Per-shard buffers of a call, kept between calls (they only grow), so a
+  // call allocates no large blocks: Stage A rows, gate_up outputs, the
+  // intermediate's Q8_0, the expert outputs.
+  struct Scratch {
+    std::vector<int8_t> xq, aq;
+    std::vector<uint8_t> xb, ab;
+    std::vector<float> xd, ad, inter, eout;
+    std::vector<int32_t> xs, as;
+  };
   int64_t E_, H_, I_;
   int qt_;
   Isa isa_;
@@ -116,6 +125,8 @@ class Engine {
   int tp_ = 1, threads_ = 1;
   std::vector<std::unique_ptr<NodePool>> pools_;
   std::vector<Shard> shards_;
+  std::vector<Scratch> scratch_;
+  std::vector<float> part_;   // [tp][T][H] shard partials
   bool loaded_ = false;
   int split_max_ = 2;
   double last_ms_ = -1.0;

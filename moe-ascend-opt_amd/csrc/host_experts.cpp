@@ -12,57 +12,6 @@
 
 namespace mimoe_host {
 
-// ---------------------------------------------------------------- pool
-Pool::Pool(int nthreads) {
-  if (nthreads < 1) nthreads = 1;
-  for (int i = 1; i < nthreads; ++i) th_.emplace_back([this] { work(); });
-}
-
-Pool::~Pool() {
-  {
-    std::lock_guard<std::mutex> lk(m_);
-    stop_ = true;
-  }
-  cv_.notify_all();
-  for (auto& t : th_) t.join();
-}
-
-void Pool::run(int64_t n, const std::function<void(int64_t)>& f) {
-  if (n <= 0) return;
-  if (th_.empty() || n == 1) {
-    for (int64_t i = 0; i < n; ++i) f(i);
-    return;
-  }
-  std::unique_lock<std::mutex> lk(m_);
-  fn_ = &f;
-  n_ = n;
-  next_.store(0);
-  busy_ = (int)th_.size();
-  ++gen_;
-  lk.unlock();
-  cv_.notify_all();
-  for (int64_t i; (i = next_.fetch_add(1)) < n;) f(i);
-  lk.lock();
-  done_.wait(lk, [&] { return busy_ == 0; });   // every worker has left this generation
-  fn_ = nullptr;
-}
-
-void Pool::work() {
-  uint64_t seen = 0;
-  for (;;) {
-    std::unique_lock<std::mutex> lk(m_);
-    cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
-    if (stop_) return;
-    seen = gen_;
-    const std::function<void(int64_t)>* f = fn_;
-    const int64_t n = n_;
-    lk.unlock();
-    for (int64_t i; (i = next_.fetch_add(1)) < n;) (*f)(i);
-    lk.lock();
-    if (--busy_ == 0) done_.notify_one();
-  }
-}
-
 // ---------------------------------------------------------------- formats
 int num_arrays(int quant) { return quant == 2 ? 6 : 4; }
 

@@ -14,6 +14,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "worker_pool.hpp"
+
 #include <atomic>
 #include <condition_variable>
 #include <functional>
@@ -26,27 +28,7 @@ namespace mimoe_host {
 // A fixed set of worker threads.  run(n, f) calls f(i) for every i in [0, n)
 // on the workers and the calling thread and returns when all calls are done.
 // One run at a time per pool.
-class Pool {
- public:
-  explicit Pool(int nthreads);
-  ~Pool();
-  Pool(const Pool&) = delete;
-  Pool& operator=(const Pool&) = delete;
-  int size() const { return (int)th_.size() + 1; }
-  void run(int64_t n, const std::function<void(int64_t)>& f);
-
- private:
-  void work();
-  std::vector<std::thread> th_;
-  std::mutex m_;
-  std::condition_variable cv_, done_;
-  const std::function<void(int64_t)>* fn_ = nullptr;
-  int64_t n_ = 0;
-  std::atomic<int64_t> next_{0};
-  int busy_ = 0;
-  uint64_t gen_ = 0;
-  bool stop_ = false;
-};
+using Pool = mimoe_pool::WorkerPool;
 
 // Number of weight arrays of a format (Q8_0 / Q4_0: gate_up_qs, gate_up_d,
 // down_qs, down_d; W4A16: w13_q, w13_z, w13_s, w2_q, w2_z, w2_s) and the

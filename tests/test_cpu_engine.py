@@ -90,6 +90,47 @@ def test_engine_bit_exact_vs_oracle(qt, T, K, threads, tp):
         L.mi_moe_cpu_destroy(c)
 
 
+@pytest.mark.parametrize("qt", [0, 1])
+@pytest.mark.parametrize("adt", [torch.bfloat16, torch.float16])
+def test_engine_special_values_bit_exact(qt, adt):
+    """Hidden rows with NaN, +-inf, signed zeros, subnormals, a zero block and
+    values at the dtype's range, and gate_up outputs far beyond exp's range
+    (weight scales x 2000, so SiLU sees |gate| in the hundreds): every
+    instruction set's Stage A and SiLU + Q8_0 of the intermediate give the
+    oracle's bits (NaN compared as NaN)."""
+    E, H, I, T, K = 10, 256, 128, 6, 8
+    gu_qs, gu_d, dn_qs, dn_d = _q_weights(qt, E, H, I, 70 + qt, torch.float16)
+    gu_d = (gu_d.float() * 2000).to(torch.float16)
+    ws = (gu_qs, gu_d, dn_qs, dn_d)
+    ids, tw = topk_routing(T, E, K, seed=71)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(72)).to(adt)
+    big = torch.finfo(adt).max
+    tiny = torch.finfo(adt).smallest_normal / 4          # a subnormal of the dtype
+    x[1, 5] = float("nan")
+    x[1, 40] = float("nan")
+    x[2, 64] = float("inf")
+    x[2, 200] = -float("inf")
+    x[3, :32] = 0.0                                     # a zero block: d = 0
+    x[3, 32:64] = -0.0
+    x[3, 64:96] = tiny
+    x[3, 100] = -tiny
+    x[4, ::7] = big
+    x[4, 3::11] = -big
+    x[5, 128:160] = torch.linspace(-3, 3, 32).to(adt) * 1e-3
+    L, c, _keep = _engine(qt, E, H, I, ws, 4, 1, torch.float16)
+    try:
+        ref = _oracle(qt, x, ids, tw, ws, E, I, 1)
+        ref_nan = np.isnan(from_bits(ref, adt).float().numpy())
+        for isa in _isas(L, c):
+            nm.check(L.mi_moe_cpu_set_isa(c, isa), "set_isa")
+            y = _forward(L, c, x, ids, tw)
+            y_nan = torch.isnan(y.float()).numpy()
+            assert np.array_equal(y_nan, ref_nan), L.mi_moe_cpu_isa_name(isa)
+            assert np.array_equal(bits(y)[~y_nan], ref[~ref_nan]), L.mi_moe_cpu_isa_name(isa)
+    finally:
+        L.mi_moe_cpu_destroy(c)
+
+
 def test_engine_online_quant_matches_wire_store():
     """quantize_and_store_expert on host (fp32 / fp16 / bf16 weights) gives the
     bytes of the oracle's quantize_weight_only restatement: the same layer
