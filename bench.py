@@ -561,7 +561,7 @@ def run_offload(steps, warmup, ncold=16, threads=0, quant=2):
     print(json.dumps({"workload": f"hybrid CPU-offload {fmt_name} layer, Qwen3-30B-A3B shape (H=2048, I=768, "
                                   f"E=128, top-8), {ncold} experts on the host", "unit": "us per call",
                       "timing": "wall clock around synchronized eager calls; graph = one HIP graph of 8 calls",
-                      "host_threads": threads or "default (hardware threads, at most 16)",
+                      "host_threads": threads or "default (affinity CPUs but one, at most 16)",
                       "device_experts": st0["device_experts"], "host_experts": st0["host_experts"],
                       "host_weight_bytes": st0["host_weight_bytes"], "per_bs": per}), flush=True)
 

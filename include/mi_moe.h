@@ -300,7 +300,8 @@ const char* mi_moe_cpu_isa_name(int isa);
  * mi_moe_hybrid_forward). */
 typedef struct mi_moe_hybrid mi_moe_hybrid;
 
-/* num_threads host threads (0: the hardware threads, at most 16).  Shape rules
+/* num_threads host threads (0: the CPUs of the affinity mask but one, at most
+ * 16; the calling thread counts as one of them).  Shape rules
  * as mi_moe_create.  Without a HIP device only an all-cold handle can be made
  * (usable through mi_moe_hybrid_host_forward). */
 int mi_moe_hybrid_create(int64_t num_experts, int64_t hidden, int64_t intermediate,
