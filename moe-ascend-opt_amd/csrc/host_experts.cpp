@@ -218,13 +218,16 @@ void awq_group(int nww, const int32_t* q, int64_t NW, int64_t k0, const float* c
 // scales [K/128][N]) against P fp32 rows xf[p] [K] with group sums xs[p]
 // [K/128]: out[p][n] = sum_g s * (sum_k x_k q_kn - z * xs_g).  j1 - j0 is
 // 2, 4, 8 or 16 words.
-void awq_cols(const int32_t* q, const int32_t* z, const uint16_t* s, int sdt, int64_t K, int64_t N, int64_t j0,
-              int64_t j1, const float* const* xf, const float* const* xs, int64_t P, float* const* out) {
+// qb points at word j0 of k row 0 and k rows are qstride words apart (N / 8
+// in the wire layout, 16 in the block-major copy).
+void awq_cols(const int32_t* qb, int64_t qstride, const int32_t* z, const uint16_t* s, int sdt, int64_t K,
+              int64_t N, int64_t j0, int64_t j1, const float* const* xf, const float* const* xs, int64_t P,
+              float* const* out) {
   const int64_t NW = N / 8, G = K / 128, nw = j1 - j0, nc = nw * 8;
   // acc / accg / sf / zf in slot-major order: index sl*nw + (j - j0)
   std::vector<float> acc((size_t)(P * nc), 0.0f), accg((size_t)(P * nc)), sf((size_t)nc), zf((size_t)nc);
   for (int64_t g = 0; g < G; ++g) {
-    awq_group((int)nw, q + j0, NW, 128 * g, xf, P, accg.data());
+    awq_group((int)nw, qb, qstride, 128 * g, xf, P, accg.data());
     for (int64_t j = j0; j < j1; ++j) {
       const uint32_t u = (uint32_t)z[g * NW + j];
       for (int sl = 0; sl < 8; ++sl) {
@@ -247,7 +250,141 @@ void awq_cols(const int32_t* q, const int32_t* z, const uint16_t* s, int sdt, in
 
 float silu_mul(float g, float u) { return u * (g / (1.0f + expf(-g))); }
 
+// ---------------------------------------------------------------- W4A16 gate_up, AVX512-BF16
+// With bf16 hidden rows, gate_up runs on vdpbf16ps: lane i of a 64-column
+// block accumulates column 4i + s (slot s = 0..3) over k pairs,
+//   acc += w(2kp + 1) * x(2kp + 1), then acc += w(2kp) * x(2kp)
+// (bf16 x small-integer products are exact in fp32; the instruction treats
+// bf16 denormal inputs as zero).  A k-pair word's slot s, shifted down by 4s,
+// indexes a 32-entry bf16 table of 0..15 (vpermw reads 5 index bits; entries
+// 16..31 repeat 0..15, so the neighbouring nibble's low bit does not matter).
+const bool kHostBf16 = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+                       __builtin_cpu_supports("avx512bf16");
+
+#define MIMOE_BF16 __attribute__((target("avx512f,avx512bw,avx512bf16")))
+
+template <int PC>
+MIMOE_BF16 __attribute__((always_inline)) inline void pair_group_pc(const uint32_t* __restrict__ q, int64_t kp0,
+                                                                    const uint16_t* const* xp,
+                                                                    float* __restrict__ accg) {
+  alignas(64) static const uint16_t tab16[32] = {
+      0x0000, 0x3f80, 0x4000, 0x4040, 0x4080, 0x40a0, 0x40c0, 0x40e0, 0x4100, 0x4110, 0x4120,
+      0x4130, 0x4140, 0x4150, 0x4160, 0x4170, 0x0000, 0x3f80, 0x4000, 0x4040, 0x4080, 0x40a0,
+      0x40c0, 0x40e0, 0x4100, 0x4110, 0x4120, 0x4130, 0x4140, 0x4150, 0x4160, 0x4170};
+  const __m512i tab = _mm512_load_si512(tab16);
+  __m512 acc[PC][4];
+  for (int pp = 0; pp < PC; ++pp)
+    for (int sl = 0; sl < 4; ++sl) acc[pp][sl] = _mm512_setzero_ps();
+  for (int64_t kp = kp0; kp < kp0 + 64; ++kp) {
+    const __m512i w = _mm512_loadu_si512(reinterpret_cast<const void*>(q + 16 * kp));
+    __m512i xv[PC];
+    for (int pp = 0; pp < PC; ++pp) {
+      int32_t x2;   // x[2kp] in the low half, x[2kp + 1] in the high half
+      memcpy(&x2, xp[pp] + 2 * kp, 4);
+      xv[pp] = _mm512_set1_epi32(x2);
+    }
+#pragma GCC unroll 4
+    for (int sl = 0; sl < 4; ++sl) {
+      const __m512i idx = sl == 0 ? w : _mm512_srli_epi32(w, 4 * sl);
+      const __m512i v = _mm512_permutexvar_epi16(idx, tab);
+      for (int pp = 0; pp < PC; ++pp)
+        acc[pp][sl] = _mm512_dpbf16_ps(acc[pp][sl], (__m512bh)v, (__m512bh)xv[pp]);
+    }
+  }
+  for (int pp = 0; pp < PC; ++pp)
+    for (int sl = 0; sl < 4; ++sl) _mm512_storeu_ps(accg + (pp * 4 + sl) * 16, acc[pp][sl]);
+}
+
+// Columns [64b, 64b + 64) of the k-pair gate_up matrix of one expert against
+// P bf16 rows xp[p] with fp32 group sums xs[p]:
+// out[p][n] = sum_g s * (sum_k x_k q_kn - z * xs_g), as awq_cols.
+MIMOE_BF16 void pair_cols(const uint32_t* pq, const uint8_t* pz, const uint16_t* ps, int sdt, int64_t K, int64_t N,
+                          int64_t b, const uint16_t* const* xp, const float* const* xs, int64_t P,
+                          float* const* out) {
+  const int64_t G = K / 128;
+  std::vector<float> acc((size_t)(P * 64), 0.0f), accg((size_t)(P * 64));
+  const uint32_t* q = pq + b * (K / 2) * 16;
+  for (int64_t g = 0; g < G; ++g) {
+    int64_t p = 0;
+    for (; p + 2 <= P; p += 2) pair_group_pc<2>(q, 64 * g, xp + p, accg.data() + p * 64);
+    if (p < P) pair_group_pc<1>(q, 64 * g, xp + p, accg.data() + p * 64);
+    const uint8_t* zg = pz + g * N + 64 * b;
+    const uint16_t* sg = ps + g * N + 64 * b;
+    for (int sl = 0; sl < 4; ++sl) {
+      const __m512 zf = _mm512_cvtepi32_ps(_mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(zg + 16 * sl))));
+      const __m256i sb = _mm256_loadu_si256(reinterpret_cast<const __m256i*>(sg + 16 * sl));
+      const __m512 sf = sdt == 1 ? _mm512_castsi512_ps(_mm512_slli_epi32(_mm512_cvtepu16_epi32(sb), 16))
+                                 : _mm512_cvtph_ps(sb);
+      for (int64_t pp = 0; pp < P; ++pp) {
+        float* a = acc.data() + pp * 64 + 16 * sl;
+        const __m512 gsum = _mm512_loadu_ps(accg.data() + pp * 64 + 16 * sl);
+        const __m512 t = _mm512_sub_ps(gsum, _mm512_mul_ps(zf, _mm512_set1_ps(xs[pp][g])));
+        _mm512_storeu_ps(a, _mm512_add_ps(_mm512_loadu_ps(a), _mm512_mul_ps(sf, t)));
+      }
+    }
+  }
+  for (int64_t pp = 0; pp < P; ++pp)
+    for (int sl = 0; sl < 4; ++sl)
+      for (int i = 0; i < 16; ++i) out[pp][64 * b + 4 * i + sl] = acc[(size_t)(pp * 64 + 16 * sl + i)];
+}
+
+#undef MIMOE_BF16
+
 }  // namespace
+
+void prepare_host_layouts(ColdSet& cs) {
+  const int64_t H = cs.H, I = cs.I, N = 2 * I, NW = N / 8, G = H / 128, Ec = cs.Ec;
+  cs.bq13.clear();
+  cs.bq2.clear();
+  cs.pq.clear();
+  cs.pz.clear();
+  cs.ps.clear();
+  if (cs.quant != 2 || Ec == 0 || H % 128 != 0 || I % 128 != 0) return;
+  // block-major copies of the two qweight arrays: [Ec][N/128][K][16]
+  auto block_major = [&](std::vector<int32_t>& dst, int a, int64_t K, int64_t Nn) {
+    dst.assign((size_t)(Ec * K * (Nn / 8)), 0);
+    for (int64_t c = 0; c < Ec; ++c) {
+      const int32_t* src = reinterpret_cast<const int32_t*>(cs.arr[a].data() + c * expert_bytes(2, H, I, a));
+      for (int64_t b = 0; b < Nn / 128; ++b)
+        for (int64_t k = 0; k < K; ++k)
+          memcpy(&dst[(size_t)(((c * (Nn / 128) + b) * K + k) * 16)], src + k * (Nn / 8) + 16 * b, 64);
+    }
+  };
+  block_major(cs.bq13, 0, H, N);
+  block_major(cs.bq2, 3, I, H);
+  if (!kHostBf16) return;
+  cs.pq.assign((size_t)(Ec * (H / 2) * (N / 4)), 0u);
+  cs.pz.assign((size_t)(Ec * G * N), 0);
+  cs.ps.assign((size_t)(Ec * G * N), 0);
+  // slot of column offset o within an AWQ word (kAwqOrder inverted)
+  int slot_of[8];
+  for (int sl = 0; sl < 8; ++sl) slot_of[kAwqOrder[sl]] = sl;
+  for (int64_t c = 0; c < Ec; ++c) {
+    const int32_t* q = reinterpret_cast<const int32_t*>(cs.arr[0].data() + c * expert_bytes(2, H, cs.I, 0));
+    const int32_t* z = reinterpret_cast<const int32_t*>(cs.arr[1].data() + c * expert_bytes(2, H, cs.I, 1));
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(cs.arr[2].data() + c * expert_bytes(2, H, cs.I, 2));
+    auto nib = [&](const int32_t* m, int64_t row, int64_t n) {
+      return ((uint32_t)m[row * NW + n / 8] >> (4 * slot_of[n % 8])) & 15u;
+    };
+    uint32_t* pq = cs.pq.data() + c * (H / 2) * (N / 4);
+    for (int64_t b = 0; b < N / 64; ++b)
+      for (int64_t kp = 0; kp < H / 2; ++kp)
+        for (int64_t i = 0; i < 16; ++i) {
+          uint32_t v = 0;
+          for (int s = 0; s < 4; ++s) {
+            const int64_t n = 64 * b + 4 * i + s;
+            v |= nib(q, 2 * kp, n) << (4 * s) | nib(q, 2 * kp + 1, n) << (16 + 4 * s);
+          }
+          pq[(b * (H / 2) + kp) * 16 + i] = v;
+        }
+    for (int64_t g = 0; g < G; ++g)
+      for (int64_t n = 0; n < N; ++n) {
+        const int64_t b = n / 64, i = (n % 64) / 4, s = n % 4, at = (c * G + g) * N + 64 * b + 16 * s + i;
+        cs.pz[(size_t)at] = (uint8_t)nib(z, g, n);
+        cs.ps[(size_t)at] = sc[g * N + n];
+      }
+  }
+}
 
 int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype, const int32_t* ids,
                 const float* topk_w, int64_t T, int64_t K, float* y_part) {
@@ -320,14 +457,31 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
     for (int64_t c = 0; c < Ec; ++c)
       if (start[c + 1] > start[c]) task_c.push_back(c);
     const int64_t nc = (int64_t)task_c.size();
+    // with the block-major copies, whole 16-word blocks (one contiguous run each)
+    const bool blocked = awq && !cs.bq13.empty();
     int aw = kAwqWordsMax;
-    while (aw > 2 && nc * ((N13 / 8) / aw) < 2 * (int64_t)pool.size()) aw /= 2;
+    while (!blocked && aw > 2 && nc * ((N13 / 8) / aw) < 2 * (int64_t)pool.size()) aw /= 2;
+    auto qblock = [&](const std::vector<int32_t>& bq, int a, int64_t c, int64_t K, int64_t N, int64_t b) {
+      return blocked ? bq.data() + ((c * (N / 128) + b) * K) * 16
+                     : reinterpret_cast<const int32_t*>(cs.arr[a].data() + c * eb[a]) + b * aw;
+    };
     const int64_t blk13 = awq ? (N13 / 8) / aw : N13 / kQRows;
     const int64_t blk2 = awq ? (H / 8) / aw : H / kQRows;
-    pool.run(nc * blk13, [&](int64_t task) {
+    // bf16 hidden rows and a k-pair copy: 64-column tasks on vdpbf16ps
+    const bool pairs = awq && act_dtype == 1 && !cs.pq.empty();
+    std::vector<const uint16_t*> pxp(pairs ? (size_t)P : 0);
+    for (int64_t p = 0; pairs && p < P; ++p) pxp[p] = x + (t0 + pair_of[p] / K) * H;
+    const int64_t blkp = N13 / 64;
+    if (pairs) {
+      pool.run(nc * blkp, [&](int64_t task) {
+        const int64_t c = task_c[task / blkp], b = task % blkp, p0 = start[c], np = start[c + 1] - p0;
+        pair_cols(cs.pq.data() + c * (H / 2) * (N13 / 4), cs.pz.data() + c * G1 * N13, cs.ps.data() + c * G1 * N13,
+                  cs.scale_dtype, H, N13, b, &pxp[p0], &pxs[p0], np, &pgu[p0]);
+      });
+    } else pool.run(nc * blk13, [&](int64_t task) {
       const int64_t c = task_c[task / blk13], b = task % blk13, p0 = start[c], np = start[c + 1] - p0;
       if (awq) {
-        awq_cols(reinterpret_cast<const int32_t*>(cs.arr[0].data() + c * eb[0]),
+        awq_cols(qblock(cs.bq13, 0, c, H, N13, b), blocked ? 16 : N13 / 8,
                  reinterpret_cast<const int32_t*>(cs.arr[1].data() + c * eb[1]),
                  reinterpret_cast<const uint16_t*>(cs.arr[2].data() + c * eb[2]), cs.scale_dtype, H, N13,
                  b * aw, (b + 1) * aw, &pxf[p0], &pxs[p0], np, &pgu[p0]);
@@ -372,7 +526,7 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
     pool.run(nc * blk2, [&](int64_t task) {
       const int64_t c = task_c[task / blk2], b = task % blk2, p0 = start[c], np = start[c + 1] - p0;
       if (awq) {
-        awq_cols(reinterpret_cast<const int32_t*>(cs.arr[3].data() + c * eb[3]),
+        awq_cols(qblock(cs.bq2, 3, c, I, H, b), blocked ? 16 : H / 8,
                  reinterpret_cast<const int32_t*>(cs.arr[4].data() + c * eb[4]),
                  reinterpret_cast<const uint16_t*>(cs.arr[5].data() + c * eb[5]), cs.scale_dtype, I, H,
                  b * aw, (b + 1) * aw, &pxf[p0], &pxs[p0], np, &pout[p0]);

@@ -44,7 +44,27 @@ struct ColdSet {
   int64_t E = 0, H = 0, I = 0, Ec = 0;
   std::vector<int32_t> cold_of;   // [E]: cold index of expert e, or -1
   std::vector<uint8_t> arr[6];
+  // W4A16 (prepare_host_layouts; empty unless H % 128 == I % 128 == 0):
+  // the qweight arrays again in 128-column blocks, each block's k rows one
+  // contiguous run of 64-byte rows, bq13 [Ec][2I/128][H][16] and
+  // bq2 [Ec][H/128][I][16] words, so that a task streams one run.
+  std::vector<int32_t> bq13, bq2;
+  // And gate_up in the k-pair order of the AVX512-BF16 kernel (also empty
+  // when the host lacks the instructions):
+  //   pq [Ec][2I/64][H/2][16] u32 (64-column blocks, each one contiguous
+  //      run): word (b, kp, i) holds, for s = 0..3, the nibble of
+  //      (k = 2kp, n = 64b + 4i + s) at bits 4s and of (k = 2kp + 1, same n)
+  //      at bits 16 + 4s;
+  //   pz [Ec][H/128][2I] zero nibbles and ps [Ec][H/128][2I] scale bits, in
+  //      lane order: column n = 64b + 4i + s at index 64b + 16s + i.
+  std::vector<uint32_t> pq;
+  std::vector<uint8_t> pz;
+  std::vector<uint16_t> ps;
 };
+
+// Fills the block-major and k-pair copies of a W4A16 ColdSet (arr stored);
+// a no-op for other formats.
+void prepare_host_layouts(ColdSet& cs);
 
 // y_part [T,H] fp32: per token, the sum over k in ascending order of
 // topk_w[t,k] * expert(x[t]) over the pairs whose id is a cold expert (rows

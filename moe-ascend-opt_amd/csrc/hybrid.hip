@@ -421,6 +421,11 @@ MI_API int mi_moe_hybrid_store_awq(mi_moe_hybrid* hh, const int32_t* w13_qweight
     if (rc) return rc;
   }
   hh->cold.scale_dtype = scale_dtype;
+  try {
+    mimoe_host::prepare_host_layouts(hh->cold);
+  } catch (...) {
+    return hfail(MI_MOE_EINVAL, "out of host memory");
+  }
   hh->loaded = true;
   return MI_MOE_OK;
 }
