@@ -292,6 +292,34 @@ MIMOE_AVX2 void quant_act_avx2(const float* gate, const float* up, int64_t n, in
   }
 }
 
+MIMOE_AVX2 void silu_mul_avx2(const float* gate, const float* up, int64_t n, float* out) {
+  int64_t j = 0;
+  for (; j + 8 <= n; j += 8) _mm256_storeu_ps(out + j, silu_mul8(gate + j, up + j));
+  for (; j < n; ++j) out[j] = up[j] * (gate[j] / (1.0f + expf_cw(-gate[j])));
+}
+
+// sums of 128-element groups: 8 lanes of 16 elements each (lane l takes
+// elements l, l + 8, ...), then the lanes in a fixed tree
+MIMOE_AVX2 void group_sums_avx2(const float* a, int64_t ngroups, float* sums) {
+  for (int64_t g = 0; g < ngroups; ++g) {
+    const float* v = a + 128 * g;
+    __m256 t[4];
+    for (int i = 0; i < 4; ++i) t[i] = _mm256_loadu_ps(v + 8 * i);
+    for (int i = 4; i < 16; ++i) t[i & 3] = _mm256_add_ps(t[i & 3], _mm256_loadu_ps(v + 8 * i));
+    const __m256 u = _mm256_add_ps(_mm256_add_ps(t[0], t[1]), _mm256_add_ps(t[2], t[3]));
+    __m128 h = _mm_add_ps(_mm256_castps256_ps128(u), _mm256_extractf128_ps(u, 1));
+    h = _mm_add_ps(h, _mm_movehl_ps(h, h));
+    h = _mm_add_ss(h, _mm_shuffle_ps(h, h, 1));
+    sums[g] = _mm_cvtss_f32(h);
+  }
+}
+
+MIMOE_AVX2 void half_to_f32_avx2(const uint16_t* x, int64_t n, int dt, float* out) {
+  int64_t j = 0;
+  for (; j + 8 <= n; j += 8) _mm256_storeu_ps(out + j, load_half8(x + j, dt));
+  for (; j < n; ++j) out[j] = half_f32(x[j], dt);
+}
+
 // acc[j] = acc[j] + w * row[j]: a product, then a sum (no fused multiply-add)
 MIMOE_AVX2 void axpy_avx2(float w, const float* row, float* acc, int64_t n) {
   const __m256 vw = _mm256_set1_ps(w);
@@ -331,6 +359,50 @@ void quant_act_row(bool simd, const float* gate, const float* up, int64_t n, int
                    int32_t* s) {
   if (simd) quant_act_avx2(gate, up, n, q, qb, d, s);
   else quant_act_scalar(gate, up, n, q, qb, d, s);
+}
+
+bool host_simd() {
+  static const bool ok = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") &&
+                         __builtin_cpu_supports("f16c");
+  return ok;
+}
+
+void silu_mul_row(const float* gate, const float* up, int64_t n, float* out) {
+  if (host_simd()) {
+    silu_mul_avx2(gate, up, n, out);
+    return;
+  }
+  for (int64_t j = 0; j < n; ++j) {
+    const float g = gate[j];
+    out[j] = up[j] * (g / (1.0f + expf_cw(-g)));
+  }
+}
+
+void group_sums_128(const float* a, int64_t ngroups, float* sums) {
+  if (host_simd()) {
+    group_sums_avx2(a, ngroups, sums);
+    return;
+  }
+  for (int64_t g = 0; g < ngroups; ++g) {   // the same lanes and tree as the AVX2 form
+    float lane[8];
+    for (int l = 0; l < 8; ++l) {
+      float t[4];
+      for (int i = 0; i < 4; ++i) t[i] = a[128 * g + 8 * i + l];
+      for (int i = 4; i < 16; ++i) t[i & 3] = t[i & 3] + a[128 * g + 8 * i + l];
+      lane[l] = (t[0] + t[1]) + (t[2] + t[3]);
+    }
+    float h[4];
+    for (int l = 0; l < 4; ++l) h[l] = lane[l] + lane[l + 4];
+    sums[g] = (h[0] + h[2]) + (h[1] + h[3]);
+  }
+}
+
+void half_row_to_f32(const uint16_t* x, int64_t n, int dt, float* out) {
+  if (host_simd()) {
+    half_to_f32_avx2(x, n, dt, out);
+    return;
+  }
+  for (int64_t j = 0; j < n; ++j) out[j] = half_f32(x[j], dt);
 }
 
 // ---------------------------------------------------------------- ISA

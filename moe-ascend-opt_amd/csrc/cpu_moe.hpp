@@ -28,6 +28,15 @@ void quant_hidden_row(bool simd, const uint16_t* x, int64_t n, int dt, int8_t* q
 void quant_act_row(bool simd, const float* gate, const float* up, int64_t n, int8_t* q, uint8_t* qb, float* d,
                    int32_t* s);
 
+// Row helpers of the W4A16 host executor, AVX2 + FMA where the host has it
+// (the scalar forms give the same bits): out = up * SiLU(gate) with the exp
+// of the device code; sums of 128-element groups (a fixed lane tree);
+// fp16 / bf16 bits -> fp32.
+bool host_simd();
+void silu_mul_row(const float* gate, const float* up, int64_t n, float* out);
+void group_sums_128(const float* a, int64_t ngroups, float* sums);
+void half_row_to_f32(const uint16_t* x, int64_t n, int dt, float* out);
+
 enum class Isa : int { kScalar = 0, kAvx2 = 1, kAvxVnni = 2, kAvx512Vnni = 3 };
 Isa detect_isa();               // the widest form the host runs
 bool isa_supported(Isa i);

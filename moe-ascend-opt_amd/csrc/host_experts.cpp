@@ -4,6 +4,8 @@
 // one thread, for all the routed rows of its expert.
 #include "host_experts.hpp"
 
+#include "cpu_moe.hpp"
+
 #include <immintrin.h>
 #include <math.h>
 #include <string.h>
@@ -248,8 +250,6 @@ void awq_cols(const int32_t* qb, int64_t qstride, const int32_t* z, const uint16
       for (int sl = 0; sl < 8; ++sl) out[p][8 * j + kAwqOrder[sl]] = acc[p * nc + sl * nw + (j - j0)];
 }
 
-float silu_mul(float g, float u) { return u * (g / (1.0f + expf(-g))); }
-
 // ---------------------------------------------------------------- W4A16 gate_up, AVX512-BF16
 // With bf16 hidden rows, gate_up runs on vdpbf16ps: lane i of a 64-column
 // block accumulates column 4i + s (slot s = 0..3) over k pairs,
@@ -418,9 +418,17 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
         pair_of[pos] = i;
         pos_of[i] = pos;
       }
-    // activations of the block's tokens
+    // per-pair and per-token stages of a few rows run on the calling thread
+    // (waking the pool costs more than the work)
+    auto small_run = [&](int64_t n, const std::function<void(int64_t)>& f) {
+      if (n <= 16) {
+        for (int64_t i = 0; i < n; ++i) f(i);
+      } else {
+        pool.run(n, f);
+      }
+    };
+    // activations of the block's tokens (W4A16: with their 128-k group sums)
     std::vector<float> xf((size_t)(nT * H));
-    for (int64_t i = 0; i < nT * H; ++i) xf[i] = half_f32(x[t0 * H + i], act_dtype);
     std::vector<float> gu((size_t)(P * N13)), out((size_t)(P * H));
     std::vector<const float*> pxf((size_t)P), pxs((size_t)P);
     std::vector<const int8_t*> paq((size_t)P);
@@ -430,15 +438,12 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
     std::vector<int8_t> xq, aq;
     std::vector<float> xd, ad;
     const int64_t G1 = H / 128, G2 = I / 128;
-    if (awq) {
-      xs.resize((size_t)(nT * G1));
-      for (int64_t t = 0; t < nT; ++t)
-        for (int64_t g = 0; g < G1; ++g) {
-          float sum = 0.0f;
-          for (int64_t k = 0; k < 128; ++k) sum += xf[t * H + 128 * g + k];
-          xs[t * G1 + g] = sum;
-        }
-    } else {
+    if (awq) xs.resize((size_t)(nT * G1));
+    small_run(nT, [&](int64_t t) {
+      mimoe_cpu::half_row_to_f32(x + (t0 + t) * H, H, act_dtype, &xf[t * H]);
+      if (awq) mimoe_cpu::group_sums_128(&xf[t * H], G1, &xs[t * G1]);
+    });
+    if (!awq) {
       xq.resize((size_t)(nT * H));
       xd.resize((size_t)(nT * (H / 32)));
       pool.run(nT, [&](int64_t t) { quant_q8_0(&xf[t * H], H, &xq[t * H], &xd[t * (H / 32)]); });
@@ -495,25 +500,12 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
     act.resize((size_t)(P * I));
     if (awq) xs.assign((size_t)(P * G2), 0.0f);
     else { aq.resize((size_t)(P * I)); ad.resize((size_t)(P * (I / 32))); }
-    // per-pair and per-token stages of a few rows run on the calling thread
-    // (waking the pool costs more than the work)
-    auto small_run = [&](int64_t n, const std::function<void(int64_t)>& f) {
-      if (n <= 16) {
-        for (int64_t i = 0; i < n; ++i) f(i);
-      } else {
-        pool.run(n, f);
-      }
-    };
     small_run(P, [&](int64_t p) {
       float* a = &act[p * I];
       const float* g = &gu[p * N13];
-      for (int64_t j = 0; j < I; ++j) a[j] = silu_mul(g[j], g[I + j]);
+      mimoe_cpu::silu_mul_row(g, g + I, I, a);
       if (awq) {
-        for (int64_t gg = 0; gg < G2; ++gg) {
-          float sum = 0.0f;
-          for (int64_t k = 0; k < 128; ++k) sum += a[128 * gg + k];
-          xs[p * G2 + gg] = sum;
-        }
+        mimoe_cpu::group_sums_128(a, G2, &xs[p * G2]);
       } else {
         quant_q8_0(a, I, &aq[p * I], &ad[p * (I / 32)]);
       }
