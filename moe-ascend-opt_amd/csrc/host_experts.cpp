@@ -44,7 +44,7 @@ namespace {
 
 constexpr int kTokBlock = 256;    // tokens per pass (bounds the per-pair buffers)
 constexpr int kQRows = 32;        // output rows per Q task
-constexpr int kAwqWordsMax = 16;  // packed words (128 columns) per W4A16 task, at most
+constexpr int kAwqWords = 16;     // packed words (128 columns) per W4A16 task
 constexpr int kAwqOrder[8] = {0, 2, 4, 6, 1, 3, 5, 7};   // nibble slot s -> column 8j + order[s]
 
 float bits_f32(uint32_t u) {
@@ -330,29 +330,8 @@ MIMOE_BF16 void pair_cols(const uint32_t* pq, const uint8_t* pz, const uint16_t*
 
 #undef MIMOE_BF16
 
-}  // namespace
-
-void prepare_host_layouts(ColdSet& cs) {
+void prepare_pairs(ColdSet& cs) {
   const int64_t H = cs.H, I = cs.I, N = 2 * I, NW = N / 8, G = H / 128, Ec = cs.Ec;
-  cs.bq13.clear();
-  cs.bq2.clear();
-  cs.pq.clear();
-  cs.pz.clear();
-  cs.ps.clear();
-  if (cs.quant != 2 || Ec == 0 || H % 128 != 0 || I % 128 != 0) return;
-  // block-major copies of the two qweight arrays: [Ec][N/128][K][16]
-  auto block_major = [&](std::vector<int32_t>& dst, int a, int64_t K, int64_t Nn) {
-    dst.assign((size_t)(Ec * K * (Nn / 8)), 0);
-    for (int64_t c = 0; c < Ec; ++c) {
-      const int32_t* src = reinterpret_cast<const int32_t*>(cs.arr[a].data() + c * expert_bytes(2, H, I, a));
-      for (int64_t b = 0; b < Nn / 128; ++b)
-        for (int64_t k = 0; k < K; ++k)
-          memcpy(&dst[(size_t)(((c * (Nn / 128) + b) * K + k) * 16)], src + k * (Nn / 8) + 16 * b, 64);
-    }
-  };
-  block_major(cs.bq13, 0, H, N);
-  block_major(cs.bq2, 3, I, H);
-  if (!kHostBf16) return;
   cs.pq.assign((size_t)(Ec * (H / 2) * (N / 4)), 0u);
   cs.pz.assign((size_t)(Ec * G * N), 0);
   cs.ps.assign((size_t)(Ec * G * N), 0);
@@ -384,6 +363,34 @@ void prepare_host_layouts(ColdSet& cs) {
         cs.ps[(size_t)at] = sc[g * N + n];
       }
   }
+}
+
+}  // namespace
+
+void prepare_host_layouts(ColdSet& cs) {
+  const int64_t H = cs.H, I = cs.I, N = 2 * I, Ec = cs.Ec;
+  cs.bq13.clear();
+  cs.bq2.clear();
+  cs.pq.clear();
+  cs.pz.clear();
+  cs.ps.clear();
+  if (cs.quant != 2 || Ec == 0 || H % 128 != 0 || I % 128 != 0) return;
+  // block-major copies of the two qweight arrays: [Ec][N/128][K][16]
+  auto block_major = [&](std::vector<int32_t>& dst, int a, int64_t K, int64_t Nn) {
+    dst.assign((size_t)(Ec * K * (Nn / 8)), 0);
+    for (int64_t c = 0; c < Ec; ++c) {
+      const int32_t* src = reinterpret_cast<const int32_t*>(cs.arr[a].data() + c * expert_bytes(2, H, I, a));
+      for (int64_t b = 0; b < Nn / 128; ++b)
+        for (int64_t k = 0; k < K; ++k)
+          memcpy(&dst[(size_t)(((c * (Nn / 128) + b) * K + k) * 16)], src + k * (Nn / 8) + 16 * b, 64);
+    }
+  };
+  block_major(cs.bq13, 0, H, N);
+  block_major(cs.bq2, 3, I, H);
+  if (kHostBf16) prepare_pairs(cs);
+  // the wire qweights are not read again (zeros and scales still are)
+  std::vector<uint8_t>().swap(cs.arr[0]);
+  std::vector<uint8_t>().swap(cs.arr[3]);
 }
 
 int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype, const int32_t* ids,
@@ -456,20 +463,17 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
       pgu[p] = &gu[p * N13];
       pout[p] = &out[p * H];
     }
-    // gate_up: tasks of (cold expert with pairs, row block); W4A16 blocks of
-    // aw packed words, the widest that still gives every thread 2 tasks
+    // tasks of (cold expert with pairs, block of output columns / rows):
+    // W4A16 blocks of 128 columns, each one contiguous run of the
+    // block-major copy (64 columns on the k-pair copy)
     std::vector<int64_t> task_c;
     for (int64_t c = 0; c < Ec; ++c)
       if (start[c + 1] > start[c]) task_c.push_back(c);
     const int64_t nc = (int64_t)task_c.size();
-    // with the block-major copies, whole 16-word blocks (one contiguous run each)
-    const bool blocked = awq && !cs.bq13.empty();
-    int aw = kAwqWordsMax;
-    while (!blocked && aw > 2 && nc * ((N13 / 8) / aw) < 2 * (int64_t)pool.size()) aw /= 2;
-    auto qblock = [&](const std::vector<int32_t>& bq, int a, int64_t c, int64_t K, int64_t N, int64_t b) {
-      return blocked ? bq.data() + ((c * (N / 128) + b) * K) * 16
-                     : reinterpret_cast<const int32_t*>(cs.arr[a].data() + c * eb[a]) + b * aw;
+    auto qblock = [&](const std::vector<int32_t>& bq, int64_t c, int64_t K, int64_t N, int64_t b) {
+      return bq.data() + ((c * (N / 128) + b) * K) * 16;
     };
+    const int aw = kAwqWords;
     const int64_t blk13 = awq ? (N13 / 8) / aw : N13 / kQRows;
     const int64_t blk2 = awq ? (H / 8) / aw : H / kQRows;
     // bf16 hidden rows and a k-pair copy: 64-column tasks on vdpbf16ps
@@ -486,7 +490,7 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
     } else pool.run(nc * blk13, [&](int64_t task) {
       const int64_t c = task_c[task / blk13], b = task % blk13, p0 = start[c], np = start[c + 1] - p0;
       if (awq) {
-        awq_cols(qblock(cs.bq13, 0, c, H, N13, b), blocked ? 16 : N13 / 8,
+        awq_cols(qblock(cs.bq13, c, H, N13, b), 16,
                  reinterpret_cast<const int32_t*>(cs.arr[1].data() + c * eb[1]),
                  reinterpret_cast<const uint16_t*>(cs.arr[2].data() + c * eb[2]), cs.scale_dtype, H, N13,
                  b * aw, (b + 1) * aw, &pxf[p0], &pxs[p0], np, &pgu[p0]);
@@ -518,7 +522,7 @@ int64_t forward(const ColdSet& cs, Pool& pool, const uint16_t* x, int act_dtype,
     pool.run(nc * blk2, [&](int64_t task) {
       const int64_t c = task_c[task / blk2], b = task % blk2, p0 = start[c], np = start[c + 1] - p0;
       if (awq) {
-        awq_cols(qblock(cs.bq2, 3, c, I, H, b), blocked ? 16 : H / 8,
+        awq_cols(qblock(cs.bq2, c, I, H, b), 16,
                  reinterpret_cast<const int32_t*>(cs.arr[4].data() + c * eb[4]),
                  reinterpret_cast<const uint16_t*>(cs.arr[5].data() + c * eb[5]), cs.scale_dtype, I, H,
                  b * aw, (b + 1) * aw, &pxf[p0], &pxs[p0], np, &pout[p0]);

@@ -171,9 +171,9 @@ def test_hybrid_stats_host_bytes():
 
 
 def test_w4a16_task_widths_bit_identical():
-    """One cold expert: the W4A16 column blocks narrow from 16 packed words
-    (1 thread) to 4 (4 threads) and 2 (16 threads) so every thread has work;
-    each output column is summed in the same order at every width."""
+    """One cold expert on 1, 4 and 16 threads: the column-block tasks are
+    handed out dynamically, and each output column is summed in the same order
+    whichever thread takes its block, so the outputs are bit-identical."""
     E, H, I, T, K = 4, 512, 128, 5, 2
     ws = w4a16_random(E, H, I, seed=70)
     ids = torch.tensor([[2, 0], [1, 2], [2, 3], [0, 1], [3, 2]], dtype=torch.int32)
