@@ -37,7 +37,8 @@ int num_arrays(int quant);
 size_t expert_bytes(int quant, int64_t H, int64_t I, int idx);
 
 // Wire-format weights of the cold experts: arr[a] holds array a of cold
-// expert c at c * expert_bytes(quant, H, I, a).
+// expert c at c * expert_bytes(quant, H, I, a) (W4A16: the two qweight
+// arrays are released once prepare_host_layouts has copied them).
 struct ColdSet {
   int quant = 0;        // 0 Q8_0, 1 Q4_0, 2 W4A16 (group 128)
   int scale_dtype = 0;  // 0 fp16, 1 bf16
@@ -62,8 +63,9 @@ struct ColdSet {
   std::vector<uint16_t> ps;
 };
 
-// Fills the block-major and k-pair copies of a W4A16 ColdSet (arr stored);
-// a no-op for other formats.
+// Fills the block-major and k-pair copies of a W4A16 ColdSet from its wire
+// arrays (all six stored), then releases arr[0] and arr[3]; a no-op for
+// other formats.
 void prepare_host_layouts(ColdSet& cs);
 
 // y_part [T,H] fp32: per token, the sum over k in ascending order of
