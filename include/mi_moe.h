@@ -270,7 +270,9 @@ int mi_moe_cpu_quantize_and_store_expert(mi_moe_cpu* c, int64_t expert, int proj
 /* The fused layer on host memory: arguments as mi_moe_forward (ids outside
  * [0,E) dropped; a token with no valid id gets zeros).  Replaces
  * MoEInfer::execute_on_cpu_routed_from_pointers (Int8-gemm/moe_infer.cpp:
- * 430-456); wall time of the call in mi_moe_cpu_get_info's last_ms. */
+ * 430-456); wall time of the call in mi_moe_cpu_get_info's last_ms.  Calls
+ * on one handle run one at a time (its buffers and thread pools are shared;
+ * the reference's process-wide pool, moe_common.cpp:57-111, is not locked). */
 int mi_moe_cpu_forward(mi_moe_cpu* c, const void* x, void* y, const float* topk_w,
                        const int32_t* topk_ids, int64_t T, int64_t K, int act_dtype);
 

@@ -912,6 +912,7 @@ void Engine::quantize_and_store(int64_t e, int proj, const float* w) {
 
 int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const int32_t* topk_ids, int64_t T,
                     int64_t K, int act_dtype, float* y_f32) {
+  std::lock_guard<std::mutex> lk(call_mu_);
   const auto t0 = std::chrono::steady_clock::now();
   const int64_t E = E_, H = H_, Ish = I_ / tp_, HB = H / 32, IB = Ish / 32;
   // routing: stable counting sort by expert (Int8-gemm/moe_common.cpp:146-216)

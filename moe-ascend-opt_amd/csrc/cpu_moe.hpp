@@ -94,8 +94,8 @@ class Engine {
   // one projection (0 gate [I,H], 1 up [I,H], 2 down [H,I]) of expert e, fp32 values
   void quantize_and_store(int64_t e, int proj, const float* w);
   // y [T,H] in act_dtype; or, with y_f32, the fp32 sums before the cast
-  // (Stage C2 without its rounding) into y_f32 and y unused.  One call at a
-  // time per engine (the call's buffers belong to the engine).
+  // (Stage C2 without its rounding) into y_f32 and y unused.  Calls on one
+  // engine run one at a time (its buffers and pools are shared).
   int forward(const uint16_t* x, uint16_t* y, const float* topk_w, const int32_t* topk_ids, int64_t T, int64_t K,
               int act_dtype, float* y_f32 = nullptr);
   bool loaded() const { return loaded_; }
@@ -136,6 +136,7 @@ class Engine {
   std::vector<Shard> shards_;
   std::vector<Scratch> scratch_;
   std::vector<float> part_;   // [tp][T][H] shard partials
+  std::mutex call_mu_;        // forward calls, one at a time
   bool loaded_ = false;
   int split_max_ = 2;
   double last_ms_ = -1.0;
