@@ -103,11 +103,11 @@ __device__ __forceinline__ uint64_t bits_range(int lo, int count) {
   return m << lo;
 }
 
-// scale bits -> fp32 (sdt: 1 bf16, 0 fp16), without a branch
-__device__ __forceinline__ float scale_f32(uint32_t bits, int sdt) {
-  const uint32_t b = __float_as_uint(bf16_to_f32(bits)), h = __float_as_uint(f16_to_f32(bits));
-  const uint32_t m = 0u - (uint32_t)(sdt != 0);
-  return __uint_as_float((b & m) | (h & ~m));
+// Scale bits -> fp32 with the scale dtype fixed at compile time (1 bf16, 0 fp16).
+template <int SDT>
+__device__ __forceinline__ float scale_of(uint32_t bits) {
+  if constexpr (SDT == 1) return bf16_to_f32(bits);
+  else return f16_to_f32(bits);
 }
 
 // acc[t] += s * (G[t] - c * X[t]) for the lane's 4 token columns
@@ -171,7 +171,7 @@ constexpr int kDownWavesPerEU = 6;
 // rows of each pass's columns are copied once the routing is known.  Work
 // item = pair index; the items of an expert's later pairs exit at once.
 // LDS (w4_p1_lds_bytes): red [S][wave][gate,up][64][4] f32 | metadata S x 80*G1 B | x rows.
-template <int ACT, int NB, int S, int NW>
+template <int ACT, int SDT, int NB, int S, int NW>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(kP1WavesPerEU)))
 void w4a16_phase1_kernel(W4Args a) {
   const SchedArgs& c = a.c;
@@ -181,7 +181,12 @@ void w4a16_phase1_kernel(W4Args a) {
   unsigned char* meta = smem + S * p1_red_bytes(NW);
   uint16_t* xs = reinterpret_cast<uint16_t*>(meta + S * 80 * G1);
   const int item = blockIdx.y, j0 = blockIdx.x * S;   // grid (I/16/S, items): an item's slices adjacent
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  // the wave index, the expert and its column count are uniform: readfirstlane
+  // keeps them (and the weight addresses made from them) in SGPRs, so a weight
+  // load is a scalar base plus the lane's 16-byte offset
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const unsigned lane16 = 16u * (unsigned)lane;
   if (a.x_all)   // uniform; x is [T][H] contiguous
     stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, NW, lane,
               [&](int k) { return (const void*)(c.x + 8 * (size_t)k); });
@@ -195,12 +200,12 @@ void w4a16_phase1_kernel(W4Args a) {
   // token of a pair (pairs are token-major)
   const float rk = 1.0f / (float)c.K;
   auto tok_of = [&](int pair) { return div_small(pair, rk); };
-  const int e = cl.e, cnt = cl.cnt;
+  const int e = __builtin_amdgcn_readfirstlane(cl.e), cnt = __builtin_amdgcn_readfirstlane(cl.cnt);
   const size_t blk = (size_t)e * NI1 + j0;   // S consecutive slices: contiguous weights and metadata
   const unsigned char* msrc = a.w13_m + blk * 80 * G1;
   stage_lds(meta, S * 5 * G1, wave, NW, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
   const int g0 = G1 * wave / NW, ng = G1 * (wave + 1) / NW - g0;   // equal for all waves (G1 % NW == 0)
-  const char* wg = (const char*)a.w13 + (blk * 2 * G1 + g0) * 1024 + lane * 16;   // slice s: + 2*G1 KB
+  const char* wg = (const char*)a.w13 + (blk * 2 * G1 + g0) * 1024;   // slice s: + 2*G1 KB; lane: + lane16
   constexpr float off = W4Consts<ACT>::offset;
   for (int cb0 = 0; cb0 < cnt; cb0 += P) {
     const int ncol = min(P, cnt - cb0);
@@ -229,8 +234,8 @@ void w4a16_phase1_kernel(W4Args a) {
 #pragma unroll
         for (int gi = 0; gi < NB; ++gi) {
           const char* p = wg + ((size_t)s * 2 * G1 + gb + gi) * 1024;
-          wgv[s][gi] = ldg16(p);
-          wuv[s][gi] = ldg16(p + (size_t)G1 * 1024);
+          wgv[s][gi] = ldg16(p + lane16);
+          wuv[s][gi] = ldg16(p + (size_t)G1 * 1024 + lane16);
         }
       if (gb == 0) wait_copies_and_sync<2 * NB * S>();   // metadata and x rows are in LDS
 #pragma unroll
@@ -255,8 +260,8 @@ void w4a16_phase1_kernel(W4Args a) {
           const unsigned char* ms = meta + s * 80 * G1;
           const uint32_t sc = reinterpret_cast<const uint32_t*>(ms)[r * G1 + g];
           const uint32_t zz = ms[64 * G1 + r * G1 + g];
-          fold(accg[s], Gg, X, scale_f32(sc & 0xffffu, a.sdt), off + (float)(zz & 0xfu));
-          fold(accu[s], Gu, X, scale_f32(sc >> 16, a.sdt), off + (float)(zz >> 4));
+          fold(accg[s], Gg, X, scale_of<SDT>(sc & 0xffffu), off + (float)(zz & 0xfu));
+          fold(accu[s], Gu, X, scale_of<SDT>(sc >> 16), off + (float)(zz >> 4));
         }
       }
     }
@@ -290,11 +295,8 @@ void w4a16_phase1_kernel(W4Args a) {
   }
 }
 
-// Scales and zeros of the (16 row x 128 k) groups of one w2 row tile: a
+// Zero point of a (16 row x 128 k) group of one w2 row tile: a metadata
 // section holds scales u16 [g2][r], then zeros [g2][r/2] (row r in nibble r&1).
-__device__ __forceinline__ float w2_scale(const unsigned char* sec, int g2, int r, int sdt) {
-  return scale_f32(reinterpret_cast<const uint16_t*>(sec)[16 * g2 + r], sdt);
-}
 __device__ __forceinline__ float w2_zero(const unsigned char* sec, int G2, int g2, int r) {
   return (float)((sec[32 * G2 + 8 * g2 + (r >> 1)] >> (4 * (r & 1))) & 0xfu);
 }
@@ -306,10 +308,10 @@ __device__ __forceinline__ float w2_zero(const unsigned char* sec, int G2, int g
 // in flight together), metadata sections from secs (tile rt at secs +
 // rt*SEC).  The column sums X of a group are shared by the RT tiles.  Waits
 // for the LDS copies and barriers after the first batch of loads is issued.
-template <int ACT, int NB, int RT>
-__device__ __forceinline__ void down_tiles(const char* wb, const uint16_t* arow,
+template <int ACT, int SDT, int NB, int RT>
+__device__ __forceinline__ void down_tiles(const char* wb, unsigned lane16, const uint16_t* arow,
                                            const unsigned char* secs, int SEC, int G2, int r,
-                                           int sdt, f32x4_t (&acc)[RT]) {
+                                           f32x4_t (&acc)[RT]) {
   constexpr float off = W4Consts<ACT>::offset;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0, 0, 0, 0};
@@ -319,7 +321,7 @@ __device__ __forceinline__ void down_tiles(const char* wb, const uint16_t* arow,
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int gi = 0; gi < NB; ++gi) wv[rt][gi] = ldg16(wb + ((size_t)rt * G2 + gb + gi) * 1024);
+      for (int gi = 0; gi < NB; ++gi) wv[rt][gi] = ldg16(wb + ((size_t)rt * G2 + gb + gi) * 1024 + lane16);
     if (gb == 0) wait_copies_and_sync<NB * RT>();   // the LDS operands are in place
 #pragma unroll
     for (int gi = 0; gi < NB; ++gi) {
@@ -337,7 +339,8 @@ __device__ __forceinline__ void down_tiles(const char* wb, const uint16_t* arow,
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) G = mfma16<ACT>(A[cc], deq4<ACT>(ww[cc]), G);
         const unsigned char* sec = secs + rt * SEC;
-        fold(acc[rt], G, X, w2_scale(sec, g2, r, sdt), off + w2_zero(sec, G2, g2, r));
+        fold(acc[rt], G, X, scale_of<SDT>(reinterpret_cast<const uint16_t*>(sec)[16 * g2 + r]),
+             off + w2_zero(sec, G2, g2, r));
       }
     }
   }
@@ -353,7 +356,7 @@ __device__ __forceinline__ void down_tiles(const char* wb, const uint16_t* arow,
 // y = 0 (Int8-gemm/q8_gemm.cpp:329-332).  No workspace traffic besides act,
 // no cross-workgroup communication.
 // LDS: act rows [K][I] | metadata [K][RT][SEC] | outputs [K][16 RT] f32 | valid [K].
-template <int ACT, int NB, int RT>
+template <int ACT, int SDT, int NB, int RT>
 __global__ __launch_bounds__(kDownMaxK * 64) __attribute__((amdgpu_waves_per_eu(kDownWavesPerEU)))
 void w4a16_down_token_kernel(W4Args a) {
   const SchedArgs& c = a.c;
@@ -361,13 +364,16 @@ void w4a16_down_token_kernel(W4Args a) {
   const int H = c.H, I = c.I, K = c.K, MQ = H >> 6, G2 = I >> 7, II = I >> 3;
   const int SEC = w2_meta_sec_bytes(G2);
   const int t = blockIdx.y, tile0 = blockIdx.x * RT, m = tile0 >> 2, jj0 = tile0 & 3;   // grid (H/16/RT, T)
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  // the wave index and the wave's expert id are uniform (SGPRs; see phase 1)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const unsigned lane16 = 16u * (unsigned)lane;
   uint16_t* as = reinterpret_cast<uint16_t*>(smem);
   unsigned char* meta = smem + (size_t)K * I * 2;
   float* outs = reinterpret_cast<float*>(meta + (size_t)K * RT * SEC);
   int* valid = reinterpret_cast<int*>(outs + 16 * RT * K);
   const int i = t * K + wave;   // this wave's pair
-  const int e = c.ids[i];
+  const int e = __builtin_amdgcn_readfirstlane(c.ids[i]);
   stage_lds(reinterpret_cast<unsigned char*>(as), K * II, wave, K, lane,
             [&](int k) { return (const void*)(a.act + (size_t)t * K * I + 8 * (size_t)k); });
   // a wave with an invalid id computes on expert 0 and its output is ignored,
@@ -378,9 +384,9 @@ void w4a16_down_token_kernel(W4Args a) {
   for (int l = lane; l < RT * SEC / 16; l += 64)
     __builtin_amdgcn_global_load_lds(a.w2_m + sec0 * SEC + 16 * l, mdst + (l - lane) * 16, 16, 0, 0);
   if (lane == 0) valid[wave] = ok;
-  const char* wb = (const char*)a.w2 + sec0 * G2 * 1024 + lane * 16;
+  const char* wb = (const char*)a.w2 + sec0 * G2 * 1024;
   f32x4_t acc[RT];
-  down_tiles<ACT, NB, RT>(wb, as + wave * I + 8 * q, mdst, SEC, G2, r, a.sdt, acc);
+  down_tiles<ACT, SDT, NB, RT>(wb, lane16, as + wave * I + 8 * q, mdst, SEC, G2, r, acc);
   if (lane < 16)   // column 0: lanes (r, q = 0)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) outs[16 * (RT * wave + rt) + lane] = acc[rt].x;
@@ -492,7 +498,7 @@ __device__ __forceinline__ void gemm_group(const unsigned char* buf, const float
 // 4 slices, a slice = 16 gate and 16 up rows); wave w owns slice w of each
 // block, so a staged activation row serves 2 * kGemm13Blocks weight tiles per
 // wave.  act[pair] gets the slices' 16 values each.
-template <int ACT>
+template <int ACT, int SDT>
 __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
   constexpr int NB = kGemm13Blocks;
   const SchedArgs& c = a.c;
@@ -568,8 +574,8 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
 #pragma unroll
       for (int p = 0; p < NB; ++p) {
         const uint32_t scc = msc[p][g], zzc = mz[p][g];
-        sc[2 * p] = scale_f32(scc & 0xffffu, a.sdt);
-        sc[2 * p + 1] = scale_f32(scc >> 16, a.sdt);
+        sc[2 * p] = scale_of<SDT>(scc & 0xffffu);
+        sc[2 * p + 1] = scale_of<SDT>(scc >> 16);
         cz[2 * p] = off + (float)(zzc & 0xfu);
         cz[2 * p + 1] = off + (float)((zzc >> 4) & 0xfu);
       }
@@ -605,7 +611,7 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
 // activation row serves kGemm2Quads weight tiles (the rows are re-staged by
 // every workgroup of the tile: 2 quads halve that traffic).  eout[pair] gets
 // the tiles' fp32 values; the combine kernel sums over k.
-template <int ACT>
+template <int ACT, int SDT>
 __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -665,7 +671,7 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
         const uint32_t w4[4] = {wc[p].x, wc[p].y, wc[p].z, wc[p].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) B[p][i] = deq4<ACT>(w4[i]);
-        scp[p] = w2_scale(sec[p], g2, r, a.sdt);
+        scp[p] = scale_of<SDT>(reinterpret_cast<const uint16_t*>(sec[p])[16 * g2 + r]);
         czp[p] = off + w2_zero(sec[p], G2, g2, r);
       }
       gemm_group<ACT, kGemm2Quads, false>(smem + b * kGemmABytes, sums0 + b * kGemmRows, nsub, q, r, B, scp,
@@ -693,26 +699,28 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
     }
 }
 
-hipError_t launch_w4a16_gemm(const W4Args& a, int act, int tiles_max, hipStream_t st, hipEvent_t mid) {
+template <int ACT, int SDT>
+static hipError_t launch_gemm_t(const W4Args& a, int tiles_max, hipStream_t st, hipEvent_t mid) {
   const int g13 = tiles_max * (a.c.I / 64 / kGemm13Blocks), g2 = tiles_max * (a.c.H / 64 / kGemm2Quads);
   const size_t lds13 = w4_gemm13_lds_bytes(a.c.H), lds2 = w4_gemm2_lds_bytes(a.c.I);
-  if (!w4_sorted_fits(a.c.H, a.c.I, device_max_lds())) return hipErrorInvalidValue;
-  if (lds13 > kMaxLds) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(act == 1 ? w4a16_gemm13_kernel<1> : w4a16_gemm13_kernel<0>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds13);
-  if (lds2 > kMaxLds) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(act == 1 ? w4a16_gemm2_kernel<1> : w4a16_gemm2_kernel<0>),
-                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
-  if (act == 1)
-    hipLaunchKernelGGL((w4a16_gemm13_kernel<1>), dim3(g13), dim3(kBlock), lds13, st, a);
-  else
-    hipLaunchKernelGGL((w4a16_gemm13_kernel<0>), dim3(g13), dim3(kBlock), lds13, st, a);
+  if (lds13 > kMaxLds)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_gemm13_kernel<ACT, SDT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds13);
+  if (lds2 > kMaxLds)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_gemm2_kernel<ACT, SDT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+  hipLaunchKernelGGL((w4a16_gemm13_kernel<ACT, SDT>), dim3(g13), dim3(kBlock), lds13, st, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
-  if (act == 1)
-    hipLaunchKernelGGL((w4a16_gemm2_kernel<1>), dim3(g2), dim3(kBlock), lds2, st, a);
-  else
-    hipLaunchKernelGGL((w4a16_gemm2_kernel<0>), dim3(g2), dim3(kBlock), lds2, st, a);
+  hipLaunchKernelGGL((w4a16_gemm2_kernel<ACT, SDT>), dim3(g2), dim3(kBlock), lds2, st, a);
   return hipGetLastError();
+}
+
+hipError_t launch_w4a16_gemm(const W4Args& a, int act, int tiles_max, hipStream_t st, hipEvent_t mid) {
+  if (!w4_sorted_fits(a.c.H, a.c.I, device_max_lds())) return hipErrorInvalidValue;
+  if (act == 1) return a.sdt == 1 ? launch_gemm_t<1, 1>(a, tiles_max, st, mid) : launch_gemm_t<1, 0>(a, tiles_max, st, mid);
+  return a.sdt == 1 ? launch_gemm_t<0, 1>(a, tiles_max, st, mid) : launch_gemm_t<0, 0>(a, tiles_max, st, mid);
 }
 
 // ================================================================ repack
@@ -845,22 +853,22 @@ hipError_t launch_awq_repack_all(const int32_t* w13q, const int32_t* w13z, const
 }
 
 // ================================================================ launchers
-template <int ACT, int NB, int S, int NW>
+template <int ACT, int SDT, int NB, int S, int NW>
 static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
   if (lds > kMaxLds)
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_phase1_kernel<ACT, NB, S, NW>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_phase1_kernel<ACT, SDT, NB, S, NW>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   const int njs = (a.c.I >> 4) / S;
-  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, NB, S, NW>), dim3(njs, grid / njs), dim3(NW * kWave), lds, st, a);
+  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, SDT, NB, S, NW>), dim3(njs, grid / njs), dim3(NW * kWave), lds, st, a);
 }
 
 // (NB, S, NW) instantiated for phase 1.  S > 1 measured slower on the
 // decode shapes (occupancy), so only S = 1 is built; NW = 8 waves (K split 8
 // ways) for the smallest calls.
-template <int ACT>
+template <int ACT, int SDT>
 static hipError_t dispatch_p1(const W4Args& a, int nb, int s, int nw, int grid, size_t lds, hipStream_t st) {
 #define P1_CASE(NB_, S_, NW_) \
-  if (nb == NB_ && s == S_ && nw == NW_) { launch_p1<ACT, NB_, S_, NW_>(a, grid, lds, st); return hipGetLastError(); }
+  if (nb == NB_ && s == S_ && nw == NW_) { launch_p1<ACT, SDT, NB_, S_, NW_>(a, grid, lds, st); return hipGetLastError(); }
   P1_CASE(1, 1, 4) P1_CASE(2, 1, 4) P1_CASE(3, 1, 4) P1_CASE(4, 1, 4) P1_CASE(6, 1, 4) P1_CASE(8, 1, 4)
   P1_CASE(1, 1, 8) P1_CASE(2, 1, 8) P1_CASE(3, 1, 8) P1_CASE(4, 1, 8)
 #undef P1_CASE
@@ -869,14 +877,14 @@ static hipError_t dispatch_p1(const W4Args& a, int nb, int s, int nw, int grid, 
 
 // (NB, RT) pairs instantiated for the down kernel.  RT > 1 (2-4 tiles per
 // wave) measured no faster on the decode shapes, so only RT = 1 is built.
-template <int ACT>
+template <int ACT, int SDT>
 static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int grid, size_t lds, hipStream_t st) {
 #define P2_CASE(NB_, RT_)                                                                           \
   if (nb == NB_ && rt == RT_) {                                                                     \
     if (lds > kMaxLds)                                                                              \
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_down_token_kernel<ACT, NB_, RT_>), \
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_down_token_kernel<ACT, SDT, NB_, RT_>), \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);              \
-    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, NB_, RT_>), dim3((a.c.H >> 4) / RT_, grid / ((a.c.H >> 4) / RT_)), \
+    hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, SDT, NB_, RT_>), dim3((a.c.H >> 4) / RT_, grid / ((a.c.H >> 4) / RT_)), \
                        dim3(64 * a.c.K), lds, st, a);                                               \
     return hipGetLastError();                                                                       \
   }
@@ -908,7 +916,7 @@ W4Plan w4a16_plan(int H, int I) {
   return p;
 }
 
-template <int ACT>
+template <int ACT, int SDT>
 static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int grid2, hipStream_t st,
                               hipEvent_t mid) {
   // the smallest calls: gate_up's K split over 8 waves (shorter chains per wave)
@@ -920,10 +928,10 @@ static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int g
   const size_t lds1 = w4_p1_lds_bytes(a.c.H, a.x_all ? a.c.T : a.p1_cols, p.s1, nw1);
   const size_t lds2 = w4_down_token_lds_bytes(a.c.I, a.c.K, p.rt2);
   if (lds1 > device_max_lds() || lds2 > device_max_lds()) return hipErrorInvalidValue;
-  hipError_t err = dispatch_p1<ACT>(a, nb1, p.s1, nw1, grid1 / p.s1, lds1, st);
+  hipError_t err = dispatch_p1<ACT, SDT>(a, nb1, p.s1, nw1, grid1 / p.s1, lds1, st);
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
-  return dispatch_p2<ACT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
+  return dispatch_p2<ACT, SDT>(a, p.nb2, p.rt2, grid2 / p.rt2, lds2, st);
 }
 
 // Decode path (T*K <= 64, K <= kDownMaxK): grid1 = T*K * I/16 (phase 1),
@@ -931,8 +939,8 @@ static hipError_t launch_w4_t(const W4Args& a, const W4Plan& p, int grid1, int g
 // slice / tile counts.  mid (optional) is recorded between the two launches.
 hipError_t launch_w4a16(const W4Args& a, const W4Plan& p, int act, int grid1, int grid2, hipStream_t st,
                         hipEvent_t mid) {
-  if (act == 1) return launch_w4_t<1>(a, p, grid1, grid2, st, mid);
-  return launch_w4_t<0>(a, p, grid1, grid2, st, mid);
+  if (act == 1) return a.sdt == 1 ? launch_w4_t<1, 1>(a, p, grid1, grid2, st, mid) : launch_w4_t<1, 0>(a, p, grid1, grid2, st, mid);
+  return a.sdt == 1 ? launch_w4_t<0, 1>(a, p, grid1, grid2, st, mid) : launch_w4_t<0, 0>(a, p, grid1, grid2, st, mid);
 }
 
 }  // namespace mimoe
