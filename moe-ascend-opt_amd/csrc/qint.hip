@@ -213,7 +213,8 @@ __device__ __forceinline__ QLds carve(unsigned char* smem, int Kmax) {
 template <int QT, int ACT, int SC, int NW>
 __device__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int sl, const QLds& L) {
   const SchedArgs& c = a.c;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // wave index uniform (SGPR): the K range and the batch branches below are scalar
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int KB = c.H / 32, S = c.I / 32;
   const int kb0 = KB * wave / NW, kb1 = KB * (wave + 1) / NW;
   const size_t tile = (size_t)e * S + sl;
@@ -294,9 +295,9 @@ __device__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int s
 template <int QT, int ACT, int SC, int NW>
 __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, const QLds& L) {
   const SchedArgs& c = a.c;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int e = rv.active[ui];
-  const int p0 = rv.starts[e], cnt = rv.starts[e + 1] - p0;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int e = __builtin_amdgcn_readfirstlane(rv.active[ui]);
+  const int p0 = __builtin_amdgcn_readfirstlane(rv.starts[e]), cnt = __builtin_amdgcn_readfirstlane(rv.starts[e + 1]) - p0;
   const int KB2 = c.I / 32, HB = c.H / 64;
   const int kb0 = KB2 * wave / NW, kb1 = KB2 * (wave + 1) / NW;
   const size_t tile = (size_t)e * HB + hb;
@@ -363,13 +364,14 @@ __global__ __launch_bounds__(NW * kWave) void q_phase1_kernel(QArgs a) {
     if (!cl.serve) return;   // uniform
     if (tid < kWave) L.route[tid] = cl.colpair;
     __syncthreads();
-    q_phase1<QT, ACT, SC, NW>(a, cl.e, cl.cnt, L.route, sl, L);
+    q_phase1<QT, ACT, SC, NW>(a, __builtin_amdgcn_readfirstlane(cl.e), __builtin_amdgcn_readfirstlane(cl.cnt),
+                              L.route, sl, L);
     return;
   }
   const RouteView rv = sched_route(a.c, L.route, &s_U);
   if (item >= rv.U) return;
-  const int e = rv.active[item], p0 = rv.starts[e];
-  q_phase1<QT, ACT, SC, NW>(a, e, rv.starts[e + 1] - p0, rv.pair + p0, sl, L);
+  const int e = __builtin_amdgcn_readfirstlane(rv.active[item]), p0 = __builtin_amdgcn_readfirstlane(rv.starts[e]);
+  q_phase1<QT, ACT, SC, NW>(a, e, __builtin_amdgcn_readfirstlane(rv.starts[e + 1]) - p0, rv.pair + p0, sl, L);
 }
 
 template <int QT, int ACT, int SC, int NW>
@@ -401,14 +403,16 @@ __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = c.H, I = c.I, K = c.K, KB2 = I / 32, HB = H / 64;
   const int t = blockIdx.y, jt = blockIdx.x;   // grid (H/16 tiles, T)
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, r = lane & 15;
+  // the wave index and the wave's expert id are uniform (SGPRs)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int q = lane >> 4, r = lane & 15;
   int8_t* xq = reinterpret_cast<int8_t*>(smem);
   float* xd = reinterpret_cast<float*>(smem + (size_t)K * I);
   int* xs = reinterpret_cast<int*>(xd + K * KB2);
   float* part = reinterpret_cast<float*>(xs + K * KB2);
   float* outs = part + K * 64;
   int* valid = reinterpret_cast<int*>(outs + K * 16);
-  const int e = c.ids[t * K + wave];
+  const int e = __builtin_amdgcn_readfirstlane(c.ids[t * K + wave]);
   const bool ok = (unsigned)e < (unsigned)c.E;
   // this lane's row in the 64-row layout tile, and its quarter of the blocks
   const int row = (jt & 3) * 16 + r;
