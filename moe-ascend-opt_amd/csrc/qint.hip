@@ -630,8 +630,17 @@ __device__ __forceinline__ long qg_wbytes(uint64_t w) {
   if constexpr (QT == 0) {
     return (long)w;
   } else {
-    const uint32_t x = (uint32_t)w ^ 0x88888888u;   // n ^ 8: the 4-bit two's complement of n - 8
-    return (long)((uint64_t)((x << 4) & 0xf0f0f0f0u) | ((uint64_t)(x & 0xf0f0f0f0u) << 32));
+    // n ^ 8 (the 4-bit two's complement of n - 8) in the high half of each
+    // byte: one 3-input bit operation for the high nibbles, a shift and one
+    // for the low ones (the constants sit in registers: gfx9 VOP3 takes no
+    // literal)
+    uint32_t k8 = 0x88888888u, kf0 = 0xf0f0f0f0u;
+    asm("" : "+v"(k8));
+    asm("" : "+v"(kf0));
+    const uint32_t w32 = (uint32_t)w;
+    const uint32_t hi = (w32 ^ k8) & kf0;
+    const uint32_t lo = ((w32 << 4) ^ k8) & kf0;
+    return (long)((uint64_t)lo | ((uint64_t)hi << 32));
   }
 }
 
