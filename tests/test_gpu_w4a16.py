@@ -148,14 +148,18 @@ def test_graph_replay_matches_eager(cuda, small, T, K):
         assert torch.equal(y.cpu(), eager[rep])
 
 
+@pytest.mark.parametrize("T", [5, 40])
 @pytest.mark.parametrize("adt,sdt", [(torch.float16, torch.bfloat16), (torch.float16, torch.float16),
                                      (torch.bfloat16, torch.float16)])
-def test_dtypes(cuda, adt, sdt):
+def test_dtypes(cuda, adt, sdt, T):
+    """Every activation / scale dtype pair on the decode kernels (T = 5: 20
+    routed pairs) and on the sorted grouped GEMMs (T = 40: 160 pairs); each
+    scale dtype is a separate kernel instance."""
     E, H, I = SMALL["E"], SMALL["H"], SMALL["I"]
     w = w4a16_random(E, H, I, seed=200, scale_dtype=sdt)
     h = _handle(E, H, I, w, True, cuda)
-    ids, tw = topk_routing(5, E, 4, seed=2)
-    x = torch.randn(5, H, generator=torch.Generator().manual_seed(2)).to(adt)
+    ids, tw = topk_routing(T, E, 4, seed=2)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(2)).to(adt)
     y = _run(h, x, ids, tw, cuda)
     assert y.dtype == adt
     assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, adt)) <= TOL
