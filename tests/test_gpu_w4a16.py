@@ -236,10 +236,12 @@ def test_qwen_shape_parity(cuda, qwen, bs):
 
 
 def test_minimax_shape_parity(cuda):
+    """MiniMax-M2 shape on the decode path at bs 1, 2 and 8: 24 groups of H
+    per gate_up row, 12 groups of I per down row (two load batches of 6)."""
     E, H, I = 256, 3072, 1536
     w = w4a16_random(E, H, I, seed=7)
     h = _handle(E, H, I, w, True, cuda)
-    for bs in (1, 8):
+    for bs in (1, 2, 8):
         ids, tw = topk_routing(bs, E, 8, seed=bs + 50)
         x = torch.randn(bs, H, generator=torch.Generator().manual_seed(bs)).to(torch.bfloat16)
         y = _run(h, x, ids, tw, cuda)
