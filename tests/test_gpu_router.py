@@ -84,3 +84,42 @@ def test_forward_logits_equals_two_step(cuda, quant, T):
     assert torch.equal(y1, y2)
     rid, rw = oracle.topk_softmax(logits.cpu().numpy(), K, True)
     assert np.array_equal(ids.cpu().numpy(), rid)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("renorm", [True, False])
+@pytest.mark.parametrize("E,T,K", [(16, 3, 8), (128, 1, 8), (128, 8, 8), (128, 6, 10), (512, 2, 16), (64, 64, 1)])
+def test_forward_logits_decode_router_pass(cuda, dt, renorm, E, T, K):
+    """mi_moe_forward_logits on W4A16 decode sizes, every logits dtype and
+    softmax mode: the ids and weights it returns are bit-exact against the
+    oracle, and y equals mi_moe_forward on them bit for bit."""
+    H, I = 512, 256
+    L = nanovllm_moe.capi()
+    g = torch.Generator().manual_seed(E * 100 + T * 10 + K)
+    hp = ctypes.c_void_p()
+    nanovllm_moe.check(L.mi_moe_create(E, H, I, 2, ctypes.byref(hp)), "create")
+    try:
+        ws = [t.to(cuda) for t in w4a16_random(E, H, I, seed=E + T)]
+        nanovllm_moe.check(L.mi_moe_store_awq(hp, *[t.data_ptr() for t in ws], 128, nanovllm_moe.BF16, 1,
+                                              nanovllm_moe.stream_ptr()), "store_awq")
+        x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(cuda)
+        logits = (torch.randn(T, E, generator=g) * 2).to(dt).to(cuda)
+        ids = torch.full((T, K), -7, dtype=torch.int32, device=cuda)
+        w = torch.full((T, K), -7.0, dtype=torch.float32, device=cuda)
+        y1 = torch.full_like(x, float("nan"))
+        code = {torch.float32: nanovllm_moe.F32, torch.bfloat16: nanovllm_moe.BF16,
+                torch.float16: nanovllm_moe.F16}
+        rc = L.mi_moe_forward_logits(hp, _ptr(x), _ptr(y1), _ptr(logits), code[dt], T, K, 1 if renorm else 0,
+                                     nanovllm_moe.BF16, _ptr(ids), _ptr(w), nanovllm_moe.stream_ptr())
+        nanovllm_moe.check(rc, "mi_moe_forward_logits")
+        torch.cuda.synchronize()
+        rid, rw = oracle.topk_softmax(logits.float().cpu().numpy(), K, renorm)
+        assert np.array_equal(ids.cpu().numpy(), rid)
+        assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+        y2 = torch.full_like(x, float("nan"))
+        nanovllm_moe.check(L.mi_moe_forward(hp, _ptr(x), _ptr(y2), _ptr(w), _ptr(ids), T, K, nanovllm_moe.BF16,
+                                            nanovllm_moe.stream_ptr()), "mi_moe_forward")
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2)
+    finally:
+        L.mi_moe_destroy(hp)
