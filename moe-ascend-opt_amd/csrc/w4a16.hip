@@ -173,10 +173,23 @@ constexpr int kDownWavesPerEU = 6;
 // LDS (w4_p1_lds_bytes): red [S][wave][gate,up][64][4] f32 | metadata S x 80*G1 B | x rows.
 template <int ACT, int SDT, int NB, int S, int NW>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(kP1WavesPerEU)))
-void w4a16_phase1_kernel(W4Args a) {
-  const SchedArgs& c = a.c;
+void w4a16_phase1_kernel(const int32_t* ids, const uint16_t* x, const char* w13, const unsigned char* w13_m, int T,
+                         int n, int E, int H, int I, int x_all, int K, W4Args a) {
+  // the leading arguments repeat fields of a: gfx950 preloads the first 14
+  // dwords of them into SGPRs at wave launch (-amdgpu-kernarg-preload-count),
+  // so the x copy, the ids read and the weight addresses do not wait for a
+  // kernel-argument fetch
+  SchedArgs c = a.c;
+  c.ids = ids;
+  c.x = x;
+  c.T = T;
+  c.n = n;
+  c.E = E;
+  c.H = H;
+  c.I = I;
+  c.K = K;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, P = a.p1_cols, HI = H >> 3;
+  const int G1 = H >> 7, NI1 = I >> 4, P = a.p1_cols, HI = H >> 3;
   float* red = reinterpret_cast<float*>(smem);
   unsigned char* meta = smem + S * p1_red_bytes(NW);
   uint16_t* xs = reinterpret_cast<uint16_t*>(meta + S * 80 * G1);
@@ -187,7 +200,7 @@ void w4a16_phase1_kernel(W4Args a) {
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int q = lane >> 4, r = lane & 15;
   const unsigned lane16 = 16u * (unsigned)lane;
-  if (a.x_all)   // uniform; x is [T][H] contiguous
+  if (x_all)   // uniform; x is [T][H] contiguous
     stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, NW, lane,
               [&](int k) { return (const void*)(c.x + 8 * (size_t)k); });
   const BallotCols cl = ballot_cols(c, item, lane);
@@ -202,15 +215,15 @@ void w4a16_phase1_kernel(W4Args a) {
   auto tok_of = [&](int pair) { return div_small(pair, rk); };
   const int e = __builtin_amdgcn_readfirstlane(cl.e), cnt = __builtin_amdgcn_readfirstlane(cl.cnt);
   const size_t blk = (size_t)e * NI1 + j0;   // S consecutive slices: contiguous weights and metadata
-  const unsigned char* msrc = a.w13_m + blk * 80 * G1;
+  const unsigned char* msrc = w13_m + blk * 80 * G1;
   stage_lds(meta, S * 5 * G1, wave, NW, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
   const int g0 = G1 * wave / NW, ng = G1 * (wave + 1) / NW - g0;   // equal for all waves (G1 % NW == 0)
-  const char* wg = (const char*)a.w13 + (blk * 2 * G1 + g0) * 1024;   // slice s: + 2*G1 KB; lane: + lane16
+  const char* wg = w13 + (blk * 2 * G1 + g0) * 1024;   // slice s: + 2*G1 KB; lane: + lane16
   constexpr float off = W4Consts<ACT>::offset;
   for (int cb0 = 0; cb0 < cnt; cb0 += P) {
     const int ncol = min(P, cnt - cb0);
     int xr;   // LDS row of this lane's column
-    if (a.x_all) {
+    if (x_all) {
       xr = tok_of(pair_of(cb0 + min(r, ncol - 1)));
     } else {
       // the pass's hidden rows: row cc at xs + cc * H, in 1 KB chunks of 64
@@ -358,10 +371,12 @@ __device__ __forceinline__ void down_tiles(const char* wb, unsigned lane16, cons
 // LDS: act rows [K][I] | metadata [K][RT][SEC] | outputs [K][16 RT] f32 | valid [K].
 template <int ACT, int SDT, int NB, int RT>
 __global__ __launch_bounds__(kDownMaxK * 64) __attribute__((amdgpu_waves_per_eu(kDownWavesPerEU)))
-void w4a16_down_token_kernel(W4Args a) {
-  const SchedArgs& c = a.c;
+void w4a16_down_token_kernel(const int32_t* ids, const uint16_t* act, const char* w2, const unsigned char* w2_m, int K,
+                             int E, int H, int I, const float* tw, uint16_t* y, W4Args a) {
+  // the leading arguments repeat fields of a (the first 14 dwords are preloaded
+  // into SGPRs; see phase 1)
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, I = c.I, K = c.K, MQ = H >> 6, G2 = I >> 7, II = I >> 3;
+  const int MQ = H >> 6, G2 = I >> 7, II = I >> 3;
   const int SEC = w2_meta_sec_bytes(G2);
   const int t = blockIdx.y, tile0 = blockIdx.x * RT, m = tile0 >> 2, jj0 = tile0 & 3;   // grid (H/16/RT, T)
   // the wave index and the wave's expert id are uniform (SGPRs; see phase 1)
@@ -373,18 +388,18 @@ void w4a16_down_token_kernel(W4Args a) {
   float* outs = reinterpret_cast<float*>(meta + (size_t)K * RT * SEC);
   int* valid = reinterpret_cast<int*>(outs + 16 * RT * K);
   const int i = t * K + wave;   // this wave's pair
-  const int e = __builtin_amdgcn_readfirstlane(c.ids[i]);
+  const int e = __builtin_amdgcn_readfirstlane(ids[i]);
   stage_lds(reinterpret_cast<unsigned char*>(as), K * II, wave, K, lane,
-            [&](int k) { return (const void*)(a.act + (size_t)t * K * I + 8 * (size_t)k); });
+            [&](int k) { return (const void*)(act + (size_t)t * K * I + 8 * (size_t)k); });
   // a wave with an invalid id computes on expert 0 and its output is ignored,
   // so every wave runs the same code (one barrier each)
-  const bool ok = (unsigned)e < (unsigned)c.E;
+  const bool ok = (unsigned)e < (unsigned)E;
   const size_t sec0 = ((size_t)(ok ? e : 0) * MQ + m) * 4 + jj0;   // RT tiles within one quad: contiguous
   unsigned char* mdst = meta + wave * RT * SEC;
   for (int l = lane; l < RT * SEC / 16; l += 64)
-    __builtin_amdgcn_global_load_lds(a.w2_m + sec0 * SEC + 16 * l, mdst + (l - lane) * 16, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(w2_m + sec0 * SEC + 16 * l, mdst + (l - lane) * 16, 16, 0, 0);
   if (lane == 0) valid[wave] = ok;
-  const char* wb = (const char*)a.w2 + sec0 * G2 * 1024;
+  const char* wb = w2 + sec0 * G2 * 1024;
   f32x4_t acc[RT];
   down_tiles<ACT, SDT, NB, RT>(wb, lane16, as + wave * I + 8 * q, mdst, SEC, G2, r, acc);
   if (lane < 16)   // column 0: lanes (r, q = 0)
@@ -392,13 +407,13 @@ void w4a16_down_token_kernel(W4Args a) {
     for (int rt = 0; rt < RT; ++rt) outs[16 * (RT * wave + rt) + lane] = acc[rt].x;
   __syncthreads();
   if (tid < 16 * RT) {
-    float y = 0.0f;
+    float yv = 0.0f;
     for (int k = 0; k < K; ++k)
       if (valid[k]) {
-        const float prod = c.tw[t * K + k] * outs[16 * RT * k + tid];
-        y = y + prod;
+        const float prod = tw[t * K + k] * outs[16 * RT * k + tid];
+        yv = yv + prod;
       }
-    c.y[(size_t)t * H + 16 * tile0 + tid] = from_f32<ACT>(y);
+    y[(size_t)t * H + 16 * tile0 + tid] = from_f32<ACT>(yv);
   }
 }
 
@@ -859,7 +874,8 @@ static void launch_p1(const W4Args& a, int grid, size_t lds, hipStream_t st) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_phase1_kernel<ACT, SDT, NB, S, NW>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   const int njs = (a.c.I >> 4) / S;
-  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, SDT, NB, S, NW>), dim3(njs, grid / njs), dim3(NW * kWave), lds, st, a);
+  hipLaunchKernelGGL((w4a16_phase1_kernel<ACT, SDT, NB, S, NW>), dim3(njs, grid / njs), dim3(NW * kWave), lds, st,
+                     a.c.ids, a.c.x, (const char*)a.w13, a.w13_m, a.c.T, a.c.n, a.c.E, a.c.H, a.c.I, a.x_all, a.c.K, a);
 }
 
 // (NB, S, NW) instantiated for phase 1.  S > 1 measured slower on the
@@ -885,7 +901,8 @@ static hipError_t dispatch_p2(const W4Args& a, int nb, int rt, int grid, size_t 
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_down_token_kernel<ACT, SDT, NB_, RT_>), \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);              \
     hipLaunchKernelGGL((w4a16_down_token_kernel<ACT, SDT, NB_, RT_>), dim3((a.c.H >> 4) / RT_, grid / ((a.c.H >> 4) / RT_)), \
-                       dim3(64 * a.c.K), lds, st, a);                                               \
+                       dim3(64 * a.c.K), lds, st, a.c.ids, (const uint16_t*)a.act, (const char*)a.w2, a.w2_m, \
+                       a.c.K, a.c.E, a.c.H, a.c.I, a.c.tw, a.c.y, a);                                \
     return hipGetLastError();                                                                       \
   }
   P2_CASE(1, 1) P2_CASE(2, 1) P2_CASE(3, 1) P2_CASE(4, 1) P2_CASE(6, 1) P2_CASE(8, 1)

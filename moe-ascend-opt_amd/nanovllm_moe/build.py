@@ -37,9 +37,13 @@ NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # Per-file device flags.  The grouped GEMMs read every MFMA result with VALU
 # ops (the per-block fp32 scaling, the W4A16 zero/scale fold); the VGPR form
 # of the MFMA saves a v_accvgpr_read per result register.  The W4A16 decode
-# kernels compile to the same code either way.
+# kernels compile to the same code either way.  Kernel-argument preloading
+# (gfx950: the first 14 dwords of a kernel's scalar arguments arrive in SGPRs
+# at wave launch) takes the argument fetch off the decode kernels' chain of
+# dependent loads; the kernels pass their first-needed fields as leading
+# scalar arguments (a by-value struct is not preloaded).
 FILE_FLAGS = {"qint.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-              "w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+              "w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def _run(cmd):
