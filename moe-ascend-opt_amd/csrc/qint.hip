@@ -211,7 +211,7 @@ __device__ __forceinline__ QLds carve(unsigned char* smem, int Kmax) {
 
 // ---------------------------------------------------------------- phase 1
 template <int QT, int ACT, int SC, int NW>
-__device__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int sl, const QLds& L) {
+__device__ __forceinline__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int sl, const QLds& L) {
   const SchedArgs& c = a.c;
   // wave index uniform (SGPR): the K range and the batch branches below are scalar
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -352,8 +352,24 @@ __device__ void q_phase2(const QArgs& a, const RouteView& rv, int ui, int hb, co
 // serves its expert iff it is the expert's first pair; ballot routing, the
 // expert's pair list staged in LDS); above, one per active expert of the
 // counting sort (in LDS, or the routing kernel's arrays).
+// The leading arguments repeat fields of a0: gfx950 preloads the first 14
+// dwords of them into SGPRs at wave launch (-amdgpu-kernarg-preload-count), so
+// the ids read, the weight addresses and the x staging do not wait for a
+// kernel-argument fetch.
 template <int QT, int ACT, int SC, int NW>
-__global__ __launch_bounds__(NW * kWave) void q_phase1_kernel(QArgs a) {
+__global__ __launch_bounds__(NW * kWave) void q_phase1_kernel(const int32_t* ids, const void* w13, const uint16_t* w13_d,
+                                                             const uint16_t* x, int n, int E, int H, int I, int K,
+                                                             QArgs a0) {
+  QArgs a = a0;
+  a.c.ids = ids;
+  a.w13 = w13;
+  a.w13_d = w13_d;
+  a.c.x = x;
+  a.c.n = n;
+  a.c.E = E;
+  a.c.H = H;
+  a.c.I = I;
+  a.c.K = K;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_U;
   const QLds L = carve(smem, a.c.H);
@@ -398,10 +414,25 @@ __global__ __launch_bounds__(NW * kWave) void q_phase2_kernel(QArgs a) {
 // partials [K][64] | outputs [K][16] | valid [K].
 
 template <int QT, int ACT, int SC>
-__global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(QArgs a) {
+__global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(const int32_t* ids, const void* w2,
+                                                                      const uint16_t* w2_d, const int8_t* act_q,
+                                                                      const float* act_d, int K, int E, int H, int I,
+                                                                      QArgs a0) {
+  // the leading arguments repeat fields of a0 (preloaded into SGPRs; see
+  // q_phase1_kernel)
+  QArgs a = a0;
+  a.c.ids = ids;
+  a.w2 = w2;
+  a.w2_d = w2_d;
+  a.act_q = const_cast<int8_t*>(act_q);
+  a.act_d = const_cast<float*>(act_d);
+  a.c.K = K;
+  a.c.E = E;
+  a.c.H = H;
+  a.c.I = I;
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int H = c.H, I = c.I, K = c.K, KB2 = I / 32, HB = H / 64;
+  const int KB2 = I / 32, HB = H / 64;
   const int t = blockIdx.y, jt = blockIdx.x;   // grid (H/16 tiles, T)
   // the wave index and the wave's expert id are uniform (SGPRs)
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -478,13 +509,15 @@ static hipError_t launch_q_nw(const QArgs& a, int grid1, int grid2, size_t route
   const size_t l1 = q_stage_bytes(a.c.H) + route;
   lds_opt_in(q_phase1_kernel<QT, ACT, SC, NW>, l1);
   hipLaunchKernelGGL((q_phase1_kernel<QT, ACT, SC, NW>), dim3(a.c.I / 32, grid1 / (a.c.I / 32)), dim3(NW * kWave),
-                     l1, st, a);
+                     l1, st, a.c.ids, a.w13, a.w13_d, a.c.x, a.c.n, a.c.E, a.c.H, a.c.I, a.c.K, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   if (token_down) {
     const size_t l2 = q_down_token_lds_bytes(a.c.I, a.c.K);
     lds_opt_in(q_down_token_kernel<QT, ACT, SC>, l2);
-    hipLaunchKernelGGL((q_down_token_kernel<QT, ACT, SC>), dim3(a.c.H / 16, a.c.T), dim3(64 * a.c.K), l2, st, a);
+    hipLaunchKernelGGL((q_down_token_kernel<QT, ACT, SC>), dim3(a.c.H / 16, a.c.T), dim3(64 * a.c.K), l2, st,
+                       a.c.ids, a.w2, a.w2_d, (const int8_t*)a.act_q, (const float*)a.act_d, a.c.K, a.c.E, a.c.H,
+                       a.c.I, a);
     return hipGetLastError();
   }
   const size_t l2 = q_stage_bytes(a.c.I) + route;

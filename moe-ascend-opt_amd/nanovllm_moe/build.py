@@ -42,7 +42,7 @@ NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # at wave launch) takes the argument fetch off the decode kernels' chain of
 # dependent loads; the kernels pass their first-needed fields as leading
 # scalar arguments (a by-value struct is not preloaded).
-FILE_FLAGS = {"qint.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+FILE_FLAGS = {"qint.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
               "w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
