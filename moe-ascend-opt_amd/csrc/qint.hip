@@ -805,7 +805,19 @@ __device__ __forceinline__ void qg_gemm(unsigned char* smem, const int8_t* rowq,
 // intermediate values of a row form one Q8_0 block (pack_A_q8_0,
 // Int8-gemm/gemm_kernels.cpp:394-425).
 template <int QT, int SC>
-__global__ __launch_bounds__(kBlock) void q_gemm13_kernel(QArgs a) {
+__global__ __launch_bounds__(kBlock) void q_gemm13_kernel(const int32_t* ntiles, const int32_t* tiles,
+                                                         const int32_t* tokl, const int8_t* xq, const float* xd,
+                                                         const void* w13, const uint16_t* w13_d, QArgs a0) {
+  // the leading arguments repeat fields of a0 (preloaded into SGPRs; see
+  // q_phase1_kernel)
+  QArgs a = a0;
+  a.c.rg.ntiles = const_cast<int32_t*>(ntiles);
+  a.c.rg.tiles = const_cast<int32_t*>(tiles);
+  a.c.rg.tok = const_cast<int32_t*>(tokl);
+  a.xq = xq;
+  a.xd = xd;
+  a.w13 = w13;
+  a.w13_d = w13_d;
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = c.H, I = c.I, S = I / 32, KB = H / 32;
@@ -890,7 +902,18 @@ __global__ __launch_bounds__(kBlock) void q_gemm13_kernel(QArgs a) {
 // owns output rows 64hb + 16w..+15.  eout[pair] gets the fp32 sums (the combine
 // kernel follows).
 template <int QT, int SC>
-__global__ __launch_bounds__(kBlock) void q_gemm2_kernel(QArgs a) {
+__global__ __launch_bounds__(kBlock) void q_gemm2_kernel(const int32_t* ntiles, const int32_t* tiles,
+                                                        const int32_t* tok, const int8_t* act_q, const float* act_d,
+                                                        const void* w2, const uint16_t* w2_d, QArgs a0) {
+  // the leading arguments repeat fields of a0 (preloaded; see q_gemm13_kernel)
+  QArgs a = a0;
+  a.c.rg.ntiles = const_cast<int32_t*>(ntiles);
+  a.c.rg.tiles = const_cast<int32_t*>(tiles);
+  a.c.rg.tok = const_cast<int32_t*>(tok);
+  a.act_q = const_cast<int8_t*>(act_q);
+  a.act_d = const_cast<float*>(act_d);
+  a.w2 = w2;
+  a.w2_d = w2_d;
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = c.H, I = c.I, HB = H / 64, KB2 = I / 32;
@@ -930,10 +953,13 @@ __global__ __launch_bounds__(kBlock) void q_gemm2_kernel(QArgs a) {
 
 template <int QT, int SC>
 static hipError_t launch_qg_t(const QArgs& a, int tiles_max, hipStream_t st) {
-  hipLaunchKernelGGL((q_gemm13_kernel<QT, SC>), dim3(tiles_max * (a.c.I / 32)), dim3(kBlock), kQgLds, st, a);
+  hipLaunchKernelGGL((q_gemm13_kernel<QT, SC>), dim3(tiles_max * (a.c.I / 32)), dim3(kBlock), kQgLds, st,
+                     a.c.rg.ntiles, a.c.rg.tiles, a.c.rg.tok, a.xq, a.xd, a.w13, a.w13_d, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((q_gemm2_kernel<QT, SC>), dim3(tiles_max * (a.c.H / 64)), dim3(kBlock), kQgLds, st, a);
+  hipLaunchKernelGGL((q_gemm2_kernel<QT, SC>), dim3(tiles_max * (a.c.H / 64)), dim3(kBlock), kQgLds, st,
+                     a.c.rg.ntiles, a.c.rg.tiles, a.c.rg.tok, (const int8_t*)a.act_q, (const float*)a.act_d, a.w2,
+                     a.w2_d, a);
   return hipGetLastError();
 }
 

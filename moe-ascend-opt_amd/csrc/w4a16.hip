@@ -514,7 +514,20 @@ __device__ __forceinline__ void gemm_group(const unsigned char* buf, const float
 // block, so a staged activation row serves 2 * kGemm13Blocks weight tiles per
 // wave.  act[pair] gets the slices' 16 values each.
 template <int ACT, int SDT>
-__global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
+__global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(const int32_t* ntiles, const int32_t* tiles,
+                                                             const int32_t* tok, const uint16_t* x, const void* w13,
+                                                             const unsigned char* w13_m, int H_, int I_, W4Args a0) {
+  // the leading arguments repeat fields of a0 (the first 14 dwords are
+  // preloaded into SGPRs, so the tile lookup does not wait for an argument fetch)
+  W4Args a = a0;
+  a.c.rg.ntiles = const_cast<int32_t*>(ntiles);
+  a.c.rg.tiles = const_cast<int32_t*>(tiles);
+  a.c.rg.tok = const_cast<int32_t*>(tok);
+  a.c.x = x;
+  a.w13 = w13;
+  a.w13_m = w13_m;
+  a.c.H = H_;
+  a.c.I = I_;
   constexpr int NB = kGemm13Blocks;
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -627,7 +640,19 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(W4Args a) {
 // every workgroup of the tile: 2 quads halve that traffic).  eout[pair] gets
 // the tiles' fp32 values; the combine kernel sums over k.
 template <int ACT, int SDT>
-__global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(W4Args a) {
+__global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(const int32_t* ntiles, const int32_t* tiles,
+                                                            const int32_t* tok, const uint16_t* act, const void* w2,
+                                                            const unsigned char* w2_m, int H_, int I_, W4Args a0) {
+  // the leading arguments repeat fields of a0 (preloaded; see the gate_up GEMM)
+  W4Args a = a0;
+  a.c.rg.ntiles = const_cast<int32_t*>(ntiles);
+  a.c.rg.tiles = const_cast<int32_t*>(tiles);
+  a.c.rg.tok = const_cast<int32_t*>(tok);
+  a.act = const_cast<uint16_t*>(act);
+  a.w2 = w2;
+  a.w2_m = w2_m;
+  a.c.H = H_;
+  a.c.I = I_;
   const SchedArgs& c = a.c;
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = c.H, I = c.I, G2 = I >> 7, MQ = H >> 6, NMB = MQ / kGemm2Quads;
@@ -724,11 +749,13 @@ static hipError_t launch_gemm_t(const W4Args& a, int tiles_max, hipStream_t st, 
   if (lds2 > kMaxLds)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_gemm2_kernel<ACT, SDT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
-  hipLaunchKernelGGL((w4a16_gemm13_kernel<ACT, SDT>), dim3(g13), dim3(kBlock), lds13, st, a);
+  hipLaunchKernelGGL((w4a16_gemm13_kernel<ACT, SDT>), dim3(g13), dim3(kBlock), lds13, st, a.c.rg.ntiles, a.c.rg.tiles,
+                     a.c.rg.tok, a.c.x, a.w13, a.w13_m, a.c.H, a.c.I, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   if (mid && (err = hipEventRecord(mid, st)) != hipSuccess) return err;
-  hipLaunchKernelGGL((w4a16_gemm2_kernel<ACT, SDT>), dim3(g2), dim3(kBlock), lds2, st, a);
+  hipLaunchKernelGGL((w4a16_gemm2_kernel<ACT, SDT>), dim3(g2), dim3(kBlock), lds2, st, a.c.rg.ntiles, a.c.rg.tiles,
+                     a.c.rg.tok, (const uint16_t*)a.act, a.w2, a.w2_m, a.c.H, a.c.I, a);
   return hipGetLastError();
 }
 

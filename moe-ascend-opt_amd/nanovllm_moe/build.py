@@ -43,7 +43,8 @@ NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # dependent loads; the kernels pass their first-needed fields as leading
 # scalar arguments (a by-value struct is not preloaded).
 FILE_FLAGS = {"qint.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
-              "w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+              "w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
+              "common_kernels.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def _run(cmd):
