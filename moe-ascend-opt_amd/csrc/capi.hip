@@ -40,6 +40,8 @@ hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, hipStream_t
 hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, bool, hipStream_t);
 hipError_t launch_qint_gemm(const QArgs&, int, int, int, hipStream_t);
+hipError_t launch_quant_route(const void*, int, int64_t, int64_t, int8_t*, float*, const int32_t*, int, int, int,
+                              const RouteGlobal&, hipStream_t, int);
 hipError_t launch_topk_softmax(const void*, int, int, int, int, int, int32_t*, float*, hipStream_t);
 hipError_t launch_q_repack(int, const void*, const uint16_t*, void*, uint16_t*, int, int, int, int,
                            int, hipStream_t);
@@ -390,8 +392,7 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
     // the two int8 grouped GEMMs, the combine
     a.xq = w.xq;
     a.xd = w.xd;
-    HIPCHK(launch_quant_act(x, act, T, h->H, w.xq, w.xd, st));
-    HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
+    HIPCHK(launch_quant_route(x, act, T, h->H, w.xq, w.xd, ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
     HIPCHK(launch_qint_gemm(a, h->quant, h->scale_dtype, (int)gemm_tiles_max(n, (int)h->E), st));
     HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
     return MI_MOE_OK;

@@ -1,6 +1,8 @@
 // common_kernels.hip -- routing and Q8_0 activation quantization kernels used
 // by every weight format (and exposed alone through the C ABI for checking).
 #pragma clang fp contract(off)
+#include <algorithm>
+
 #include "mi_moe_device.hpp"
 #include "mi_moe_internal.hpp"
 
@@ -146,11 +148,10 @@ __device__ __forceinline__ void route_seg_rank(int lo, int hi, int K, const int*
 // exclusive prefix over waves, then the segments are ranked.
 // LDS: (kRouteWaves + 1) * E ints (E <= 512).
 static_assert(kRouteMultiMin <= kRouteThreads * kRouteSegIter, "a wave segment fits kRouteSegIter batches");
-__global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
-    const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
-    int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out,
-    int tok_div, int32_t* tiles_out, int32_t* ntiles_out) {
-  extern __shared__ int lds[];
+__device__ __forceinline__ void route_global_body(const int32_t* __restrict__ ids, int n, int K, int E,
+                                                  int32_t* counts_out, int32_t* starts_out, int32_t* active_out,
+                                                  int32_t* tok, int32_t* scat, int32_t* U_out, int tok_div,
+                                                  int32_t* tiles_out, int32_t* ntiles_out, int* lds) {
   int* counts = lds;            // [E]: totals, then the starts
   int* cw = lds + E;            // [kRouteWaves][E]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -176,6 +177,15 @@ __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
   if (tid < kWave) route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out);
   __syncthreads();
   route_seg_rank(lo, hi, K, counts, lane, mine, seg, tok, scat, tok_div);
+}
+
+__global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
+    const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
+    int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out,
+    int tok_div, int32_t* tiles_out, int32_t* ntiles_out) {
+  extern __shared__ int lds[];
+  route_global_body(ids, n, K, E, counts_out, starts_out, active_out, tok, scat, U_out, tok_div, tiles_out,
+                    ntiles_out, lds);
 }
 
 // Multi-workgroup routing, step 1: the expert histogram of one chunk of ids.
@@ -328,10 +338,9 @@ hipError_t launch_combine(const float* eout, const float* tw, const int32_t* ids
 // if d == 0), q = sat8(RNE(x*id)) (Int8-gemm/gemm_kernels.cpp:37-57); d stays
 // fp32 (Int8-gemm/q8_gemm.cpp:371-375).
 template <int ACT>
-__global__ void quant_act_q8_0_kernel(const uint16_t* __restrict__ x, int64_t nblk,
-                                      int8_t* __restrict__ qs, float* __restrict__ d) {
-  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
-       b += (int64_t)gridDim.x * blockDim.x) {
+__device__ __forceinline__ void quant_act_blocks(const uint16_t* __restrict__ x, int64_t b0, int64_t stride,
+                                                 int64_t nblk, int8_t* __restrict__ qs, float* __restrict__ d) {
+  for (int64_t b = b0; b < nblk; b += stride) {
     const u32x4_t* src = reinterpret_cast<const u32x4_t*>(x + b * 32);
     float v[32];
 #pragma unroll
@@ -349,6 +358,32 @@ __global__ void quant_act_q8_0_kernel(const uint16_t* __restrict__ x, int64_t nb
   }
 }
 
+template <int ACT>
+__global__ void quant_act_q8_0_kernel(const uint16_t* __restrict__ x, int64_t nblk,
+                                      int8_t* __restrict__ qs, float* __restrict__ d) {
+  quant_act_blocks<ACT>(x, (int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x, nblk,
+                        qs, d);
+}
+
+// The single-workgroup routing and Stage A in one launch (the two are
+// independent): workgroup 0 routes, the others quantize.
+template <int ACT>
+__global__ __launch_bounds__(kRouteThreads) void route_quant_kernel(
+    const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out, int32_t* starts_out,
+    int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out, int tok_div, int32_t* tiles_out,
+    int32_t* ntiles_out, const uint16_t* __restrict__ x, int64_t nblk, int8_t* __restrict__ qs,
+    float* __restrict__ d) {
+  extern __shared__ int lds[];
+  if (blockIdx.x == 0) {   // uniform
+    route_global_body(ids, n, K, E, counts_out, starts_out, active_out, tok, scat, U_out, tok_div, tiles_out,
+                      ntiles_out, lds);
+    return;
+  }
+  quant_act_blocks<ACT>(x, (int64_t)(blockIdx.x - 1) * kRouteThreads + threadIdx.x,
+                        (int64_t)(gridDim.x - 1) * kRouteThreads, nblk, qs, d);
+}
+
+
 hipError_t launch_quant_act(const void* x, int act, int64_t T, int64_t H, int8_t* qs, float* d,
                             hipStream_t st) {
   const int64_t nblk = T * (H / 32);
@@ -361,6 +396,26 @@ hipError_t launch_quant_act(const void* x, int act, int64_t T, int64_t H, int8_t
   else
     hipLaunchKernelGGL(quant_act_q8_0_kernel<0>, dim3((unsigned)grid), dim3(256), 0, st,
                        (const uint16_t*)x, nblk, qs, d);
+  return hipGetLastError();
+}
+
+// Stage A (Q8_0 of the T hidden rows) and the routing of the sorted path; one
+// launch when the routing is a single workgroup.
+hipError_t launch_quant_route(const void* x, int act, int64_t T, int64_t H, int8_t* qs, float* d,
+                              const int32_t* ids, int n, int K, int E, const RouteGlobal& rg, hipStream_t st,
+                              int tok_div) {
+  const int64_t nblk = T * (H / 32);
+  if (n > kRouteMultiMin || nblk == 0) {
+    hipError_t err = launch_quant_act(x, act, T, H, qs, d, st);
+    if (err != hipSuccess) return err;
+    return launch_route_global(ids, n, K, E, rg, st, tok_div);
+  }
+  const int64_t gq = std::min<int64_t>((nblk + kRouteThreads - 1) / kRouteThreads, 1024);
+  const size_t lds = (size_t)(kRouteWaves + 1) * E * sizeof(int);
+  auto kern = act == 1 ? route_quant_kernel<1> : route_quant_kernel<0>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(1 + gq)), dim3(kRouteThreads), lds, st, ids, n, K, E, rg.counts,
+                     rg.starts, rg.active, rg.tok, rg.scat, rg.U, tok_div, rg.tiles, rg.ntiles, (const uint16_t*)x,
+                     nblk, qs, d);
   return hipGetLastError();
 }
 
