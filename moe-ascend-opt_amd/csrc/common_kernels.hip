@@ -99,13 +99,21 @@ struct RouteSeg {
 // counts added into mine[E], ids and masks kept in seg.
 __device__ __forceinline__ void route_seg_count(const int32_t* __restrict__ ids, int lo, int hi, int E, int nbits,
                                                 int lane, int* mine, RouteSeg& seg) {
+  // every batch's ids are loaded before the first is used: one memory round
+  // trip for the segment, not one per batch
+  int ev[kRouteSegIter];
+#pragma unroll
+  for (int it = 0; it < kRouteSegIter; ++it) {
+    const int i = lo + 64 * it + lane;
+    ev[it] = i < hi ? ids[i] : -1;
+  }
 #pragma unroll
   for (int it = 0; it < kRouteSegIter; ++it) {
     const int i = lo + 64 * it + lane;
     int e = -1;
     uint64_t m = 0;
     if (lo + 64 * it < hi) {   // uniform
-      e = (i < hi) ? ids[i] : -1;
+      e = ev[it];
       const bool valid = (i < hi) && ((unsigned)e < (unsigned)E);
       m = route_match(e, valid, nbits);
       if (!valid) e = -1;
@@ -190,6 +198,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
 
 // Multi-workgroup routing, step 1: the expert histogram of one chunk of ids.
 constexpr int kRouteCountThreads = 256;
+static_assert(kRouteChunk % kRouteCountThreads == 0, "a count thread takes a whole number of ids");
 __global__ __launch_bounds__(kRouteCountThreads) void route_count_kernel(const int32_t* __restrict__ ids, int n,
                                                                          int E, int32_t* chunk_counts) {
   extern __shared__ int hist[];   // [E]
@@ -197,10 +206,16 @@ __global__ __launch_bounds__(kRouteCountThreads) void route_count_kernel(const i
   for (int e = tid; e < E; e += kRouteCountThreads) hist[e] = 0;
   __syncthreads();
   const int lo = c * kRouteChunk, hi = min(n, lo + kRouteChunk);
-  for (int i = lo + tid; i < hi; i += kRouteCountThreads) {
-    const int e = ids[i];
-    if ((unsigned)e < (unsigned)E) atomicAdd(&hist[e], 1);
+  constexpr int kPer = kRouteChunk / kRouteCountThreads;   // ids per thread, all loaded before use
+  int ev[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = lo + tid + j * kRouteCountThreads;
+    ev[j] = i < hi ? ids[i] : -1;
   }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if ((unsigned)ev[j] < (unsigned)E) atomicAdd(&hist[ev[j]], 1);
   __syncthreads();
   for (int e = tid; e < E; e += kRouteCountThreads) chunk_counts[(size_t)c * E + e] = hist[e];
 }
@@ -214,9 +229,17 @@ __global__ __launch_bounds__(kRouteThreads) void route_scan_kernel(int32_t* chun
                                                                    int32_t* tiles_out, int32_t* ntiles_out) {
   extern __shared__ int counts[];   // [E]
   const int tid = threadIdx.x, lane = tid & 63;
+  // chunk counts in batches of 8 loads issued together (one round trip per batch)
+  constexpr int kB = 8;
   for (int e = tid; e < E; e += kRouteThreads) {
     int s = 0;
-    for (int c = 0; c < C; ++c) s += chunk_counts[(size_t)c * E + e];
+    for (int c0 = 0; c0 < C; c0 += kB) {
+      int v[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) v[j] = c0 + j < C ? chunk_counts[(size_t)(c0 + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kB; ++j) s += v[j];
+    }
     counts[e] = s;
   }
   __syncthreads();
@@ -224,10 +247,16 @@ __global__ __launch_bounds__(kRouteThreads) void route_scan_kernel(int32_t* chun
   __syncthreads();
   for (int e = tid; e < E; e += kRouteThreads) {
     int run = counts[e];
-    for (int c = 0; c < C; ++c) {
-      const int v = chunk_counts[(size_t)c * E + e];
-      chunk_counts[(size_t)c * E + e] = run;
-      run += v;
+    for (int c0 = 0; c0 < C; c0 += kB) {
+      int v[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) v[j] = c0 + j < C ? chunk_counts[(size_t)(c0 + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kB; ++j)
+        if (c0 + j < C) {
+          chunk_counts[(size_t)(c0 + j) * E + e] = run;
+          run += v[j];
+        }
     }
   }
 }

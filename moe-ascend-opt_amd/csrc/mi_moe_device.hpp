@@ -166,6 +166,7 @@ __device__ inline void route_lds(const int32_t* __restrict__ ids, int n, int K,
   __syncthreads();
   for (int i = tid; i < n; i += blockDim.x) {
     const int e = ids[i];
+    scat[i] = e;   // the ranking below reads the ids from LDS (no second global read)
     if ((unsigned)e < (unsigned)E) atomicAdd(&counts[e], 1);
   }
   __syncthreads();
@@ -202,7 +203,7 @@ __device__ inline void route_lds(const int32_t* __restrict__ ids, int n, int K,
     while ((1 << nbits) < E) ++nbits;
     for (int b0 = 0; b0 < n; b0 += kWave) {
       const int i = b0 + lane;
-      const int e = (i < n) ? ids[i] : -1;
+      const int e = (i < n) ? scat[i] : -1;
       const bool valid = (i < n) && ((unsigned)e < (unsigned)E);
       uint64_t m = __ballot(valid);
       for (int bit = 0; bit < nbits; ++bit) {
