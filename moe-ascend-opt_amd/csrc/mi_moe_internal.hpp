@@ -40,8 +40,9 @@ constexpr int kGemmRows = 64;
 // scaling to more pairs than Q8_0's).
 inline int q_lpr_max_pairs(int quant) { return quant == 1 ? 160 : 96; }
 // Q8_0 / Q4_0 lane-per-row gate_up: up to this many routed pairs the work
-// items are pairs routed by one ballot per wave (grid = pairs x slices).
-constexpr int kQBallotMaxPairs = 64;
+// items are pairs routed by ballots over all ids (one per 64 ids; grid =
+// pairs x slices).
+constexpr int kQBallotMaxPairs = 192;
 __host__ __device__ inline int64_t gemm_tiles_max(int64_t n, int E) {
   return n / kGemmRows + (n < E ? n : E);
 }

@@ -73,4 +73,50 @@ __device__ __forceinline__ BallotCols ballot_cols(const SchedArgs& c, int pi, in
   return b;
 }
 
+// The same routing for up to 64 * NH pairs (lane l holds ids l, l + 64, ...):
+// work item pi serves its expert iff it is the expert's first pair; the
+// expert's pairs in ascending order (its columns) go to cols[0, cnt) in LDS,
+// written by wave 0 (the caller barriers before reading them).  Every wave
+// computes the same values.  Whole-workgroup routine.
+template <int NH>
+__device__ __forceinline__ bool ballot_route_n(const SchedArgs& c, int pi, int tid, int* cols, int& e_out,
+                                               int& cnt_out) {
+  const int lane = tid & 63;
+  int id[NH];
+  bool ok[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {   // all loads issued before any is used
+    const int i = 64 * h + lane;
+    id[h] = i < c.n ? c.ids[i] : -1;
+  }
+  int e = -1;
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    ok[h] = 64 * h + lane < c.n && (unsigned)id[h] < (unsigned)c.E;
+    const int v = __shfl(id[h], pi & 63);
+    if ((pi >> 6) == h) e = v;
+  }
+  uint64_t m[NH];
+  int cnt = 0, first = -1;
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    m[h] = __ballot(ok[h] && id[h] == e);
+    if (first < 0 && m[h]) first = 64 * h + __ffsll((long long)m[h]) - 1;
+    cnt += __popcll(m[h]);
+  }
+  const bool serve = (unsigned)e < (unsigned)c.E && first == pi;
+  if (serve && tid < kWave) {
+    const uint64_t lt = lanemask_lt(lane);
+    int off = 0;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      if ((m[h] >> lane) & 1) cols[off + __popcll(m[h] & lt)] = 64 * h + lane;
+      off += __popcll(m[h]);
+    }
+  }
+  e_out = e;
+  cnt_out = cnt;
+  return serve;
+}
+
 }  // namespace mimoe

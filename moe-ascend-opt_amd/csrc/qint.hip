@@ -374,7 +374,7 @@ __global__ __launch_bounds__(NW * kWave) void q_phase1_kernel(const int32_t* ids
   __shared__ int s_U;
   const QLds L = carve(smem, a.c.H);
   const int item = blockIdx.y, sl = blockIdx.x;   // grid (I/32 slices, items)
-  if (a.c.n <= kQBallotMaxPairs) {   // uniform
+  if (a.c.n <= kWave) {   // uniform: one ballot over all ids, no sort
     const int tid = threadIdx.x;
     const BallotCols cl = ballot_cols(a.c, item, tid & 63);   // every wave: same result
     if (!cl.serve) return;   // uniform
@@ -382,6 +382,17 @@ __global__ __launch_bounds__(NW * kWave) void q_phase1_kernel(const int32_t* ids
     __syncthreads();
     q_phase1<QT, ACT, SC, NW>(a, __builtin_amdgcn_readfirstlane(cl.e), __builtin_amdgcn_readfirstlane(cl.cnt),
                               L.route, sl, L);
+    return;
+  }
+  if (a.c.n <= kQBallotMaxPairs) {   // uniform: ballots over 2-3 batches of 64 ids
+    const int tid = threadIdx.x;
+    int e, cnt;
+    const bool serve = a.c.n <= 128 ? ballot_route_n<2>(a.c, item, tid, L.route, e, cnt)
+                                    : ballot_route_n<3>(a.c, item, tid, L.route, e, cnt);
+    if (!serve) return;   // uniform
+    __syncthreads();
+    q_phase1<QT, ACT, SC, NW>(a, __builtin_amdgcn_readfirstlane(e), __builtin_amdgcn_readfirstlane(cnt), L.route,
+                              sl, L);
     return;
   }
   const RouteView rv = sched_route(a.c, L.route, &s_U);

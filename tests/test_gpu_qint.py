@@ -83,6 +83,28 @@ def test_forward_parity_small(cuda, qt, T, K):
 
 
 @pytest.mark.parametrize("qt", [0, 1])
+@pytest.mark.parametrize("T,K", [(150, 1), (70, 1), (16, 10)])
+def test_ballot_routing_concentrated(cuda, qt, T, K):
+    """Lane-per-row gate_up with the ballot routing over 2-3 batches of 64 ids
+    (65-192 routed pairs), K = 1 with one expert taking more than 64 columns:
+    Q4_0 at 150 / 70 / 160 pairs and Q8_0 at 70 pairs stay on the lane-per-row
+    kernels (Q8_0 at 150 and 160 pairs takes the grouped GEMMs).  Three
+    quarters of the tokens put their first pick on expert 3, and some ids are
+    out of range."""
+    E, H, I = 16, 256, 128
+    w = _weights(qt, E, H, I, seed=20 + qt)
+    h = _handle(qt, E, H, I, w, True, cuda)
+    ids, tw = topk_routing(T, E, K, seed=T + K)
+    ids = ids.clone()
+    ids[: (3 * T) // 4, 0] = 3
+    ids[T - 2, 0] = -1
+    ids[T - 1, K - 1] = E
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
+    y = _run(h, x, ids, tw, cuda)
+    assert max_rel_err(y, _oracle(qt, x, ids, tw, w, E, I)) <= TOL
+
+
+@pytest.mark.parametrize("qt", [0, 1])
 def test_forward_dtypes_and_invalid_ids(cuda, qt):
     E, H, I, T, K = 8, 192, 96, 6, 8
     w = _weights(qt, E, H, I, seed=3, sdt=torch.bfloat16)
