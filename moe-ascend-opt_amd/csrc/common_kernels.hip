@@ -328,17 +328,30 @@ __global__ void combine_kernel(const float* __restrict__ eout, const float* __re
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int t = (int)(idx / H4), h = (int)(idx - (int64_t)t * H4) * 4;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k = 0; k < K; ++k) {
-      const int i = t * K + k;
-      const int e = ids[i];
-      if ((unsigned)e >= (unsigned)E) continue;
-      const float w = tw[i];
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(eout + (size_t)i * H + h);
-      const float vv[4] = {v.x, v.y, v.z, v.w};
+    // 8 pairs at a time: their ids, weights and rows are loaded together (the
+    // row of a pair with an invalid id is read but not used), then added in k
+    // order
+    constexpr int kB = 8;
+    for (int k0 = 0; k0 < K; k0 += kB) {
+      int ev[kB];
+      float wv[kB];
+      f32x4_t rv[kB];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float prod = w * vv[j];
-        acc[j] = acc[j] + prod;
+      for (int j = 0; j < kB; ++j) {
+        const int i = t * K + min(k0 + j, K - 1);
+        ev[j] = k0 + j < K ? ids[i] : -1;
+        wv[j] = tw[i];
+        rv[j] = *reinterpret_cast<const f32x4_t*>(eout + (size_t)i * H + h);
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        if ((unsigned)ev[j] >= (unsigned)E) continue;
+        const float vv[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float prod = wv[j] * vv[q];
+          acc[q] = acc[q] + prod;
+        }
       }
     }
     const uint32_t lo = from_f32<ACT>(acc[0]) | ((uint32_t)from_f32<ACT>(acc[1]) << 16);
