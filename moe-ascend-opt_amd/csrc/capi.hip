@@ -38,6 +38,8 @@ hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*,
 W4Plan w4a16_plan(int, int);
 hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
+W4FusedPlan w4a16_fused_plan(int, int, int, int, int, int);
+hipError_t launch_w4a16_fused(const W4Args&, const W4FusedPlan&, int, hipStream_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, bool, hipStream_t);
 hipError_t launch_qint_gemm(const QArgs&, int, int, int, hipStream_t);
 hipError_t launch_quant_route(const void*, int, int64_t, int64_t, int8_t*, float*, const int32_t*, int, int, int,
@@ -126,6 +128,7 @@ struct mi_moe_handle {
   bool mid_recorded = false;
   // weights (device layout)
   DevBuf w13, w13_s, w13_z, w2, w2_s, w2_z;
+  DevBuf tact;   // tagged_act_bytes(I): act hand-over units of the one-launch decode kernel
   // workspace
   int64_t cap_T = 0, cap_n = 0;
   DevBuf act, eout, act_d, r_counts, r_starts, r_active, r_tok, r_scat, r_U, r_tiles, r_ntiles;
@@ -202,6 +205,7 @@ struct Work {
   float* eout = nullptr;    // [n, H] per-pair outputs (paths with a separate combine)
   int8_t* xq = nullptr;     // [T, H] Q8_0 activations (int8 grouped GEMMs)
   float* xd = nullptr;      // [T, H/32]
+  unsigned long long* tact = nullptr; // tagged act units of the one-launch decode kernel
   RouteGlobal rg{};
 };
 
@@ -230,6 +234,10 @@ int init_scratch(int dev) {
   const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess || p == nullptr)
     return fail(MI_MOE_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+  // the one-launch decode units at the head start zeroed (no dispatch has tag 0)
+  const hipError_t ez = hipMemset(p, 0, tagged_act_bytes(kTagActMaxI));
+  if (ez != hipSuccess)
+    return fail(MI_MOE_EHIP, "clearing the no-alloc scratch head failed on device %d: %s", dev, hipGetErrorString(ez));
   g_scratch_ptr[dev] = p;
   return MI_MOE_OK;
 }
@@ -243,7 +251,8 @@ void* scratch_of(int dev) {
 // Slices of one call's workspace laid out from base (256-byte aligned);
 // returns the bytes taken.  With base == nullptr it only measures.
 size_t carve_work(unsigned char* base, const mi_moe_handle* h, int64_t T, int64_t n, bool need_eout, Work& w) {
-  size_t off = 0;
+  size_t off = tagged_act_bytes(kTagActMaxI);   // the head holds the one-launch decode units
+  w.tact = base ? (unsigned long long*)base : nullptr;
   auto take = [&](size_t bytes) -> void* {
     void* p = base ? base + off : nullptr;
     off += (bytes + 255) & ~(size_t)255;
@@ -280,6 +289,7 @@ int get_work(mi_moe_handle* h, int64_t T, int64_t n, bool need_eout, bool noallo
     w.eout = (float*)h->eout.p;
     w.xq = (int8_t*)h->xq.p;
     w.xd = (float*)h->xd.p;
+    w.tact = (unsigned long long*)h->tact.p;
     w.rg = route_view(h);
     return MI_MOE_OK;
   }
@@ -325,6 +335,7 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
   a.w2 = h->w2.p; a.w2_m = (const unsigned char*)h->w2_s.p;
   a.act = (uint16_t*)w.act;
   a.sdt = h->scale_dtype;
+  a.tact = w.tact;
   hipEvent_t mid = h->timing && !noalloc ? h->evmid : nullptr;
   if (decode) {
     // phase 1 copies the hidden rows of every token when they are few
@@ -334,6 +345,12 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
     // keeps the LDS small (occupancy), extra columns take another pass
     a.p1_cols = (int)(T < kDecodeCols ? T : kDecodeCols);
     while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1, nw1) > lmax) --a.p1_cols;
+    // one launch (gate_up hands act to down inside it) for top-k <= 8
+    const W4FusedPlan fp = w4a16_fused_plan((int)T, (int)K, (int)h->H, (int)h->I, a.x_all, a.p1_cols);
+    if (fp.ok && a.tact) {
+      HIPCHK(launch_w4a16_fused(a, fp, act, st));
+      return MI_MOE_OK;
+    }
     const W4Plan plan = w4a16_plan((int)h->H, (int)h->I);
     HIPCHK(launch_w4a16(a, plan, act, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st, mid));
     h->mid_recorded = mid != nullptr;
@@ -489,6 +506,13 @@ MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe
     delete h;
     return fail(MI_MOE_EHIP, "HIP device query / event creation failed");
   }
+  // the one-launch decode units (zeroed: no dispatch has tag 0)
+  if (I <= kTagActMaxI && quant_type == MI_MOE_W4A16 &&
+      (h->tact.alloc(tagged_act_bytes((int)I)) != hipSuccess ||
+       hipMemset(h->tact.p, 0, tagged_act_bytes((int)I)) != hipSuccess)) {
+    mi_moe_destroy(h);
+    return fail(MI_MOE_EHIP, "allocating the decode hand-over buffer failed");
+  }
   // the no-alloc entry point's scratch address on this device (once per device)
   if (init_scratch(h->device) != MI_MOE_OK) {
     const std::string msg = g_err;
@@ -505,7 +529,7 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
   DevBuf* bufs[] = {&h->w13, &h->w13_s, &h->w13_z, &h->w2, &h->w2_s, &h->w2_z,
                     &h->act, &h->eout, &h->act_d, &h->r_counts, &h->r_starts,
                     &h->r_active, &h->r_tok, &h->r_scat, &h->r_U, &h->r_tiles, &h->r_ntiles,
-                    &h->xq, &h->xd, &h->r_chunk, &h->r_rids, &h->r_rw};
+                    &h->xq, &h->xd, &h->r_chunk, &h->r_rids, &h->r_rw, &h->tact};
   for (DevBuf* b : bufs) b->release();
   if (h->ev0) (void)hipEventDestroy(h->ev0);
   if (h->ev1) (void)hipEventDestroy(h->ev1);

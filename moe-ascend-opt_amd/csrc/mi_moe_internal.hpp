@@ -76,6 +76,7 @@ struct W4Args {
   int p1_cols;                 // phase-1 token columns per pass (rows staged in LDS)
   int sdt;                     // scale dtype: 1 bf16, 0 fp16
   int x_all;                   // phase 1 copies the hidden rows of all T tokens at start
+  unsigned long long* tact;    // one-launch decode: tagged act units (tagged_act_bytes(I))
 };
 
 // Bytes of the w2 metadata of one 16-row tile: G2 = I/128 groups of 16 u16
@@ -108,6 +109,35 @@ inline int w4_p1_waves(int64_t n, int H) {
 __host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) {
   return (size_t)K * I * 2 + (size_t)K * RT * w2_meta_sec_bytes(I >> 7) + (size_t)K * 16 * RT * 4 + (size_t)K * 4;
 }
+
+// One-launch W4A16 decode kernel (w4a16_fused.hip): 8-wave workgroups; gate_up
+// items take 8 / NW slices of 16 rows of I with NW waves splitting H each, down
+// items a wave per routed expert (top-k <= 8).
+constexpr int kW4FusedWaves = 8;
+// Up to this many routed pairs the one-launch kernel serves the decode path
+// (measured faster than two launches there; above it the gate_up tail and the
+// down workgroups' 2-per-CU occupancy cost more than the saved launch).
+constexpr int kW4FusedMaxPairs = 32;
+// Its hand-over buffer (per handle, and the head of the no-alloc scratch):
+// u64 units [64 pairs][I/2] of (dispatch tag << 32 | two act values), then
+// one u64 that records a wait that gave up.  A unit is valid for a call iff
+// it carries that dispatch's tag, so the buffer is never cleared; it starts
+// zeroed (no dispatch has tag 0).  The one-launch kernel serves I <= kTagActMaxI.
+constexpr int kTagActMaxI = 4096;
+__host__ __device__ constexpr size_t tagged_act_bytes(int I) { return (size_t)64 * I * 4 + 64; }
+inline size_t w4_fused_gate_up_lds_bytes(int H, int xrows, int NW) {
+  return (size_t)(kW4FusedWaves / NW) * (p1_red_bytes(NW) + 80 * (H >> 7)) + (size_t)xrows * H * 2;
+}
+// act rows [8][I] | w2 metadata [8][SEC] | outputs [8][16] f32 | state [8]
+inline size_t w4_fused_down_lds_bytes(int I) {
+  return (size_t)kW4FusedWaves * ((size_t)I * 2 + w2_meta_sec_bytes(I >> 7) + 16 * 4 + 4);
+}
+struct W4FusedPlan {
+  int ok;          // the one-launch kernel serves the call
+  int nw, njs;     // gate_up: waves splitting H per slice (8 or 4), slice blocks per item
+  int nb1, nb2;    // load batches (groups) of the gate_up and down roles
+  size_t lds;
+};
 
 // W4A16 decode path: both kernels fit in `lds` bytes (phase 1 with one token
 // column per pass).

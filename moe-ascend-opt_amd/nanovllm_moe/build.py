@@ -23,7 +23,7 @@ SHIM = os.path.join(PKG_DIR, "libnanovllm_shim.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["capi.hip", "common_kernels.hip", "w4a16.hip", "qint.hip", "hybrid.hip"]
+HIP_SOURCES = ["capi.hip", "common_kernels.hip", "w4a16.hip", "w4a16_fused.hip", "qint.hip", "hybrid.hip"]
 # Host-only C++ (no HIP): the host executor of the hybrid offload path and the
 # CPU engine of the Q8_0 / Q4_0 layer (its C ABI too).  Inner loops are
 # compiled per instruction set (target attributes) and picked at run time;
@@ -44,6 +44,7 @@ NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # scalar arguments (a by-value struct is not preloaded).
 FILE_FLAGS = {"qint.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
               "w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
+              "w4a16_fused.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
               "common_kernels.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
@@ -75,8 +76,9 @@ def build_lib(verbose: bool = False) -> str:
         return obj, _run(cmd)
 
     cpp = [s for s in CPP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    with ThreadPoolExecutor(max_workers=4) as ex:
-        results = list(ex.map(compile_one, srcs)) + list(ex.map(compile_cpp, cpp))
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
+        jobs = [ex.submit(compile_one, s) for s in srcs] + [ex.submit(compile_cpp, s) for s in cpp]
+        results = [j.result() for j in jobs]
     tmp = LIB + ".tmp"
     out = _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for o, _ in results], "-o", tmp,
                 "-pthread"])
