@@ -38,7 +38,7 @@ hipError_t launch_quant_act(const void*, int, int64_t, int64_t, int8_t*, float*,
 W4Plan w4a16_plan(int, int);
 hipError_t launch_w4a16(const W4Args&, const W4Plan&, int, int, int, hipStream_t, hipEvent_t);
 hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
-W4FusedPlan w4a16_fused_plan(int, int, int, int, int, int);
+W4FusedPlan w4a16_fused_plan(int, int, int, int, int, int, int);
 hipError_t launch_w4a16_fused(const W4Args&, const W4FusedPlan&, int, hipStream_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, bool, hipStream_t);
 hipError_t launch_qint_gemm(const QArgs&, int, int, int, hipStream_t);
@@ -346,7 +346,7 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
     a.p1_cols = (int)(T < kDecodeCols ? T : kDecodeCols);
     while (!a.x_all && a.p1_cols > 1 && w4_p1_lds_bytes((int)h->H, a.p1_cols, 1, nw1) > lmax) --a.p1_cols;
     // one launch (gate_up hands act to down inside it) for top-k <= 8
-    const W4FusedPlan fp = w4a16_fused_plan((int)T, (int)K, (int)h->H, (int)h->I, a.x_all, a.p1_cols);
+    const W4FusedPlan fp = w4a16_fused_plan((int)T, (int)K, (int)h->H, (int)h->I, a.x_all, a.p1_cols, h->num_cu);
     if (fp.ok && a.tact) {
       HIPCHK(launch_w4a16_fused(a, fp, act, st));
       return MI_MOE_OK;

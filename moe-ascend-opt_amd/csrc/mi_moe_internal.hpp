@@ -114,10 +114,9 @@ __host__ __device__ inline size_t w4_down_token_lds_bytes(int I, int K, int RT) 
 // items take 8 / NW slices of 16 rows of I with NW waves splitting H each, down
 // items a wave per routed expert (top-k <= 8).
 constexpr int kW4FusedWaves = 8;
-// Up to this many routed pairs the one-launch kernel serves the decode path
-// (measured faster than two launches there; above it the gate_up tail and the
-// down workgroups' 2-per-CU occupancy cost more than the saved launch).
-constexpr int kW4FusedMaxPairs = 32;
+// The one-launch kernel serves the whole decode path (up to 64 routed pairs,
+// top-k <= 8); the two-launch kernels serve top-k 9-16.
+constexpr int kW4FusedMaxPairs = 64;
 // Its hand-over buffer (per handle, and the head of the no-alloc scratch):
 // u64 units [64 pairs][I/2] of (dispatch tag << 32 | two act values), then
 // one u64 that records a wait that gave up.  A unit is valid for a call iff
@@ -128,14 +127,15 @@ __host__ __device__ constexpr size_t tagged_act_bytes(int I) { return (size_t)64
 inline size_t w4_fused_gate_up_lds_bytes(int H, int xrows, int NW) {
   return (size_t)(kW4FusedWaves / NW) * (p1_red_bytes(NW) + 80 * (H >> 7)) + (size_t)xrows * H * 2;
 }
-// act rows [8][I] | w2 metadata [8][SEC] | outputs [8][16] f32 | state [8]
-inline size_t w4_fused_down_lds_bytes(int I) {
-  return (size_t)kW4FusedWaves * ((size_t)I * 2 + w2_meta_sec_bytes(I >> 7) + 16 * 4 + 4);
+// act rows [8][I] | w2 metadata [8][RT][SEC] | outputs [8][16 RT] f32 | state [8]
+inline size_t w4_fused_down_lds_bytes(int I, int RT) {
+  return (size_t)kW4FusedWaves * ((size_t)I * 2 + (size_t)RT * (w2_meta_sec_bytes(I >> 7) + 16 * 4) + 4);
 }
 struct W4FusedPlan {
   int ok;          // the one-launch kernel serves the call
   int nw, njs;     // gate_up: waves splitting H per slice (8 or 4), slice blocks per item
   int nb1, nb2;    // load batches (groups) of the gate_up and down roles
+  int rt;          // 16-row tiles of H per down item (1 or 2)
   size_t lds;
 };
 

@@ -188,24 +188,26 @@ __device__ __forceinline__ void fused_gate_up(const SchedArgs& c, const W4Args& 
 }
 
 // ---------------------------------------------------------------- down role
-// LDS: act rows [8][I] | metadata [8][SEC] | outputs [8][16] f32 | state [8].
-template <int ACT, int SDT, int NB>
+// Down item (token t, RT consecutive 16-row tiles of H from tile0, within one
+// quad of 64 rows).  LDS: act rows [8][I] | metadata [8][RT][SEC] | outputs
+// [8][16 RT] f32 | state [8].
+template <int ACT, int SDT, int NB, int RT>
 __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, const char* w2,
-                                           const unsigned char* w2_m, int t, int tile, unsigned char* smem) {
+                                           const unsigned char* w2_m, int t, int tile0, unsigned char* smem) {
   const int K = c.K, E = c.E, H = c.H, I = c.I;
-  const int MQ = H >> 6, G2 = I >> 7, II = I >> 3, SEC = w2_meta_sec_bytes(G2);
-  const int m = tile >> 2, jj = tile & 3;
+  const int MQ = H >> 6, G2 = I >> 7, SEC = w2_meta_sec_bytes(G2);
+  const int m = tile0 >> 2, jj = tile0 & 3;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int q = lane >> 4, r = lane & 15;
   const unsigned lane16 = 16u * (unsigned)lane;
   uint16_t* as = reinterpret_cast<uint16_t*>(smem);
   unsigned char* meta = smem + (size_t)kFusedWaves * I * 2;
-  float* outs = reinterpret_cast<float*>(meta + (size_t)kFusedWaves * SEC);
-  int* state = reinterpret_cast<int*>(outs + 16 * kFusedWaves);   // 0 invalid id, 1 valid, 2 wait gave up
+  float* outs = reinterpret_cast<float*>(meta + (size_t)kFusedWaves * RT * SEC);
+  int* state = reinterpret_cast<int*>(outs + 16 * RT * kFusedWaves);   // 0 invalid id, 1 valid, 2 wait gave up
   constexpr float off = W4Consts<ACT>::offset;
-  // the combine's routing weights, loaded now (lanes 0-15 of wave 0 sum the tile)
+  // the combine's routing weights, loaded now (threads < 16 RT sum the tiles)
   float tw[kW4FusedWaves];
-  if (tid < 16)
+  if (tid < 16 * RT)
 #pragma unroll
     for (int k = 0; k < kW4FusedWaves; ++k) tw[k] = k < K ? c.tw[t * K + k] : 0.0f;
   if (wave < K) {   // uniform: wave k takes routed expert k of token t
@@ -213,14 +215,16 @@ __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, 
     const int e = __builtin_amdgcn_readfirstlane(c.ids[i]);
     // an invalid id computes on expert 0 and its output is ignored
     const bool ok = (unsigned)e < (unsigned)E;
-    const size_t sec0 = ((size_t)(ok ? e : 0) * MQ + m) * 4 + jj;
-    unsigned char* mdst = meta + wave * SEC;
-    for (int l = lane; l < SEC / 16; l += 64)
+    const size_t sec0 = ((size_t)(ok ? e : 0) * MQ + m) * 4 + jj;   // the RT tiles: contiguous
+    unsigned char* mdst = meta + wave * RT * SEC;
+    for (int l = lane; l < RT * SEC / 16; l += 64)
       __builtin_amdgcn_global_load_lds(w2_m + sec0 * SEC + 16 * l, mdst + (l - lane) * 16, 16, 0, 0);
-    const char* wb = w2 + sec0 * G2 * 1024 + lane16;
-    u32x4_t wv[NB];
+    const char* wb = w2 + sec0 * G2 * 1024 + lane16;   // tile rt: + rt * G2 KB
+    u32x4_t wv[RT][NB];
 #pragma unroll
-    for (int gi = 0; gi < NB; ++gi) wv[gi] = ldg16(wb + (size_t)gi * 1024);   // in flight during the wait
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int gi = 0; gi < NB; ++gi) wv[rt][gi] = ldg16(wb + (size_t)(rt * G2 + gi) * 1024);   // in flight during the wait
     int st = ok ? 1 : 0;
     if (ok) {
       // act row i: I/2 tagged units; slice j's units are the line at unit 8j.
@@ -268,12 +272,15 @@ __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, 
     __builtin_amdgcn_s_waitcnt(0);   // this wave's metadata and first weights
     issue_order_fence();
     const uint16_t* arow = as + (size_t)wave * I + 8 * q;
-    const unsigned char* sec = mdst;
-    f32x4_t acc = {0, 0, 0, 0};
+    f32x4_t acc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0, 0, 0, 0};
     for (int gb = 0; gb < G2; gb += NB) {
       if (gb > 0) {
 #pragma unroll
-        for (int gi = 0; gi < NB; ++gi) wv[gi] = ldg16(wb + (size_t)(gb + gi) * 1024);
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int gi = 0; gi < NB; ++gi) wv[rt][gi] = ldg16(wb + (size_t)(rt * G2 + gb + gi) * 1024);
       }
 #pragma unroll
       for (int gi = 0; gi < NB; ++gi) {
@@ -284,18 +291,24 @@ __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, 
         f32x4_t X = {0, 0, 0, 0};
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) X = mfma16<ACT>(A[cc], ones4<ACT>(), X);
-        f32x4_t G = {0, 0, 0, 0};
-        const uint32_t ww[4] = {wv[gi].x, wv[gi].y, wv[gi].z, wv[gi].w};
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) G = mfma16<ACT>(A[cc], deq4<ACT>(ww[cc]), G);
-        fold(acc, G, X, scale_of<SDT>(reinterpret_cast<const uint16_t*>(sec)[16 * g2 + r]),
-             off + w2_zero(sec, G2, g2, r));
+        for (int rt = 0; rt < RT; ++rt) {
+          f32x4_t G = {0, 0, 0, 0};
+          const uint32_t ww[4] = {wv[rt][gi].x, wv[rt][gi].y, wv[rt][gi].z, wv[rt][gi].w};
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) G = mfma16<ACT>(A[cc], deq4<ACT>(ww[cc]), G);
+          const unsigned char* sec = mdst + rt * SEC;
+          fold(acc[rt], G, X, scale_of<SDT>(reinterpret_cast<const uint16_t*>(sec)[16 * g2 + r]),
+               off + w2_zero(sec, G2, g2, r));
+        }
       }
     }
-    if (lane < 16) outs[16 * wave + lane] = acc.x;   // column 0: lanes (r, q = 0)
+    if (lane < 16)   // column 0: lanes (r, q = 0)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) outs[16 * (RT * wave + rt) + lane] = acc[rt].x;
   }
   __syncthreads();
-  if (tid < 16) {
+  if (tid < 16 * RT) {
     float yv = 0.0f;
     bool gave_up = false;
 #pragma unroll
@@ -303,11 +316,11 @@ __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, 
       const int s = k < K ? state[k] : 0;
       if (s) {
         gave_up |= s == 2;
-        const float prod = tw[k] * outs[16 * k + tid];
+        const float prod = tw[k] * outs[16 * RT * k + tid];
         yv = yv + prod;
       }
     }
-    c.y[(size_t)t * H + 16 * tile + tid] = gave_up ? (uint16_t)0x7fc0u : from_f32<ACT>(yv);
+    c.y[(size_t)t * H + 16 * tile0 + tid] = gave_up ? (uint16_t)0x7fc0u : from_f32<ACT>(yv);
   }
 }
 
@@ -316,7 +329,7 @@ __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, 
 // kernel-argument dwords into SGPRs at wave launch
 // (-amdgpu-kernarg-preload-count), so the role choice, the ids read and the
 // weight addresses do not wait for an argument fetch.
-template <int ACT, int SDT, int NB1, int NW, int S, int NB2>
+template <int ACT, int SDT, int NB1, int NW, int S, int NB2, int RT>
 __global__ __launch_bounds__(kW4FusedWaves * kWave) __attribute__((amdgpu_waves_per_eu(4)))
 void w4a16_decode_kernel(const int32_t* ids, const uint16_t* x, const char* w13, const unsigned char* w13_m,
                          const char* w2, const unsigned char* w2_m, int n1, int njs, W4Args a) {
@@ -329,31 +342,31 @@ void w4a16_decode_kernel(const int32_t* ids, const uint16_t* x, const char* w13,
     const int item = b / njs;
     fused_gate_up<ACT, SDT, NB1, NW, S>(c, a, w13, w13_m, item, b - item * njs, smem);
   } else {
-    const int nt = c.H >> 4, d = b - n1, t = d / nt;
-    fused_down<ACT, SDT, NB2>(c, a, w2, w2_m, t, d - t * nt, smem);
+    const int nt = (c.H >> 4) / RT, d = b - n1, t = d / nt;
+    fused_down<ACT, SDT, NB2, RT>(c, a, w2, w2_m, t, RT * (d - t * nt), smem);
   }
 }
 
-template <int ACT, int SDT, int NB1, int NW, int S, int NB2>
+template <int ACT, int SDT, int NB1, int NW, int S, int NB2, int RT>
 static hipError_t launch_fused_t(const W4Args& a, int njs, size_t lds, hipStream_t st) {
   if (lds > kMaxLds)
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_decode_kernel<ACT, SDT, NB1, NW, S, NB2>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_decode_kernel<ACT, SDT, NB1, NW, S, NB2, RT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  const int n1 = a.c.n * njs, n2 = a.c.T * (a.c.H >> 4);
-  hipLaunchKernelGGL((w4a16_decode_kernel<ACT, SDT, NB1, NW, S, NB2>), dim3(n1 + n2), dim3(kW4FusedWaves * kWave),
+  const int n1 = a.c.n * njs, n2 = a.c.T * (a.c.H >> 4) / RT;
+  hipLaunchKernelGGL((w4a16_decode_kernel<ACT, SDT, NB1, NW, S, NB2, RT>), dim3(n1 + n2), dim3(kW4FusedWaves * kWave),
                      lds, st, a.c.ids, a.c.x, (const char*)a.w13, a.w13_m, (const char*)a.w2, a.w2_m, n1, njs, a);
   return hipGetLastError();
 }
 
-template <int ACT, int SDT, int NW, int S>
+template <int ACT, int SDT, int NW, int S, int RT>
 static hipError_t dispatch_fused_nb(const W4Args& a, int nb1, int nb2, int njs, size_t lds, hipStream_t st) {
-#define FUSED_NB2(NB1_)                                                                    \
-  if (nb1 == NB1_) {                                                                       \
-    if (nb2 == 6) return launch_fused_t<ACT, SDT, NB1_, NW, S, 6>(a, njs, lds, st); \
-    if (nb2 == 4) return launch_fused_t<ACT, SDT, NB1_, NW, S, 4>(a, njs, lds, st); \
-    if (nb2 == 3) return launch_fused_t<ACT, SDT, NB1_, NW, S, 3>(a, njs, lds, st); \
-    if (nb2 == 2) return launch_fused_t<ACT, SDT, NB1_, NW, S, 2>(a, njs, lds, st); \
-    if (nb2 == 1) return launch_fused_t<ACT, SDT, NB1_, NW, S, 1>(a, njs, lds, st); \
+#define FUSED_NB2(NB1_)                                                                        \
+  if (nb1 == NB1_) {                                                                           \
+    if (nb2 == 6) return launch_fused_t<ACT, SDT, NB1_, NW, S, 6, RT>(a, njs, lds, st); \
+    if (nb2 == 4) return launch_fused_t<ACT, SDT, NB1_, NW, S, 4, RT>(a, njs, lds, st); \
+    if (nb2 == 3) return launch_fused_t<ACT, SDT, NB1_, NW, S, 3, RT>(a, njs, lds, st); \
+    if (nb2 == 2) return launch_fused_t<ACT, SDT, NB1_, NW, S, 2, RT>(a, njs, lds, st); \
+    if (nb2 == 1) return launch_fused_t<ACT, SDT, NB1_, NW, S, 1, RT>(a, njs, lds, st); \
   }
   FUSED_NB2(1) FUSED_NB2(2) FUSED_NB2(3) FUSED_NB2(4)
 #undef FUSED_NB2
@@ -362,8 +375,9 @@ static hipError_t dispatch_fused_nb(const W4Args& a, int nb1, int nb2, int njs, 
 
 template <int ACT, int SDT>
 static hipError_t dispatch_fused(const W4Args& a, const W4FusedPlan& p, hipStream_t st) {
-  if (p.nw == 8) return dispatch_fused_nb<ACT, SDT, 8, 1>(a, p.nb1, p.nb2, p.njs, p.lds, st);
-  return dispatch_fused_nb<ACT, SDT, 4, 2>(a, p.nb1, p.nb2, p.njs, p.lds, st);
+  if (p.nw == 8) return dispatch_fused_nb<ACT, SDT, 8, 1, 1>(a, p.nb1, p.nb2, p.njs, p.lds, st);
+  if (p.rt == 2) return dispatch_fused_nb<ACT, SDT, 4, 2, 2>(a, p.nb1, p.nb2, p.njs, p.lds, st);
+  return dispatch_fused_nb<ACT, SDT, 4, 2, 1>(a, p.nb1, p.nb2, p.njs, p.lds, st);
 }
 
 // largest of {1, 2, 3, 4, 6} (up to cap) that divides need
@@ -375,7 +389,11 @@ static int fused_batch(int need, int cap) {
   return b;
 }
 
-W4FusedPlan w4a16_fused_plan(int T, int K, int H, int I, int x_all, int p1_cols) {
+// Slots: workgroups resident at once (2 per CU at the kernel's register
+// budget).  Down items take 2 tiles where that makes every workgroup of the
+// call resident at once, or where 1-tile items would need more than one round
+// of slots; otherwise 1 (more items in flight).
+W4FusedPlan w4a16_fused_plan(int T, int K, int H, int I, int x_all, int p1_cols, int num_cu) {
   W4FusedPlan p{};
   const int n = T * K, G1 = H / 128, G2 = I / 128;
   p.nw = (n <= kW4WideMaxPairs && G1 % 8 == 0) ? 8 : 4;
@@ -383,8 +401,11 @@ W4FusedPlan w4a16_fused_plan(int T, int K, int H, int I, int x_all, int p1_cols)
   p.njs = (I / 16) / S;
   p.nb1 = fused_batch(G1 / p.nw, 4);
   p.nb2 = fused_batch(G2, 6);
+  const long slots = 2L * num_cu, n1 = (long)n * p.njs, tiles = (long)T * (H / 16);
+  p.rt = 1;
+  if (p.nw == 4 && (H / 16) % 2 == 0 && (tiles > slots || (n1 + tiles > slots && n1 + tiles / 2 <= slots))) p.rt = 2;
   const size_t gate_up = w4_fused_gate_up_lds_bytes(H, x_all ? T : p1_cols, p.nw);
-  const size_t down = w4_fused_down_lds_bytes(I);
+  const size_t down = w4_fused_down_lds_bytes(I, p.rt);
   p.lds = gate_up > down ? gate_up : down;
   p.ok = K <= kW4FusedWaves && n <= kW4FusedMaxPairs && G1 % p.nw == 0 && (I / 16) % S == 0 && I <= kTagActMaxI &&
          p.lds <= device_max_lds();
