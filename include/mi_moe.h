@@ -109,7 +109,14 @@ int mi_moe_store_awq(mi_moe_handle* h, const int32_t* w13_qweight,
  *             (Int8-gemm/moe_common.cpp:158,175-181); a token with no valid
  *             id gets y = 0.
  * Stream-ordered and asynchronous.  Calls that overlap on one handle race on
- * its workspace (the reference is likewise not re-entrant). */
+ * its workspace (the reference is likewise not re-entrant).
+ * Graph capture: a call can be captured into a HIP graph once the handle's
+ * workspace holds it (an earlier call of at least its size, or
+ * mi_moe_reserve); decode calls (T*K <= 64, top-k <= 8) need no workspace at
+ * all.  Once a call on the handle has been captured, workspace that a later,
+ * larger call outgrows is kept until mi_moe_destroy instead of being freed,
+ * so captured graphs stay valid through eager calls of any size.  A graph
+ * must not outlive its handle. */
 int mi_moe_forward(mi_moe_handle* h, const void* x, void* y,
                    const float* topk_w, const int32_t* topk_ids, int64_t T,
                    int64_t K, int act_dtype, void* stream);
@@ -136,14 +143,17 @@ int mi_moe_forward_noalloc(mi_moe_handle* h, const void* x, void* y,
                            const float* topk_w, const int32_t* topk_ids,
                            int64_t T, int64_t K, int act_dtype, void* stream);
 
-/* Wall time of the last mi_moe_forward on the handle, in ms, measured with
- * HIP events around its launches (synchronizes on the end event).
+/* Wall time of the last timed mi_moe_forward on the handle, in ms, measured
+ * with HIP events around its launches (synchronizes on the end event).
  * Replaces MoEInfer::get_last_run_time_ms (Int8-gemm/moe_infer.h:23,
- * Int8-gemm/moe_infer.cpp:439-455).  Returns a negative value if timing is
- * off or no call was made. */
+ * Int8-gemm/moe_infer.cpp:439-455).  Timing is off by default (see
+ * mi_moe_set_timing); returns a negative value if it is off or no timed call
+ * was made. */
 double mi_moe_get_last_run_time_ms(mi_moe_handle* h);
 
-/* Enable (1) / disable (0) the per-call HIP-event timing (default 1). */
+/* Enable (1) / disable (0) the per-call HIP-event timing.  Default 0: a
+ * forward records no events unless a caller asks for timing, so serving calls
+ * pay nothing for it. */
 int mi_moe_set_timing(mi_moe_handle* h, int enable);
 
 /* Grow the handle's device workspace to hold a call of T tokens at top_k K
@@ -154,9 +164,12 @@ int mi_moe_set_timing(mi_moe_handle* h, int enable);
  * staging for num_tokens x top_k. */
 int mi_moe_reserve(mi_moe_handle* h, int64_t T, int64_t K, void* stream);
 
-/* Per-launch-phase times of the last timed mi_moe_forward, in ms: W4A16
- * fills ms[0] = routing + gate_up (+SiLU) launch(es), ms[1] = down (+combine)
- * launch(es) and returns 2; the integer path returns 1 (whole call).
+/* Per-launch-phase times of the last timed mi_moe_forward, in ms: calls with
+ * two launch phases (the W4A16 sorted path and the top-k 9-16 decode path)
+ * fill ms[0] = routing + gate_up (+SiLU) launch(es), ms[1] = down (+combine)
+ * launch(es) and return 2; the one-launch W4A16 decode kernel and the integer
+ * path return 1 (whole call).  mi_moe_forward_noalloc leaves the record of the
+ * last timed call unchanged.
  * Synchronizes on the end event.  No counterpart in the reference (its timer
  * covers the whole op); it is the measurement hook behind the per-kernel
  * roofline figures. */
@@ -213,6 +226,13 @@ int mi_moe_block_dots_mfma(mi_moe_handle* h, int64_t expert, int proj,
 int mi_moe_topk_softmax(const void* logits, int logits_dtype, int64_t T,
                         int64_t E, int64_t K, int renormalize,
                         int32_t* topk_ids, float* topk_w, void* stream);
+
+/* mi_moe_topk_softmax on host memory and host cores: fp32 logits [T,E] ->
+ * topk_ids [T,K], topk_w [T,K].  The same picks and weights as the device
+ * kernel, bit for bit (non-NaN logits).  Replaces make_topk_from_logits_cpu
+ * (Int8-gemm/test/fused_moe_cpu.py:20-37) for the CPU dispatch key. */
+int mi_moe_cpu_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t K,
+                            int renormalize, int32_t* topk_ids, float* topk_w);
 
 /* Router top-k + softmax followed by mi_moe_forward on the same stream:
  * router_logits [T,E] with E the handle's expert count.  The picks go to
@@ -335,7 +355,10 @@ int mi_moe_hybrid_store_awq(mi_moe_hybrid* hh, const int32_t* w13_qweight,
  * mi_moe_forward.  Growing the staging buffers synchronizes the streams; a
  * call can be captured into a HIP graph once a call of at least its size has
  * been made (under capture a call that would grow returns MI_MOE_EINVAL), and
- * the graph must not outlive the handle.  If a host pass fails (out of host
+ * the graph must not outlive the handle.  A captured call's host callback
+ * reads the staging buffers the graph captured (staging outgrown after a
+ * capture is kept until destroy), and its arguments belong to the graph (a
+ * HIP user object: freed with the graph).  If a host pass fails (out of host
  * memory) its partial is filled with NaN, so that call's y is NaN, and the
  * next mi_moe_hybrid_forward on the handle returns MI_MOE_EDEVICE. */
 int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y,

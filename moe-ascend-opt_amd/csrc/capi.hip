@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "mi_moe.h"
 #include "mi_moe_device.hpp"
@@ -87,6 +88,12 @@ struct DevBuf {
     p = nullptr;
     bytes = 0;
   }
+  // hand the allocation over to `keep` (freed later) instead of freeing it
+  void retire(std::vector<void*>& keep) {
+    if (p) keep.push_back(p);
+    p = nullptr;
+    bytes = 0;
+  }
   hipError_t alloc(size_t b) {
     release();
     if (b == 0) b = 256;
@@ -121,7 +128,7 @@ struct mi_moe_handle {
   int device = 0;
   int num_cu = 0;
   bool loaded = false;
-  bool timing = true;
+  bool timing = false;   // HIP events around each forward only when asked (mi_moe_set_timing)
   bool timed_once = false;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   hipEvent_t evmid = nullptr;   // between the gate_up and down launches (W4A16)
@@ -136,6 +143,11 @@ struct mi_moe_handle {
   DevBuf r_chunk;  // per-chunk expert counts of the multi-workgroup routing
   DevBuf r_rids, r_rw;   // router top-k ids / weights of mi_moe_forward_logits
   int64_t cap_r = 0;     // capacity of r_rids / r_rw in (t, k) entries
+  // A call captured into a HIP graph bakes the workspace addresses into the
+  // graph: workspace that was live during a capture is not freed when it
+  // grows but kept here until mi_moe_destroy, so such graphs stay valid.
+  bool captured = false;   // a forward on this handle has been captured
+  std::vector<void*> retired;
 };
 
 namespace {
@@ -165,8 +177,12 @@ int ensure_workspace(mi_moe_handle* h, int64_t T, int64_t n, hipStream_t st) {
   while (capT < T) capT *= 2;
   int64_t capn = h->cap_n ? h->cap_n : 128;
   while (capn < n) capn *= 2;
-  // buffers may be in use by queued work on this stream
+  // buffers may be in use by queued work on this stream, or by captured graphs
   HIPCHK(hipStreamSynchronize(st));
+  if (h->captured) {
+    for (DevBuf* b : {&h->act, &h->act_d, &h->eout, &h->r_tok, &h->r_scat, &h->r_tiles, &h->r_chunk, &h->xq, &h->xd})
+      b->retire(h->retired);
+  }
   HIPCHK(h->act.alloc((size_t)capn * h->I * 2));
   HIPCHK(h->act_d.alloc((size_t)capn * (h->I / 32) * sizeof(float)));
   HIPCHK(h->eout.alloc((size_t)capn * h->H * sizeof(float)));
@@ -353,13 +369,13 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
     }
     const W4Plan plan = w4a16_plan((int)h->H, (int)h->I);
     HIPCHK(launch_w4a16(a, plan, act, (int)(n * (h->I / 16)), (int)(T * (h->H / 16)), st, mid));
-    h->mid_recorded = mid != nullptr;
+    if (!noalloc) h->mid_recorded = mid != nullptr;   // a no-alloc call leaves the timed call's record
     return MI_MOE_OK;
   }
   // sorted path: routing with row tiles, the two grouped GEMMs, the combine
   HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
   HIPCHK(launch_w4a16_gemm(a, act, (int)gemm_tiles_max(n, (int)h->E), st, mid));
-  h->mid_recorded = mid != nullptr;
+  if (!noalloc) h->mid_recorded = mid != nullptr;
   HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
   return MI_MOE_OK;
 }
@@ -531,6 +547,7 @@ MI_API int mi_moe_destroy(mi_moe_handle* h) {
                     &h->r_active, &h->r_tok, &h->r_scat, &h->r_U, &h->r_tiles, &h->r_ntiles,
                     &h->xq, &h->xd, &h->r_chunk, &h->r_rids, &h->r_rw, &h->tact};
   for (DevBuf* b : bufs) b->release();
+  for (void* p : h->retired) (void)hipFree(p);
   if (h->ev0) (void)hipEventDestroy(h->ev0);
   if (h->ev1) (void)hipEventDestroy(h->ev1);
   if (h->evmid) (void)hipEventDestroy(h->evmid);
@@ -715,6 +732,8 @@ MI_API int mi_moe_forward(mi_moe_handle* h, const void* x, void* y, const float*
   int rc = check_forward_args(h, x, y, topk_w, topk_ids, T, K, act_dtype);
   if (rc || T == 0) return rc;
   hipStream_t st = (hipStream_t)stream;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) h->captured = true;
   if (h->timing) HIPCHK(hipEventRecord(h->ev0, st));
   h->mid_recorded = false;
   if (h->quant == MI_MOE_W4A16) rc = forward_w4a16(h, x, y, topk_w, topk_ids, T, K, act_dtype, false, st);
@@ -769,6 +788,10 @@ MI_API int mi_moe_forward_logits(mi_moe_handle* h, const void* x, void* y, const
       int64_t cap = h->cap_r ? h->cap_r : 1024;
       while (cap < need) cap *= 2;
       HIPCHK(hipStreamSynchronize(st));   // the buffers may be in use by queued work
+      if (h->captured) {                  // or by captured graphs
+        h->r_rids.retire(h->retired);
+        h->r_rw.retire(h->retired);
+      }
       HIPCHK(h->r_rids.alloc((size_t)cap * sizeof(int32_t)));
       HIPCHK(h->r_rw.alloc((size_t)cap * sizeof(float)));
       h->cap_r = cap;

@@ -148,6 +148,16 @@ MI_API int mi_moe_cpu_set_isa(mi_moe_cpu* c, int isa) {
   return MI_MOE_OK;
 }
 
+MI_API int mi_moe_cpu_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t K, int renormalize,
+                                   int32_t* topk_ids, float* topk_w) {
+  if (T < 0 || E < 1 || E > 512 || K < 1 || K > E || K > 64)
+    return fail(MI_MOE_EINVAL, "bad T / E / top_k (E <= 512, 1 <= top_k <= min(E, 64))");
+  if (T == 0) return MI_MOE_OK;
+  if (!logits || !topk_ids || !topk_w) return fail(MI_MOE_EINVAL, "null pointer");
+  mimoe_cpu::topk_softmax(logits, T, E, K, renormalize, topk_ids, topk_w);
+  return MI_MOE_OK;
+}
+
 MI_API const char* mi_moe_cpu_isa_name(int isa) {
   return isa >= 0 && isa <= 3 ? mimoe_cpu::isa_name((mimoe_cpu::Isa)isa) : "unknown";
 }

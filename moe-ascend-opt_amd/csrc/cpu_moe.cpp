@@ -349,6 +349,42 @@ void axpy_row(bool simd, float w, const float* row, float* acc, int64_t n) {
 
 float half_to_f32(uint16_t v, int dt) { return half_f32(v, dt); }
 
+// make_topk_from_logits_cpu (Int8-gemm/test/fused_moe_cpu.py:20-37): K
+// selection passes over the row, then the softmax of the picks (renormalize)
+// or of the whole row gathered at the picks.
+void topk_softmax(const float* logits, int64_t T, int64_t E, int64_t K, int renormalize, int32_t* ids,
+                  float* w) {
+  std::vector<unsigned char> taken((size_t)E);
+  std::vector<float> ex((size_t)(E > K ? E : K));
+  for (int64_t t = 0; t < T; ++t) {
+    const float* x = logits + t * E;
+    int32_t* oi = ids + t * K;
+    std::fill(taken.begin(), taken.end(), (unsigned char)0);
+    for (int64_t k = 0; k < K; ++k) {
+      int64_t best = -1;
+      for (int64_t e = 0; e < E; ++e)
+        if (!taken[(size_t)e] && (best < 0 || x[e] > x[best])) best = e;
+      taken[(size_t)best] = 1;
+      oi[k] = (int32_t)best;
+    }
+    const float m = x[oi[0]];
+    float s = 0.0f;
+    if (renormalize) {
+      for (int64_t k = 0; k < K; ++k) {
+        ex[(size_t)k] = expf_cw(x[oi[k]] - m);
+        s = s + ex[(size_t)k];
+      }
+      for (int64_t k = 0; k < K; ++k) w[t * K + k] = ex[(size_t)k] / s;
+    } else {
+      for (int64_t e = 0; e < E; ++e) {
+        ex[(size_t)e] = expf_cw(x[e] - m);
+        s = s + ex[(size_t)e];
+      }
+      for (int64_t k = 0; k < K; ++k) w[t * K + k] = ex[(size_t)oi[k]] / s;
+    }
+  }
+}
+
 void quant_hidden_row(bool simd, const uint16_t* x, int64_t n, int dt, int8_t* q, uint8_t* qb, float* d,
                       int32_t* s) {
   if (simd) quant_hidden_avx2(x, n, dt, q, qb, d, s);
@@ -957,7 +993,9 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
   const int64_t nlive = (int64_t)live.size();
   grow(part_, (size_t)(tp_ * T * H));
   float* const part = part_.data();
-  const bool simd = isa_ != Isa::kScalar;
+  // the row quantizers' vector form needs AVX2, FMA and F16C, which a vector
+  // dot-product ISA alone does not imply
+  const bool simd = isa_ != Isa::kScalar && host_simd();
   // per-token stages of a few tokens run on the calling thread: waking the
   // pool costs more than the work
   auto per_token = [&](NodePool& pool, int64_t n, const std::function<void(int64_t)>& f) {
@@ -981,20 +1019,24 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
       quant_hidden_row(simd, x + t * H, H, act_dtype, sc.xq.data() + t * H, sc.xb.data() + t * H,
                        sc.xd.data() + t * HB, sc.xs.data() + t * HB);
     });
-    // the task's rows gathered (pack_A_q8_0_from_quantized_indirect, Int8-gemm/gemm_kernels.cpp:427-464)
-    auto gather = [&](const Task& tk, std::vector<int8_t>& a, std::vector<uint8_t>& ab, std::vector<float>& ad,
-                      std::vector<int32_t>& as) {
-      a.resize((size_t)(tk.count * H));
-      ab.resize((size_t)(tk.count * H));
-      ad.resize((size_t)(tk.count * HB));
-      as.resize((size_t)(tk.count * HB));
-      for (int m = 0; m < tk.count; ++m) {
-        const int64_t t = tok[(size_t)(tk.start + m)];
-        memcpy(&a[(size_t)(m * H)], &sc.xq[(size_t)(t * H)], (size_t)H);
-        memcpy(&ab[(size_t)(m * H)], &sc.xb[(size_t)(t * H)], (size_t)H);
-        memcpy(&ad[(size_t)(m * HB)], &sc.xd[(size_t)(t * HB)], sizeof(float) * (size_t)HB);
-        memcpy(&as[(size_t)(m * HB)], &sc.xs[(size_t)(t * HB)], sizeof(int32_t) * (size_t)HB);
-      }
+    // every routed row gathered in sorted order once, into the shard's
+    // persistent buffers (pack_A_q8_0_from_quantized_indirect,
+    // Int8-gemm/gemm_kernels.cpp:427-464): a task's rows are then one
+    // contiguous block, and no task allocates
+    grow(sc.ga, (size_t)(total * H));
+    grow(sc.gab, (size_t)(total * H));
+    grow(sc.gad, (size_t)(total * HB));
+    grow(sc.gas, (size_t)(total * HB));
+    per_token(pool, total, [&](int64_t r) {
+      const int64_t t = tok[(size_t)r];
+      memcpy(&sc.ga[(size_t)(r * H)], &sc.xq[(size_t)(t * H)], (size_t)H);
+      memcpy(&sc.gab[(size_t)(r * H)], &sc.xb[(size_t)(t * H)], (size_t)H);
+      memcpy(&sc.gad[(size_t)(r * HB)], &sc.xd[(size_t)(t * HB)], sizeof(float) * (size_t)HB);
+      memcpy(&sc.gas[(size_t)(r * HB)], &sc.xs[(size_t)(t * HB)], sizeof(int32_t) * (size_t)HB);
+    });
+    auto task_rows = [&](const Task& tk) {
+      return ARows{sc.ga.data() + (size_t)tk.start * H, sc.gab.data() + (size_t)tk.start * H,
+                   sc.gad.data() + (size_t)tk.start * HB, sc.gas.data() + (size_t)tk.start * HB, H};
     };
     // gate_up outputs [total][2 * Ish], the intermediate's Q8_0 [total][Ish]
     // (SiLU(gate) * up, Int8-gemm/vec_simd.h:36-64, then pack_A_q8_0,
@@ -1045,12 +1087,7 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
         int64_t c0, c1;
         part_range(Ish / 32, 32, (int)(i % P), c0, c1);
         if (c0 == c1) return;
-        std::vector<int8_t> a;
-        std::vector<uint8_t> ab;
-        std::vector<float> ad;
-        std::vector<int32_t> as;
-        gather(tk, a, ab, ad, as);
-        const ARows A{a.data(), ab.data(), ad.data(), as.data(), H};
+        const ARows A = task_rows(tk);
         float* in = inter + (size_t)tk.start * 2 * Ish;
         gemm_rows(isa_, sh.w13[(size_t)tk.e], A, tk.count, c0, c1, in, 2 * Ish);
         gemm_rows(isa_, sh.w13[(size_t)tk.e], A, tk.count, Ish + c0, Ish + c1, in, 2 * Ish);
@@ -1066,12 +1103,7 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
     } else {
       pool.run(ntasks, [&](int64_t ti) {
         const Task& tk = tasks[(size_t)ti];
-        std::vector<int8_t> a;
-        std::vector<uint8_t> ab;
-        std::vector<float> ad;
-        std::vector<int32_t> as;
-        gather(tk, a, ab, ad, as);
-        const ARows A1{a.data(), ab.data(), ad.data(), as.data(), H};
+        const ARows A1 = task_rows(tk);
         gemm_rows(isa_, sh.w13[(size_t)tk.e], A1, tk.count, 0, 2 * Ish, inter + (size_t)tk.start * 2 * Ish, 2 * Ish);
         activate(tk, 0, Ish);
         gemm_rows(isa_, sh.w2[(size_t)tk.e], down_rows(tk), tk.count, 0, H, eout + (size_t)tk.start * H, H);
@@ -1100,13 +1132,27 @@ int Engine::forward(const uint16_t* x, uint16_t* y, const float* topk_w, const i
   if (tp_ == 1) {
     run_shard(0);
   } else {
+    // a shard's exception is carried to this thread after every launcher
+    // has been joined
     std::vector<std::thread> launch;
-    for (int s = 0; s < tp_; ++s)
-      launch.emplace_back([&, s] {
-        pools_[(size_t)s]->pin(0);   // the shard's launcher works on its node too
-        run_shard(s);
-      });
+    std::vector<std::exception_ptr> errs((size_t)tp_);
+    try {
+      for (int s = 0; s < tp_; ++s)
+        launch.emplace_back([&, s] {
+          try {
+            pools_[(size_t)s]->pin(0);   // the shard's launcher works on its node too
+            run_shard(s);
+          } catch (...) {
+            errs[(size_t)s] = std::current_exception();
+          }
+        });
+    } catch (...) {
+      for (auto& th : launch) th.join();
+      throw;
+    }
     for (auto& th : launch) th.join();
+    for (auto& e : errs)
+      if (e) std::rethrow_exception(e);
   }
   // Stage C2 (Int8-gemm/q8_gemm.cpp:621-641): shard order, then the cast
   per_token(*pools_[0], T, [&](int64_t t) {

@@ -20,6 +20,12 @@ namespace mimoe_cpu {
 
 // fp16 (dt 0) / bf16 (dt 1) bits -> fp32, exact
 float half_to_f32(uint16_t v, int dt);
+// Router top-k + softmax on host cores: the device kernel's picks (strictly
+// larger logit first, equal logits the lower id) and weights (float exp of the
+// Cody-Waite routine the device uses, summed in float in pick / expert order),
+// bit-equal to the device kernel for non-NaN logits.
+void topk_softmax(const float* logits, int64_t T, int64_t E, int64_t K, int renormalize, int32_t* ids,
+                  float* w);
 
 // Q8_0 of n values (n % 32 == 0) into q, q ^ 0x80, block scales d and int32
 // block sums s: a hidden row of fp16 / bf16 bits (Stage A), or SiLU(gate) * up
@@ -126,6 +132,10 @@ class Engine {
     std::vector<uint8_t> xb, ab;
     std::vector<float> xd, ad, inter, eout;
     std::vector<int32_t> xs, as;
+    std::vector<int8_t> ga;       // routed rows of the Stage-A activations, sorted order
+    std::vector<uint8_t> gab;
+    std::vector<float> gad;
+    std::vector<int32_t> gas;
   };
   int64_t E_, H_, I_;
   int qt_;

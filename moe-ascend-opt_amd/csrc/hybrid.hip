@@ -74,6 +74,11 @@ struct DBuf {
     p = nullptr;
     bytes = 0;
   }
+  void retire(std::vector<void*>& keep) {   // freed later by the owner
+    if (p) keep.push_back(p);
+    p = nullptr;
+    bytes = 0;
+  }
 };
 
 struct PinBuf {
@@ -87,6 +92,11 @@ struct PinBuf {
   }
   void release() {
     if (p) (void)hipHostFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  void retire(std::vector<void*>& keep) {   // freed later by the owner
+    if (p) keep.push_back(p);
     p = nullptr;
     bytes = 0;
   }
@@ -151,16 +161,25 @@ int default_threads() {
 
 using namespace mimoe;
 
-// Arguments of one host callback.  An eager call's context is freed by its
-// callback; a call captured into a graph keeps its context in the handle
-// (graph_ctx), since every replay of the graph runs the callback on it.
+// Arguments of one host callback, with the staging buffers of its call (a
+// graph replays the staging kernel on the buffers it captured, so the
+// callback must read those, not the handle's current ones).  An eager call's
+// context is freed by its callback; a captured call's context belongs to the
+// graph (a HIP user object it retains: freed when the graph and its
+// instances are), or, if that cannot be set up, to the handle (graph_ctx).
 struct CallCtx {
   struct mi_moe_hybrid* hh;
   int64_t T, K;
   int act;
   std::chrono::steady_clock::time_point enqueued;
   bool eager;
+  const uint16_t* x_h;
+  const int32_t* ids_h;
+  const float* w_h;
+  float* part_h;
 };
+
+void delete_call_ctx(void* p) { delete static_cast<CallCtx*>(p); }
 
 struct mi_moe_hybrid {
   int64_t E = 0, H = 0, I = 0;
@@ -184,7 +203,11 @@ struct mi_moe_hybrid {
   std::atomic<double> last_queue_ms{-1.0};   // forward call -> start of its host callback
   std::atomic<int64_t> last_pairs{0};
   std::atomic<int> host_error{0};    // a host callback failed (reported by the next call)
-  std::vector<std::unique_ptr<CallCtx>> graph_ctx;   // arguments of callbacks captured in graphs
+  std::vector<std::unique_ptr<CallCtx>> graph_ctx;   // captured callbacks' arguments not owned by a graph
+  // staging that was live during a capture is not freed when it grows but
+  // kept until destroy (captured graphs hold its addresses)
+  bool captured = false;
+  std::vector<void*> retired_dev, retired_pin;
 };
 
 namespace {
@@ -222,10 +245,9 @@ void host_callback(void* arg) {
     hh->last_queue_ms.store(
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - ctx->enqueued).count());
   try {
-    run_host(hh, (const uint16_t*)hh->x_h.p, ctx->act, (const int32_t*)hh->ids_h.p, (const float*)hh->w_h.p,
-             ctx->T, ctx->K, (float*)hh->part_h.p);
+    run_host(hh, ctx->x_h, ctx->act, ctx->ids_h, ctx->w_h, ctx->T, ctx->K, ctx->part_h);
   } catch (...) {   // poison the partial: the call's y must not look valid
-    float* part = (float*)hh->part_h.p;
+    float* part = ctx->part_h;
     const float qnan = __builtin_nanf("");
     for (int64_t i = 0; i < ctx->T * hh->H; ++i) part[i] = qnan;
     hh->host_error.store(1);
@@ -248,6 +270,10 @@ int grow(mi_moe_hybrid* hh, int64_t T, int64_t n, hipStream_t st) {
   while (capn < n) capn *= 2;
   HCHK(hipStreamSynchronize(st));   // queued work may still use the buffers
   HCHK(hipStreamSynchronize(hh->side));
+  if (hh->captured) {   // and captured graphs
+    for (PinBuf* b : {&hh->x_h, &hh->part_h, &hh->ids_h, &hh->w_h}) b->retire(hh->retired_pin);
+    hh->ids_dev.retire(hh->retired_dev);
+  }
   HCHK(hh->x_h.alloc((size_t)capT * hh->H * 2));
   HCHK(hh->part_h.alloc((size_t)capT * hh->H * sizeof(float)));
   HCHK(hh->ids_h.alloc((size_t)capn * sizeof(int32_t)));
@@ -360,6 +386,8 @@ MI_API int mi_moe_hybrid_destroy(mi_moe_hybrid* hh) {
   if (hh->dev) mi_moe_destroy(hh->dev);
   hh->slot_dev.release(); hh->ids_dev.release();
   hh->x_h.release(); hh->ids_h.release(); hh->w_h.release(); hh->part_h.release();
+  for (void* p : hh->retired_dev) (void)hipFree(p);
+  for (void* p : hh->retired_pin) (void)hipHostFree(p);
   if (hh->ev_in) (void)hipEventDestroy(hh->ev_in);
   if (hh->ev_part) (void)hipEventDestroy(hh->ev_part);
   if (hh->side) (void)hipStreamDestroy(hh->side);
@@ -469,14 +497,36 @@ MI_API int mi_moe_hybrid_forward(mi_moe_hybrid* hh, const void* x, void* y, cons
   HCHK(hipGetLastError());
   HCHK(hipEventRecord(hh->ev_in, st));
   HCHK(hipStreamWaitEvent(hh->side, hh->ev_in, 0));
-  CallCtx* ctx = new (std::nothrow) CallCtx{hh, T, K, act_dtype, std::chrono::steady_clock::now(), !capturing};
+  const CallCtx proto{hh, T, K, act_dtype, std::chrono::steady_clock::now(), !capturing,
+                      (const uint16_t*)hh->x_h.p, (const int32_t*)hh->ids_h.p, (const float*)hh->w_h.p,
+                      (float*)hh->part_h.p};
+  CallCtx* ctx = new (std::nothrow) CallCtx(proto);
   if (!ctx) return hfail(MI_MOE_EINVAL, "out of host memory");
+  if (capturing) {
+    hh->captured = true;
+    // the graph being captured owns the context (a user object it retains);
+    // failing that, the handle keeps it
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipGraph_t graph = nullptr;
+    hipUserObject_t obj = nullptr;
+    bool owned = false;
+    if (hipStreamGetCaptureInfo_v2(st, &cs, nullptr, &graph, nullptr, nullptr) == hipSuccess && graph &&
+        hipUserObjectCreate(&obj, ctx, delete_call_ctx, 1, hipUserObjectNoDestructorSync) == hipSuccess) {
+      owned = hipGraphRetainUserObject(graph, obj, 1, hipGraphUserObjectMove) == hipSuccess;
+      if (!owned) {
+        (void)hipUserObjectRelease(obj, 1);   // deletes ctx
+        ctx = new (std::nothrow) CallCtx(proto);
+        if (!ctx) return hfail(MI_MOE_EINVAL, "out of host memory");
+      }
+    }
+    (void)hipGetLastError();
+    if (!owned) hh->graph_ctx.emplace_back(ctx);
+  }
   hipError_t e = hipLaunchHostFunc(hh->side, host_callback, ctx);
   if (e != hipSuccess) {
-    delete ctx;
+    if (!capturing) delete ctx;   // a captured call's context stays with its owner
     return hfail(MI_MOE_EHIP, "hipLaunchHostFunc failed: %s", hipGetErrorString(e));
   }
-  if (capturing) hh->graph_ctx.emplace_back(ctx);
   HCHK(hipEventRecord(hh->ev_part, hh->side));
   // caller stream: the hot experts on the device
   if (hh->dev) {

@@ -127,9 +127,10 @@ __host__ __device__ constexpr size_t tagged_act_bytes(int I) { return (size_t)64
 inline size_t w4_fused_gate_up_lds_bytes(int H, int xrows, int NW) {
   return (size_t)(kW4FusedWaves / NW) * (p1_red_bytes(NW) + 80 * (H >> 7)) + (size_t)xrows * H * 2;
 }
-// act rows [8][I] | w2 metadata [8][RT][SEC] | outputs [8][16 RT] f32 | state [8]
+// act rows [8][I] | w2 metadata [8][RT][SEC] | outputs [8][16 RT] f32 |
+// state [8] | routing weights [8] f32
 inline size_t w4_fused_down_lds_bytes(int I, int RT) {
-  return (size_t)kW4FusedWaves * ((size_t)I * 2 + (size_t)RT * (w2_meta_sec_bytes(I >> 7) + 16 * 4) + 4);
+  return (size_t)kW4FusedWaves * ((size_t)I * 2 + (size_t)RT * (w2_meta_sec_bytes(I >> 7) + 16 * 4) + 8);
 }
 struct W4FusedPlan {
   int ok;          // the one-launch kernel serves the call

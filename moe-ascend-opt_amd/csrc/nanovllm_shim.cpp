@@ -228,25 +228,7 @@ std::tuple<at::Tensor, at::Tensor> moe_topk_softmax_cpu(const at::Tensor& logits
   const float* g = x.data_ptr<float>();
   int32_t* oi = ids.data_ptr<int32_t>();
   float* ow = w.data_ptr<float>();
-  std::vector<int32_t> ord((size_t)E);
-  for (int64_t t = 0; t < T; ++t) {
-    const float* row = g + t * E;
-    for (int64_t e = 0; e < E; ++e) ord[(size_t)e] = (int32_t)e;
-    std::partial_sort(ord.begin(), ord.begin() + top_k, ord.end(), [&](int32_t a, int32_t b) {
-      return row[a] > row[b] || (row[a] == row[b] && a < b);
-    });
-    const float mx = row[ord[0]];
-    double den = 0.0;
-    if (renormalize) {
-      for (int64_t k = 0; k < top_k; ++k) den += std::exp((double)row[ord[(size_t)k]] - mx);
-    } else {
-      for (int64_t e = 0; e < E; ++e) den += std::exp((double)row[e] - mx);
-    }
-    for (int64_t k = 0; k < top_k; ++k) {
-      oi[t * top_k + k] = ord[(size_t)k];
-      ow[t * top_k + k] = (float)(std::exp((double)row[ord[(size_t)k]] - mx) / den);
-    }
-  }
+  check_status(mi_moe_cpu_topk_softmax(g, T, E, top_k, renormalize ? 1 : 0, oi, ow), "moe_topk_softmax");
   return {ids, w};
 }
 

@@ -43,7 +43,7 @@ namespace mimoe {
 
 constexpr int kFusedWaves = kW4FusedWaves;
 constexpr int kSpinMax = 1 << 18;   // polls of one wait (each at least one memory round trip)
-constexpr int kUnitBatch = 8;       // act units per lane loaded together by a down wave
+constexpr int kUnitBatch = 6;       // act units per lane loaded together by a down wave (I = 768: all)
 
 __device__ __forceinline__ unsigned long long load_agent(const unsigned long long* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -190,7 +190,7 @@ __device__ __forceinline__ void fused_gate_up(const SchedArgs& c, const W4Args& 
 // ---------------------------------------------------------------- down role
 // Down item (token t, RT consecutive 16-row tiles of H from tile0, within one
 // quad of 64 rows).  LDS: act rows [8][I] | metadata [8][RT][SEC] | outputs
-// [8][16 RT] f32 | state [8].
+// [8][16 RT] f32 | state [8] | routing weights [8] f32.
 template <int ACT, int SDT, int NB, int RT>
 __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, const char* w2,
                                            const unsigned char* w2_m, int t, int tile0, unsigned char* smem) {
@@ -204,12 +204,11 @@ __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, 
   unsigned char* meta = smem + (size_t)kFusedWaves * I * 2;
   float* outs = reinterpret_cast<float*>(meta + (size_t)kFusedWaves * RT * SEC);
   int* state = reinterpret_cast<int*>(outs + 16 * RT * kFusedWaves);   // 0 invalid id, 1 valid, 2 wait gave up
+  float* tws = reinterpret_cast<float*>(state + kFusedWaves);
   constexpr float off = W4Consts<ACT>::offset;
-  // the combine's routing weights, loaded now (threads < 16 RT sum the tiles)
-  float tw[kW4FusedWaves];
-  if (tid < 16 * RT)
-#pragma unroll
-    for (int k = 0; k < kW4FusedWaves; ++k) tw[k] = k < K ? c.tw[t * K + k] : 0.0f;
+  // the combine's routing weights, copied into LDS now (wave 0's wait below
+  // covers the copy; no registers held)
+  if (tid < K) __builtin_amdgcn_global_load_lds(c.tw + t * K + tid, tws, 4, 0, 0);
   if (wave < K) {   // uniform: wave k takes routed expert k of token t
     const int i = t * K + wave;
     const int e = __builtin_amdgcn_readfirstlane(c.ids[i]);
@@ -316,7 +315,7 @@ __device__ __forceinline__ void fused_down(const SchedArgs& c, const W4Args& a, 
       const int s = k < K ? state[k] : 0;
       if (s) {
         gave_up |= s == 2;
-        const float prod = tw[k] * outs[16 * RT * k + tid];
+        const float prod = tws[k] * outs[16 * RT * k + tid];
         yv = yv + prod;
       }
     }

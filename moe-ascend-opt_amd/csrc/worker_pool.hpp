@@ -1,7 +1,10 @@
 // worker_pool.hpp -- the fixed host thread pool of the CPU paths (host
 // engine, hybrid host executor).  run(n, f) calls f(i) for every i < n on the
 // calling thread and on the pool's workers, handing indices out dynamically,
-// and returns when all calls are done.  One run at a time per pool.
+// and returns when all calls are done.  One run at a time per pool.  If a
+// call throws, no further indices are handed out, the run is closed and
+// drained as usual, and run() rethrows the first exception on the calling
+// thread; the pool stays usable.
 //
 // A call of the host paths is a few short phases back to back (tens of
 // microseconds each), so the hand-offs are built for latency:
@@ -22,7 +25,9 @@
 #include <atomic>
 #include <chrono>
 #include <climits>
+#include <exception>
 #include <functional>
+#include <mutex>
 #include <memory>
 #include <thread>
 #include <vector>
@@ -72,13 +77,14 @@ class WorkerPool {
     }
     fn_ = &f;
     n_ = n;
+    err_ = nullptr;
     next_.store(0, std::memory_order_relaxed);
     // open the run: clears the closed bit, keeps the count of any worker
     // that is passing through on its way out of the previous run
     state_.fetch_and(~kClosed);
     gen_.fetch_add(1);
     if (sleepers_.load() > 0) futex_wake((int)std::min<int64_t>(n - 1, (int64_t)th_.size()));
-    for (int64_t i; (i = next_.fetch_add(1, std::memory_order_relaxed)) < n;) f(i);
+    call_all(f, n);
     state_.fetch_or(kClosed);
     // the workers still inside finish their current index at most
     for (unsigned spins = 0; (state_.load(std::memory_order_acquire) & ~kClosed) != 0; ++spins) {
@@ -86,10 +92,29 @@ class WorkerPool {
       else std::this_thread::yield();
     }
     fn_ = nullptr;
+    if (err_) {
+      std::exception_ptr e = err_;
+      err_ = nullptr;
+      std::rethrow_exception(e);
+    }
   }
 
  private:
   static constexpr uint32_t kClosed = 1u << 31;
+
+  // f(i) for the indices this thread takes; the first exception of the run is
+  // kept and the remaining indices are skipped
+  void call_all(const std::function<void(int64_t)>& f, int64_t n) {
+    for (int64_t i; (i = next_.fetch_add(1, std::memory_order_relaxed)) < n;) {
+      try {
+        f(i);
+      } catch (...) {
+        std::lock_guard<std::mutex> lk(err_mu_);
+        if (!err_) err_ = std::current_exception();
+        next_.store(n, std::memory_order_relaxed);
+      }
+    }
+  }
 
   void futex_wake(int count) {
     syscall(SYS_futex, reinterpret_cast<uint32_t*>(&gen_), FUTEX_WAKE_PRIVATE, count, nullptr, nullptr, 0);
@@ -118,9 +143,7 @@ class WorkerPool {
       if (stop_.load()) return;
       const uint32_t s = state_.fetch_add(1);
       if (!(s & kClosed)) {   // inside an open run: its fn_ / n_ are set
-        const std::function<void(int64_t)>* f = fn_;
-        const int64_t n = n_;
-        for (int64_t i; (i = next_.fetch_add(1, std::memory_order_relaxed)) < n;) (*f)(i);
+        call_all(*fn_, n_);
       }
       state_.fetch_sub(1, std::memory_order_release);
     }
@@ -135,6 +158,8 @@ class WorkerPool {
   std::atomic<int64_t> next_{0};
   const std::function<void(int64_t)>* fn_ = nullptr;
   int64_t n_ = 0;
+  std::mutex err_mu_;
+  std::exception_ptr err_;   // first exception of the current run
 };
 
 }  // namespace mimoe_pool

@@ -8,9 +8,13 @@ After ``nanovllm_moe.load()`` (or ``import nanovllm_ext``):
     h.store_awq_repack(w13_q, w13_z, w13_s, w2_q, w2_z, w2_s, 128)      # W4A16
     y = torch.ops.nanovllm.moe_forward(hidden, topk_ids, topk_w, h)     # HIP tensors
 
-The op runs the hand-written HIP kernels of ``libmimoe.so`` on the current
-stream.  There is no CPU fallback: a missing library raises, and CPU tensors
-are rejected.
+The op dispatches on the tensors' device, like the reference's registration
+(Int8-gemm/nanovllm_ops.cpp:410-412).  HIP tensors run the hand-written HIP
+kernels of ``libmimoe.so`` on the current stream; a missing library raises,
+and the HIP key never falls back to the host.  CPU tensors run the reference
+CPU algorithm on host cores (the CPU key: Q8_0 / Q4_0 on the host engine,
+W4A16 on the host executor), from the host copy of the weights a handle keeps
+when no HIP device is present or MIMOE_HOST_WEIGHTS=1.
 """
 from __future__ import annotations
 
@@ -42,7 +46,7 @@ C_SYMBOLS = (
     "mi_moe_hybrid_store_awq", "mi_moe_hybrid_forward", "mi_moe_hybrid_host_forward",
     "mi_moe_hybrid_get_stats", "mi_moe_cpu_create", "mi_moe_cpu_destroy", "mi_moe_cpu_store_quantized",
     "mi_moe_cpu_quantize_and_store_expert", "mi_moe_cpu_forward", "mi_moe_cpu_get_info", "mi_moe_cpu_set_isa",
-    "mi_moe_cpu_isa_name",
+    "mi_moe_cpu_isa_name", "mi_moe_cpu_topk_softmax",
 )
 
 
@@ -111,6 +115,7 @@ def capi():
     L.mi_moe_cpu_forward.argtypes = [P, P, P, P, P, I64, I64, I]
     L.mi_moe_cpu_get_info.argtypes = [P, P, P, P, P, P, P]
     L.mi_moe_cpu_set_isa.argtypes = [P, I]
+    L.mi_moe_cpu_topk_softmax.argtypes = [P, I64, I64, I64, I, P, P]
     L.mi_moe_cpu_isa_name.restype = ctypes.c_char_p
     L.mi_moe_cpu_isa_name.argtypes = [I]
     for name in C_SYMBOLS:

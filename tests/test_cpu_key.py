@@ -100,8 +100,12 @@ def test_topk_softmax_and_forward_logits_cpu():
     ids, w = torch.ops.nanovllm.moe_topk_softmax(logits, K, True)
     rid, rw = oracle.topk_softmax(logits.numpy(), K, renormalize=True)
     assert np.array_equal(ids.numpy(), rid)
-    assert np.allclose(w.numpy(), rw, rtol=1e-6, atol=1e-7)
+    assert np.array_equal(w.numpy().view(np.uint32), rw.view(np.uint32))   # the device kernel's bits
     assert ids[0, 0] == 3 and ids[0, 1] == 5
+    ids_all, w_all = torch.ops.nanovllm.moe_topk_softmax(logits, K, False)
+    rid, rw = oracle.topk_softmax(logits.numpy(), K, renormalize=False)
+    assert np.array_equal(ids_all.numpy(), rid)
+    assert np.array_equal(w_all.numpy().view(np.uint32), rw.view(np.uint32))
     ws = _q_weights(1, E, H, I, 90, torch.float16)
     h = torch.classes.nanovllm.MoEInfer(E, H, I, 1)
     h.store_quantized_repack(*[torch.from_numpy(np.ascontiguousarray(t)) if isinstance(t, np.ndarray) else t

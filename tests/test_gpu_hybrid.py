@@ -174,3 +174,34 @@ def test_hybrid_graph_replay_matches_eager(cuda, w4w, kind):
         torch.cuda.synchronize()
         assert torch.equal(y, eager[rep % 2])
     del g
+
+
+def test_hybrid_graph_survives_staging_growth(cuda, w4w):
+    """A captured hybrid call keeps its staging buffers and its callback's view
+    of them: a later, larger eager call grows the staging (and the device
+    workspace) without freeing what the graph holds, and the graph still
+    replays the eager result bit for bit."""
+    E, H, I = W4["E"], W4["H"], W4["I"]
+    hm = HybridMoE(E, H, I, nm.W4A16, host_experts=COLD, num_threads=4)
+    hm.store_awq(*w4w)
+    T, K = 4, 8
+    ids, tw = topk_routing(T, E, K, seed=450)
+    x, ids, tw = _x(T, H, 451).to(cuda), ids.to(cuda), tw.to(cuda)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=cuda)
+    hm.forward(x, ids, tw, out=out)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        hm.forward(x, ids, tw, out=out)
+    T2 = 64                                        # staging capacity 16 tokens / 128 pairs: grows
+    ids2, tw2 = topk_routing(T2, E, K, seed=452)
+    y2 = hm.forward(_x(T2, H, 453).to(cuda), ids2.to(cuda), tw2.to(cuda))
+    torch.cuda.synchronize()
+    assert torch.isfinite(y2.float()).all()
+    for rep in range(2):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+    del g

@@ -103,11 +103,26 @@ def test_repeat_calls_deterministic(cuda, small, T, K):
     E, H = SMALL["E"], SMALL["H"]
     ids, tw = topk_routing(T, E, K, seed=9)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    h.set_timing(True)
     outs = [_run(h, x, ids, tw, cuda) for _ in range(4)]
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     ms = h.get_last_run_time_ms()
+    h.set_timing(False)
     assert ms > 0
+
+
+def test_timing_off_by_default(cuda):
+    """A new handle records no HIP events: no run time until timing is asked for."""
+    E, H, I = SMALL["E"], SMALL["H"], SMALL["I"]
+    h = _handle(E, H, I, w4a16_random(E, H, I, seed=7), True, cuda)
+    ids, tw = topk_routing(2, E, 4, seed=2)
+    x = torch.randn(2, H, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    _run(h, x, ids, tw, cuda)
+    assert h.get_last_run_time_ms() < 0
+    h.set_timing(True)
+    _run(h, x, ids, tw, cuda)
+    assert h.get_last_run_time_ms() > 0
 
 
 @pytest.mark.parametrize("T,K", [(4, 8), (40, 8)])
@@ -146,6 +161,39 @@ def test_graph_replay_matches_eager(cuda, small, T, K):
         y = torch.ops.nanovllm.moe_forward(x, ids, tw, h)
         torch.cuda.synchronize()
         assert torch.equal(y.cpu(), eager[rep])
+
+
+def test_graph_survives_workspace_growth(cuda):
+    """A captured sorted-path call keeps the workspace addresses it captured: a
+    later, larger eager call that grows the workspace must not free them, so
+    the graph still replays the eager result bit for bit."""
+    E, H, I = SMALL["E"], SMALL["H"], SMALL["I"]
+    w = w4a16_random(E, H, I, seed=111)
+    h = _handle(E, H, I, w, True, cuda)
+    T, K = 40, 8                                   # 320 pairs: sorted path, workspace of 512 pairs
+    ids, tw = topk_routing(T, E, K, seed=112)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(112)).to(torch.bfloat16).to(cuda)
+    ids, tw = ids.to(cuda), tw.to(cuda)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=cuda)
+    torch.ops.nanovllm.moe_forward_out(x, ids, tw, h, out)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        torch.ops.nanovllm.moe_forward_out(x, ids, tw, h, out)
+    # 4096 pairs: the workspace grows past the captured buffers
+    T2 = 512
+    ids2, tw2 = topk_routing(T2, E, K, seed=113)
+    x2 = torch.randn(T2, H, generator=torch.Generator().manual_seed(113)).to(torch.bfloat16).to(cuda)
+    y2 = torch.ops.nanovllm.moe_forward(x2, ids2.to(cuda), tw2.to(cuda), h)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y2.float()).all()
+    for rep in range(2):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+    del g
 
 
 @pytest.mark.parametrize("T", [5, 40])

@@ -84,3 +84,25 @@ def test_noalloc_rejects_oversize_call(cuda):
         assert b"mi_moe_forward_noalloc holds at most" in L.mi_moe_last_error()
     finally:
         L.mi_moe_destroy(hp)
+
+
+def test_noalloc_keeps_phase_times(cuda):
+    """A no-alloc call records no timing and leaves the phase times of the last
+    timed mi_moe_forward as they were (2 phases for a sorted-path call)."""
+    L = nanovllm_moe.capi()
+    E, H, I = 8, 512, 256
+    hp = _handle(L, E, H, I, 2, cuda, seed=5)
+    try:
+        nanovllm_moe.check(L.mi_moe_set_timing(hp, 1), "set_timing")
+        T, K = 40, 8                       # 320 pairs: the sorted path, two launch phases
+        ids, tw = topk_routing(T, E, K, seed=4)
+        ids, tw = ids.to(cuda), tw.to(cuda)
+        x = torch.randn(T, H, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(cuda)
+        _call(L, L.mi_moe_forward, hp, x, ids, tw)
+        ms = (ctypes.c_double * 2)()
+        assert L.mi_moe_get_last_phase_times_ms(hp, ms, 2) == 2
+        _call(L, L.mi_moe_forward_noalloc, hp, x[:3], ids[:3].contiguous(), tw[:3].contiguous())
+        torch.cuda.synchronize()
+        assert L.mi_moe_get_last_phase_times_ms(hp, ms, 2) == 2
+    finally:
+        L.mi_moe_destroy(hp)
