@@ -80,11 +80,17 @@ def cpu_reference_config1(torch, fmt, nsets=4, warmup=5, runs=50, tokens=(1, 4, 
     config's seeded routing (N(0,1) logits, top-8, softmax) and the
     reference's round-robin routing ids[t,k] = (t*K + k) % E, w = 1/K.
     Weights: uniform int8 codes and fp16 scales of the config's shape (the
-    timing does not depend on the values)."""
+    timing does not depend on the values).  The engine's layout follows the
+    reference's variables when they are set (NANOVLLM_TP_SIZE,
+    NANOVLLM_TP_THREADS_PER_NODE: tp shards over NUMA nodes, threads per node),
+    else one shard per NUMA node over the host's thread share."""
     import ctypes
     import nanovllm_moe as nm
     L = nm.capi()
     nthr = host_threads()
+    env = {k: os.environ.get(k) for k in ("NANOVLLM_TP_SIZE", "NANOVLLM_TP_THREADS_PER_NODE")}
+    tp_env = int(env["NANOVLLM_TP_SIZE"]) if env["NANOVLLM_TP_SIZE"] else -1
+    per_env = int(env["NANOVLLM_TP_THREADS_PER_NODE"]) if env["NANOVLLM_TP_THREADS_PER_NODE"] else -1
     handles = []
     for s_ in range(nsets):
         g = torch.Generator().manual_seed(50 + s_)
@@ -93,7 +99,11 @@ def cpu_reference_config1(torch, fmt, nsets=4, warmup=5, runs=50, tokens=(1, 4, 
         gd = (torch.rand(E, 2 * I, H // 32, generator=g) * 1e-3).half()
         dd = (torch.rand(E, H, I // 32, generator=g) * 1e-3).half()
         c = ctypes.c_void_p()
-        nm.check(L.mi_moe_cpu_create(E, H, I, 0, nthr, 0, ctypes.byref(c)), "cpu_create")
+        if tp_env >= 0 or per_env >= 0:
+            nm.check(L.mi_moe_cpu_create_numa(E, H, I, 0, max(tp_env, 0), max(per_env, 0), ctypes.byref(c)),
+                     "cpu_create_numa")
+        else:
+            nm.check(L.mi_moe_cpu_create(E, H, I, 0, nthr, 0, ctypes.byref(c)), "cpu_create")
         nm.check(L.mi_moe_cpu_store_quantized(c, gq.data_ptr(), gd.data_ptr(), dq.data_ptr(), dd.data_ptr(), 0),
                  "cpu_store")
         del gq, dq, gd, dd
@@ -139,6 +149,7 @@ def cpu_reference_config1(torch, fmt, nsets=4, warmup=5, runs=50, tokens=(1, 4, 
                   "GB/s = unique experts x 5,013,504 B / ms (Int8-gemm/test/benchmark_fused_moe_cpu.py)",
         "threads": th.value, "tp_shards": tp.value, "isa": L.mi_moe_cpu_isa_name(isa.value).decode(),
         "affinity_cpus": acpu.value, "numa_nodes": anodes.value,
+        "env": {k: (v if v is not None else "unset") for k, v in env.items()},
         "results": out,
         "reference_published_kunpeng920": {"T1_ms": 0.29, "T4_ms": 0.83, "T8_ms": 1.45,
                                            "note": "2 CPUs, TP=4, 80 threads, README.md:69-79"},
@@ -178,16 +189,30 @@ def cpu_baseline(torch, fmt, wire_cpu, inputs_cpu, batches=BATCHES, reps=20, war
         tot_s += dt
     L.mi_moe_hybrid_destroy(hh)
     ref = cpu_reference_config1(torch, fmt)
+    # value: the reference CPU algorithm (the host engine) on config 1 with the
+    # reference's method, seeded routing, bytes / time over T = 1, 4, 8
+    per_expert = fmt.bytes_per_expert(0, H, I)
+    seeded = [v for k, v in ref["results"].items() if k.startswith("seeded_")]
+    ref_bytes = sum(v["unique_experts"] * per_expert for v in seeded)
+    ref_s = sum(v["ms"] for v in seeded) * 1e-3
     return {
-        "value": round(tot_bytes / tot_s / 1e9, 3),
+        "value": round(ref_bytes / ref_s / 1e9, 3),
         "unit": "GB/s",
-        "cores": nthr,
+        "cores": ref["threads"],
         "kind": "port",
-        "sample": f"W4A16 layer, every expert on the host executor of this library, bs 1,2,4,8 on routing #0 "
-                  f"of the GPU sweep, {warmup} warmup + {reps} timed calls each ({tot_s * reps * 1e3:.0f} ms "
-                  f"timed); {nthr} threads of {len(os.sched_getaffinity(0))} affinity CPUs",
-        "per_batch": per,
+        "sample": f"the reference CPU algorithm (Int8-gemm/q8_gemm.cpp:276-646 restated for x86, {ref['isa']}, "
+                  f"{ref['tp_shards']} tp shard(s)) on BASELINE config 1: Q8_0 H=2048 I=768 E=128 top-8, "
+                  f"T=1,4,8 with seeded routing, 4 weight sets cycled, 5 warmup + 50 timed calls each (the "
+                  f"reference's method); {ref['threads']} threads of {ref['affinity_cpus']} affinity CPUs; "
+                  f"NANOVLLM_TP_SIZE={ref['env']['NANOVLLM_TP_SIZE']}, "
+                  f"NANOVLLM_TP_THREADS_PER_NODE={ref['env']['NANOVLLM_TP_THREADS_PER_NODE']}",
         "reference_algorithm_config1": ref,
+        "w4a16_host_executor": {
+            "GB_per_s": round(tot_bytes / tot_s / 1e9, 3), "threads": nthr, "per_batch": per,
+            "sample": f"the headline W4A16 layer with every expert on this library's host executor (no reference "
+                      f"counterpart), bs 1,2,4,8 on routing #0 of the GPU sweep, {warmup} warmup + {reps} timed "
+                      f"calls each",
+        },
     }
 
 
@@ -589,6 +614,10 @@ def main():
     ap.add_argument("--offload", type=int, default=0, metavar="NCOLD",
                     help="hybrid CPU-offload executor with NCOLD experts on the host (one JSON line)")
     ap.add_argument("--host-threads", type=int, default=0)
+    ap.add_argument("--read-floor", action="store_true",
+                    help="only run the read-only floor probe (nanovllm_moe/mimoe_read_floor, built by build()): "
+                         "kernels that read a decode call's expert bytes with the shipped kernel's grid, as one "
+                         "and as two launches, and the best plain streaming form; one JSON line")
     ap.add_argument("--router", action="store_true",
                     help="measure the router top-k kernel and the layer from router logits instead")
     args = ap.parse_args()
@@ -601,6 +630,12 @@ def main():
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
+    if args.read_floor:
+        import subprocess
+        exe = os.path.join(ROOT, "moe-ascend-opt_amd", "nanovllm_moe", "mimoe_read_floor")
+        if not os.path.exists(exe):
+            sys.exit(f"{exe} is not built: run __graft_entry__.build()")
+        sys.exit(subprocess.run([exe]).returncode)
     if args.router:
         run_router(args.steps, args.warmup)
         return
@@ -777,12 +812,14 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / PEAK_GBS, 4),
                      "traffic": traffic["bytes_per_call"] if traffic else None,
-                     "kernel": "fused decode layer: w4a16_phase1_kernel (gate_up + SiLU*mul) then "
-                               "w4a16_down_token_kernel (down + combine), back to back per call",
+                     "kernel": "w4a16_decode_kernel: the whole decode layer in one launch (gate_up + SiLU*mul "
+                               "items, then down + k-order combine items with the act hand-over inside the "
+                               "launch), one launch per call",
                      "achieved_basis": "algorithmic bytes (routed experts' weights + x + y + ids/weights) "
-                                       "/ graph-replayed call time, summed over the batch sweep; equals the "
-                                       "sum of the two kernels' rocprofv3 durations",
-                     "traffic_basis": (f"bs-8 call, rocprofv3 FETCH_SIZE+WRITE_SIZE of both kernels, "
+                                       "/ graph-replayed call time (HIP events on the call's stream), summed "
+                                       "over the batch sweep; per batch size it matches the kernel's "
+                                       "rocprofv3 duration (profiles/w4a16_decode_qwen3_kernel_trace.md)",
+                     "traffic_basis": (f"bs-8 call, rocprofv3 FETCH_SIZE+WRITE_SIZE of the kernel, "
                                        f"copy-scaled ({traffic['source']}; algorithmic "
                                        f"{traffic['algorithmic_bytes_per_call']} B)") if traffic else None},
     }

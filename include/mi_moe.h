@@ -273,6 +273,18 @@ typedef struct mi_moe_cpu mi_moe_cpu;
  * threads, else exactly tp shards (I/tp a multiple of 32).  quant_type 0 / 1. */
 int mi_moe_cpu_create(int64_t num_experts, int64_t hidden, int64_t intermediate,
                       int quant_type, int num_threads, int tp, mi_moe_cpu** out);
+
+/* The reference's NUMA layout: tp shards, shard s on NUMA node s with
+ * threads_per_node of its CPUs (0: all of them, as when
+ * NANOVLLM_TP_THREADS_PER_NODE is unset); tp 0 = one shard per NUMA node of
+ * the affinity mask.  On a host with fewer nodes than tp the affinity CPUs
+ * are split into tp groups in order (the reference refuses tp > nodes).
+ * Replaces the tp_size / threads-per-node setup of MoEInfer
+ * (Int8-gemm/moe_infer.cpp:25-36, Int8-gemm/numa_threadpool.h:498-504);
+ * the CPU dispatch key calls it when NANOVLLM_TP_SIZE or
+ * NANOVLLM_TP_THREADS_PER_NODE is set. */
+int mi_moe_cpu_create_numa(int64_t num_experts, int64_t hidden, int64_t intermediate,
+                           int quant_type, int tp, int threads_per_node, mi_moe_cpu** out);
 int mi_moe_cpu_destroy(mi_moe_cpu* c);
 
 /* Wire layout as mi_moe_store_quantized (store_quantized_weights_repack,

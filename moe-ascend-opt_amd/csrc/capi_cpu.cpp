@@ -31,19 +31,19 @@ int check(const mi_moe_cpu* c) {
 
 }  // namespace
 
-MI_API int mi_moe_cpu_create(int64_t E, int64_t H, int64_t I, int quant_type, int num_threads, int tp,
-                             mi_moe_cpu** out) {
+namespace {
+template <class Make>
+int cpu_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe_cpu** out, Make make) {
   if (!out) return fail(MI_MOE_EINVAL, "out is null");
   *out = nullptr;
   if (E <= 0 || H <= 0 || I <= 0) return fail(MI_MOE_EINVAL, "E, H, I must be positive");
   if (quant_type != MI_MOE_Q8_0 && quant_type != MI_MOE_Q4_0)
     return fail(MI_MOE_EUNSUPPORTED, "the CPU engine runs Q8_0 and Q4_0 (quant_type 0 / 1)");
   if (H % 32 != 0 || I % 32 != 0) return fail(MI_MOE_EINVAL, "hidden and intermediate sizes must be multiples of 32");
-  if (num_threads < 0 || tp < 0) return fail(MI_MOE_EINVAL, "num_threads and tp must be >= 0");
   mi_moe_cpu* c = new (std::nothrow) mi_moe_cpu();
   if (!c) return fail(MI_MOE_EINVAL, "out of host memory");
   try {
-    c->eng = new mimoe_cpu::Engine(E, H, I, quant_type, num_threads, tp);
+    c->eng = make();
   } catch (const std::exception& ex) {
     delete c;
     return fail(MI_MOE_EINVAL, ex.what());
@@ -58,6 +58,22 @@ MI_API int mi_moe_cpu_create(int64_t E, int64_t H, int64_t I, int quant_type, in
   }
   *out = c;
   return MI_MOE_OK;
+}
+}  // namespace
+
+MI_API int mi_moe_cpu_create(int64_t E, int64_t H, int64_t I, int quant_type, int num_threads, int tp,
+                             mi_moe_cpu** out) {
+  if (num_threads < 0 || tp < 0) return fail(MI_MOE_EINVAL, "num_threads and tp must be >= 0");
+  return cpu_create(E, H, I, quant_type, out,
+                    [&] { return new mimoe_cpu::Engine(E, H, I, quant_type, num_threads, tp); });
+}
+
+MI_API int mi_moe_cpu_create_numa(int64_t E, int64_t H, int64_t I, int quant_type, int tp, int threads_per_node,
+                                  mi_moe_cpu** out) {
+  if (tp < 0 || threads_per_node < 0) return fail(MI_MOE_EINVAL, "tp and threads_per_node must be >= 0");
+  return cpu_create(E, H, I, quant_type, out, [&] {
+    return new mimoe_cpu::Engine(E, H, I, quant_type, mimoe_cpu::Engine::NumaLayout{}, tp, threads_per_node);
+  });
 }
 
 MI_API int mi_moe_cpu_destroy(mi_moe_cpu* c) {

@@ -862,6 +862,33 @@ Engine::Engine(int64_t E, int64_t H, int64_t I, int qt, int max_threads, int tp)
   scratch_.resize((size_t)tp_);
 }
 
+Engine::Engine(int64_t E, int64_t H, int64_t I, int qt, NumaLayout, int tp, int threads_per_node)
+    : E_(E), H_(H), I_(I), qt_(qt), isa_(detect_isa()) {
+  topo_ = host_topology(0);
+  const std::vector<std::vector<int>>& nodes = topo_.node_cpus;
+  const int ntp = tp > 0 ? tp : (int)std::max<size_t>(1, nodes.size());
+  std::vector<std::vector<int>> groups;
+  if ((int)nodes.size() >= ntp) {
+    for (int s = 0; s < ntp; ++s) groups.push_back(nodes[(size_t)s]);
+  } else {
+    std::vector<int> all;
+    for (auto& g : nodes) all.insert(all.end(), g.begin(), g.end());
+    if (all.empty()) all.push_back(0);
+    groups.assign((size_t)ntp, {});
+    for (size_t i = 0; i < all.size(); ++i) groups[i * (size_t)ntp / all.size()].push_back(all[i]);
+    for (auto& g : groups)
+      if (g.empty()) g.push_back(all[0]);
+  }
+  for (auto& g : groups)
+    if (threads_per_node > 0 && (int)g.size() > threads_per_node) g.resize((size_t)threads_per_node);
+  tp_ = (int)groups.size();
+  for (auto& g : groups) pools_.emplace_back(new NodePool(g));
+  threads_ = 0;
+  for (auto& p : pools_) threads_ += p->size();
+  shards_.resize((size_t)tp_);
+  scratch_.resize((size_t)tp_);
+}
+
 Engine::~Engine() = default;
 
 bool Engine::shape_ok() const {

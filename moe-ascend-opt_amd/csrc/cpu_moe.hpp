@@ -92,6 +92,13 @@ class Engine {
   // max_threads 0: every CPU of the affinity mask; tp 0: one shard per NUMA
   // node holding chosen CPUs.
   Engine(int64_t E, int64_t H, int64_t I, int quant, int max_threads, int tp);
+  // The reference's NUMA layout (Int8-gemm/moe_infer.cpp:25-36,
+  // numa_threadpool.h:498-504): tp shards (0: one per NUMA node of the
+  // affinity mask), shard s on node s with threads_per_node of its CPUs (0:
+  // all).  With fewer nodes than tp the affinity CPUs are split into tp
+  // groups in order, each cut to threads_per_node.
+  struct NumaLayout {};
+  Engine(int64_t E, int64_t H, int64_t I, int quant, NumaLayout, int tp, int threads_per_node);
   ~Engine();
   bool shape_ok() const;
   // wire layout of store_quantized_weights_repack (Int8-gemm/moe_infer.cpp:96-282)

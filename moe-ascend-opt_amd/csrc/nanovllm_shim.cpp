@@ -42,6 +42,17 @@ void* stream_of(const at::Tensor& ref) {
   return (void*)c10::hip::getCurrentHIPStream().stream();
 }
 
+// The reference's CPU layout variables (Int8-gemm/moe_infer.cpp:25,
+// Int8-gemm/numa_threadpool.h:498-504, README.md:179): -1 when unset.
+int64_t env_int(const char* name) {
+  const char* s = getenv(name);
+  if (!s || !*s) return -1;
+  char* end = nullptr;
+  const long long v = strtoll(s, &end, 10);
+  TORCH_CHECK(end && *end == '\0', name, "=", s, " is not an integer");
+  return v;
+}
+
 // Host threads of the CPU path: MIMOE_CPU_THREADS, else OMP_NUM_THREADS, else
 // every CPU of the affinity mask (0).
 int host_threads() {
@@ -88,8 +99,23 @@ struct MoEInferHandle : torch::CustomClassHolder {
     TORCH_CHECK(h != nullptr, "MoEInfer: no HIP device for this call");
     return h;
   }
+  // NANOVLLM_TP_SIZE / NANOVLLM_TP_THREADS_PER_NODE, when set, give the
+  // reference's layout: tp shards over NUMA nodes, that many threads per node
+  // (the reference's default tp of 2 fails on one-node hosts, so unset means
+  // one shard per NUMA node here); otherwise MIMOE_CPU_THREADS /
+  // OMP_NUM_THREADS threads over whole nodes.
   mi_moe_cpu* host_engine() {
-    if (!cpu) check_status(mi_moe_cpu_create(E, H, I, (int)quant_type, host_threads(), 0, &cpu), "MoEInfer (host)");
+    if (!cpu) {
+      const int64_t tp = env_int("NANOVLLM_TP_SIZE"), per = env_int("NANOVLLM_TP_THREADS_PER_NODE");
+      if (tp >= 0 || per >= 0) {
+        TORCH_CHECK(tp != 0 && tp < 0x10000, "tp_size must be >= 1 (NANOVLLM_TP_SIZE=", tp, ")");
+        check_status(mi_moe_cpu_create_numa(E, H, I, (int)quant_type, tp > 0 ? (int)tp : 0,
+                                            per > 0 ? (int)std::min<int64_t>(per, 1 << 20) : 0, &cpu),
+                     "MoEInfer (host)");
+      } else {
+        check_status(mi_moe_cpu_create(E, H, I, (int)quant_type, host_threads(), 0, &cpu), "MoEInfer (host)");
+      }
+    }
     return cpu;
   }
   mi_moe_hybrid* host_w4() {

@@ -46,7 +46,7 @@ C_SYMBOLS = (
     "mi_moe_hybrid_store_awq", "mi_moe_hybrid_forward", "mi_moe_hybrid_host_forward",
     "mi_moe_hybrid_get_stats", "mi_moe_cpu_create", "mi_moe_cpu_destroy", "mi_moe_cpu_store_quantized",
     "mi_moe_cpu_quantize_and_store_expert", "mi_moe_cpu_forward", "mi_moe_cpu_get_info", "mi_moe_cpu_set_isa",
-    "mi_moe_cpu_isa_name", "mi_moe_cpu_topk_softmax",
+    "mi_moe_cpu_isa_name", "mi_moe_cpu_topk_softmax", "mi_moe_cpu_create_numa",
 )
 
 
@@ -116,6 +116,7 @@ def capi():
     L.mi_moe_cpu_get_info.argtypes = [P, P, P, P, P, P, P]
     L.mi_moe_cpu_set_isa.argtypes = [P, I]
     L.mi_moe_cpu_topk_softmax.argtypes = [P, I64, I64, I64, I, P, P]
+    L.mi_moe_cpu_create_numa.argtypes = [I64, I64, I64, I, I, I, ctypes.POINTER(P)]
     L.mi_moe_cpu_isa_name.restype = ctypes.c_char_p
     L.mi_moe_cpu_isa_name.argtypes = [I]
     for name in C_SYMBOLS:

@@ -115,9 +115,25 @@ def build_shim(verbose: bool = False) -> str:
     return SHIM
 
 
+FLOOR = os.path.join(PKG_DIR, "mimoe_read_floor")
+
+
+def build_read_floor(verbose: bool = False) -> str:
+    """The read-only floor probe (csrc/read_floor.hip): a standalone HIP program
+    that `bench.py --read-floor` runs."""
+    tmp = FLOOR + ".tmp"
+    out = _run([HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17", *NO_PK_FP32,
+                os.path.join(CSRC, "read_floor.hip"), "-o", tmp])
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, FLOOR)
+    return FLOOR
+
+
 def build_all(verbose: bool = False):
     build_lib(verbose)
     build_shim(verbose)
+    build_read_floor(verbose)
     return LIB, SHIM
 
 

@@ -39,20 +39,36 @@ def w4a16_random(E, H, I, seed, scale_dtype=torch.bfloat16, group=128):
     return w13_q, w13_z, w13_s, w2_q, w2_z, w2_s
 
 
-def w4a16_from_normal(E, H, I, seed, scale_dtype=torch.bfloat16, group=128, std=0.02):
-    """The BASELINE recipe: fp weights ~ N(0, std^2) quantized AWQ-style."""
-    g = torch.Generator().manual_seed(seed)
-    w1 = torch.randn(E, 2 * I, H, generator=g) * std
-    w2 = torch.randn(E, H, I, generator=g) * std
-    a = fmt.awq_quantize(w1, group, scale_dtype)
-    b = fmt.awq_quantize(w2, group, scale_dtype)
+def w4a16_from_normal(E, H, I, seed, scale_dtype=torch.bfloat16, group=128, std=0.02, device="cpu"):
+    """The BASELINE recipe: fp weights ~ N(0, std^2) quantized AWQ-style (on
+    `device`; the wire tensors are returned on the CPU)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    w1 = torch.randn(E, 2 * I, H, generator=g, device=device) * std
+    a = [t.cpu() for t in fmt.awq_quantize(w1, group, scale_dtype)]
+    del w1
+    w2 = torch.randn(E, H, I, generator=g, device=device) * std
+    b = [t.cpu() for t in fmt.awq_quantize(w2, group, scale_dtype)]
     return a[0], a[1], a[2], b[0], b[1], b[2]
 
 
 def max_rel_err(y, ref):
+    """max |y - ref| over the whole output / max |ref| (the north star's measure)."""
     y = y.to(torch.float64)
     ref = ref.to(torch.float64)
     return float((y - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+def token_rel_err(y, ref):
+    """The same measure per token (row), worst token: a token whose output is
+    small next to the batch maximum is held to its own scale."""
+    y = y.to(torch.float64).reshape(ref.shape[0], -1)
+    ref = ref.to(torch.float64).reshape(ref.shape[0], -1)
+    num = (y - ref).abs().amax(dim=1)
+    den = ref.abs().amax(dim=1)
+    live = den > 0
+    if not bool(live.any()):
+        return float(num.max())
+    return float((num[live] / den[live]).max())
 
 
 def zipf_routing(T, E, K, seed, alpha=1.2):

@@ -90,6 +90,38 @@ def test_engine_bit_exact_vs_oracle(qt, T, K, threads, tp):
         L.mi_moe_cpu_destroy(c)
 
 
+@pytest.mark.parametrize("tp,per", [(2, 2), (2, 0), (3, 1), (0, 0)])
+def test_numa_layout_engine(tp, per):
+    """mi_moe_cpu_create_numa: the reference's layout (tp shards, one per NUMA
+    node, per threads each); on a host with fewer nodes the affinity CPUs are
+    split into tp groups.  The shards sum in shard order, bit-equal to the
+    oracle at that tp."""
+    import os
+    E, H, I, T, K, qt = 12, 256, 192, 6, 8, 0
+    ws = _q_weights(qt, E, H, I, 61, torch.float16)
+    L = nm.capi()
+    c = ctypes.c_void_p()
+    nm.check(L.mi_moe_cpu_create_numa(E, H, I, qt, tp, per, ctypes.byref(c)), "cpu_create_numa")
+    try:
+        a, b, cq, d = [np.ascontiguousarray(t) if isinstance(t, np.ndarray) else t.contiguous() for t in ws]
+        ptr = lambda t: t.ctypes.data if isinstance(t, np.ndarray) else t.data_ptr()
+        nm.check(L.mi_moe_cpu_store_quantized(c, ptr(a), ptr(b), ptr(cq), ptr(d), 0), "cpu_store")
+        thr, tpu, nodes = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        nm.check(L.mi_moe_cpu_get_info(c, ctypes.byref(thr), ctypes.byref(tpu), None, None, ctypes.byref(nodes),
+                                       None), "info")
+        want_tp = tp if tp > 0 else max(1, nodes.value)
+        assert tpu.value == want_tp
+        cpus = len(os.sched_getaffinity(0))
+        if per > 0 and cpus >= want_tp * per:
+            assert thr.value == want_tp * per
+        ids, tw = topk_routing(T, E, K, seed=62)
+        x = (torch.randn(T, H, generator=torch.Generator().manual_seed(63)) * 0.8).to(torch.bfloat16)
+        y = _forward(L, c, x, ids, tw)
+        assert np.array_equal(bits(y), _oracle(qt, x, ids, tw, ws, E, I, want_tp))
+    finally:
+        L.mi_moe_cpu_destroy(c)
+
+
 @pytest.mark.parametrize("qt", [0, 1])
 @pytest.mark.parametrize("adt", [torch.bfloat16, torch.float16])
 def test_engine_special_values_bit_exact(qt, adt):

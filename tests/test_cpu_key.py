@@ -27,6 +27,8 @@ from test_oracle_forward import _q_weights
 @pytest.fixture(autouse=True)
 def _host_weights(monkeypatch):
     monkeypatch.setenv("MIMOE_HOST_WEIGHTS", "1")
+    monkeypatch.delenv("NANOVLLM_TP_SIZE", raising=False)
+    monkeypatch.delenv("NANOVLLM_TP_THREADS_PER_NODE", raising=False)
     nanovllm_moe.load()
 
 
@@ -158,3 +160,32 @@ def test_reference_device_op_names_on_cpu():
         torch.ops.nanovllm.moe_forward_npu_graph_out(x.half(), ids, tw, h, ctx, out.half())
     with pytest.raises(RuntimeError, match="dtype must be"):
         torch.classes.nanovllm.MoEGraphContext(h, 8, K, 2)
+
+
+def test_reference_env_contract(monkeypatch):
+    """NANOVLLM_TP_SIZE / NANOVLLM_TP_THREADS_PER_NODE keep the reference's
+    meaning (Int8-gemm/moe_infer.cpp:25-36, Int8-gemm/numa_threadpool.h:498-504,
+    README.md:179): with NANOVLLM_TP_SIZE=2 on a one-node host the CPU key runs
+    two tp shards, bit-equal to the oracle at tp=2 (whose shard-order sum
+    differs from tp=1 here); tp_size 0 is refused as in the reference."""
+    E, H, I, T, K, qt = 16, 1024, 512, 16, 8, 0
+    ws = _q_weights(qt, E, H, I, 4, torch.float16)
+    ids, tw = topk_routing(T, E, K, seed=5)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(6)).to(torch.float16)
+    acode, scode = 0, 0
+    refs = {tp: oracle.moe_forward_q(qt, acode, scode, bits(x), tw.numpy(), ids.numpy(), np.asarray(ws[0]),
+                                     bits(ws[1]), np.asarray(ws[2]), bits(ws[3]), E, I, tp=tp)[0] for tp in (1, 2)}
+    assert not np.array_equal(refs[1], refs[2])
+    load = lambda h: h.store_quantized_repack(*[torch.from_numpy(np.ascontiguousarray(t))
+                                                if isinstance(t, np.ndarray) else t for t in ws])
+    monkeypatch.setenv("NANOVLLM_TP_SIZE", "2")
+    monkeypatch.setenv("NANOVLLM_TP_THREADS_PER_NODE", "2")
+    h = torch.classes.nanovllm.MoEInfer(E, H, I, qt)
+    load(h)
+    y = torch.ops.nanovllm.moe_forward(x, ids, tw, h)
+    assert np.array_equal(bits(y), refs[2])
+    monkeypatch.setenv("NANOVLLM_TP_SIZE", "0")
+    with pytest.raises(RuntimeError, match="tp_size must be >= 1"):   # when the host engine is made
+        h0 = torch.classes.nanovllm.MoEInfer(E, H, I, qt)
+        load(h0)
+        torch.ops.nanovllm.moe_forward(x, ids, tw, h0)

@@ -10,7 +10,7 @@ import torch
 
 import nanovllm_moe
 import oracle
-from helpers import bits, from_bits, max_rel_err, topk_routing, w4a16_from_normal, w4a16_random
+from helpers import bits, from_bits, max_rel_err, token_rel_err, topk_routing, w4a16_from_normal, w4a16_random
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
@@ -267,6 +267,33 @@ def test_normal_weights_recipe(cuda):
 
 
 @pytest.fixture(scope="module")
+def qwen_recipe(cuda):
+    """BASELINE config 2 exactly: E=128, H=2048, I=768, AWQ int4 from N(0, 0.02)
+    weights, group 128, bf16 scales."""
+    E, H, I = 128, 2048, 768
+    w = w4a16_from_normal(E, H, I, seed=2, device=cuda)
+    return w, _handle(E, H, I, w, True, cuda)
+
+
+@pytest.mark.parametrize("bs", [1, 8])
+def test_config2_recipe_parity(cuda, qwen_recipe, bs):
+    """The headline configuration against the oracle's fp32 result, over the
+    whole output and per token (each token held to its own scale)."""
+    w, h = qwen_recipe
+    E, H, I = 128, 2048, 768
+    g = torch.Generator().manual_seed(1000 + bs)
+    x = torch.randn(bs, H, generator=g).to(torch.bfloat16)
+    val, ids = torch.topk(torch.randn(bs, E, generator=g), 8, dim=-1)
+    tw = torch.softmax(val, dim=-1).float()
+    ids = ids.to(torch.int32)
+    y = _run(h, x, ids, tw, cuda)
+    ref = _oracle(x, ids, tw, w, E, I, torch.bfloat16)
+    err, terr = max_rel_err(y, ref), token_rel_err(y, ref)
+    print(f"[config2 bs={bs}] max_rel_err {err:.2e}, worst per-token {terr:.2e}", flush=True)
+    assert err <= TOL and terr <= TOL
+
+
+@pytest.fixture(scope="module")
 def qwen(cuda):
     E, H, I = 128, 2048, 768
     w = w4a16_random(E, H, I, seed=2024)
@@ -280,7 +307,9 @@ def test_qwen_shape_parity(cuda, qwen, bs):
     ids, tw = topk_routing(bs, E, 8, seed=bs)
     x = torch.randn(bs, H, generator=torch.Generator().manual_seed(bs)).to(torch.bfloat16)
     y = _run(h, x, ids, tw, cuda)
-    assert max_rel_err(y, _oracle(x, ids, tw, w, E, I, torch.bfloat16)) <= TOL
+    ref = _oracle(x, ids, tw, w, E, I, torch.bfloat16)
+    assert max_rel_err(y, ref) <= TOL
+    assert token_rel_err(y, ref) <= TOL
 
 
 def test_minimax_shape_parity(cuda):
