@@ -124,8 +124,10 @@ constexpr int kW4FusedMaxPairs = 64;
 // zeroed (no dispatch has tag 0).  The one-launch kernel serves I <= kTagActMaxI.
 constexpr int kTagActMaxI = 4096;
 __host__ __device__ constexpr size_t tagged_act_bytes(int I) { return (size_t)64 * I * 4 + 64; }
+// red [2][S][...] (double-buffered: a unit's sums while the previous unit's
+// epilogue reads its own) | metadata [S][80*G1] | hidden rows
 inline size_t w4_fused_gate_up_lds_bytes(int H, int xrows, int NW) {
-  return (size_t)(kW4FusedWaves / NW) * (p1_red_bytes(NW) + 80 * (H >> 7)) + (size_t)xrows * H * 2;
+  return (size_t)(kW4FusedWaves / NW) * (2 * p1_red_bytes(NW) + 80 * (H >> 7)) + (size_t)xrows * H * 2;
 }
 // act rows [8][I] | w2 metadata [8][RT][SEC] | outputs [8][16 RT] f32 |
 // state [8] | routing weights [8] f32
@@ -137,6 +139,7 @@ struct W4FusedPlan {
   int nw, njs;     // gate_up: waves splitting H per slice (8 or 4), slice blocks per item
   int nb1, nb2;    // load batches (groups) of the gate_up and down roles
   int rt;          // 16-row tiles of H per down item (1 or 2)
+  int ngu;         // gate_up workgroups (each takes every ngu-th item)
   size_t lds;
 };
 

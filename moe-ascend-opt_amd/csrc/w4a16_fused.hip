@@ -44,6 +44,12 @@ namespace mimoe {
 constexpr int kFusedWaves = kW4FusedWaves;
 constexpr int kSpinMax = 1 << 18;   // polls of one wait (each at least one memory round trip)
 constexpr int kUnitBatch = 6;       // act units per lane loaded together by a down wave (I = 768: all)
+// From this many gate_up items per resident-workgroup slot on, the gate_up
+// workgroups fill the slots and each takes several items (pipelined); below
+// it, one workgroup per item.  Same-box graph replays: at 3 items per slot
+// (bs 8) the pipelined form is 0.7 us faster per layer, at 1.5 (bs 4) 0.2 us
+// slower, and with half or three quarters of the slots slower at every size.
+constexpr long kPipelinedItemsPerSlot = 2;
 
 __device__ __forceinline__ unsigned long long load_agent(const unsigned long long* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -67,14 +73,16 @@ __device__ __forceinline__ unsigned dispatch_tag32() {
 }
 
 // ---------------------------------------------------------------- gate_up role
-// LDS: red [S][NW][gate,up][64][4] f32 | metadata [S][80*G1] | hidden rows.
+// One item per workgroup (the grid holds every item): item (pair, block js of
+// S slices).  LDS: red [S][NW][gate,up][64][4] f32 | metadata [S][80*G1] |
+// hidden rows (the pipelined role's layout, its second reduction buffer unused).
 template <int ACT, int SDT, int NB, int NW, int S>
-__device__ __forceinline__ void fused_gate_up(const SchedArgs& c, const W4Args& a, const char* w13,
+__device__ __forceinline__ void fused_gate_up_one(const SchedArgs& c, const W4Args& a, const char* w13,
                                               const unsigned char* w13_m, int item, int js,
                                               unsigned char* smem) {
   const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, P = a.p1_cols, HI = H >> 3;
   float* red = reinterpret_cast<float*>(smem);
-  unsigned char* meta = smem + S * p1_red_bytes(NW);
+  unsigned char* meta = smem + 2 * S * p1_red_bytes(NW);
   uint16_t* xs = reinterpret_cast<uint16_t*>(meta + S * 80 * G1);
   const int j0 = js * S;
   // wave index, slice group and expert are uniform: SGPRs (weight addresses
@@ -185,6 +193,176 @@ __device__ __forceinline__ void fused_gate_up(const SchedArgs& c, const W4Args& 
     }
     __syncthreads();   // red and xs are reused by the next pass
   }
+}
+
+// Pipelined gate_up role (at least kPipelinedItemsPerSlot items per slot):
+// workgroup g takes the items g, g + NG, g + 2 NG, ... (item = pair x block of
+// S slices); an item serves its expert iff its pair is the expert's first
+// pair.  The ids are read once per workgroup and every item's routing
+// (ballots over them) needs no memory access, so an item that does not serve
+// costs nothing.  Units (an item's passes of P token columns) are software
+// pipelined: a unit's metadata / hidden-row copies and first weight batch are
+// issued, then the previous unit's epilogue (cross-wave sums, SiLU*mul, act
+// stores) runs from the other reduction buffer while they arrive.
+// LDS: red [2][S][NW][gate,up][64][4] f32 | metadata [S][80*G1] | hidden rows.
+template <int ACT, int SDT, int NB, int NW, int S>
+__device__ __forceinline__ void fused_gate_up(const SchedArgs& c, const W4Args& a, const char* w13,
+                                              const unsigned char* w13_m, int g, int NG, int njs,
+                                              unsigned char* smem) {
+  const int H = c.H, G1 = H >> 7, NI1 = c.I >> 4, HI = H >> 3;
+  // token columns per pass: all 16 MFMA columns when every hidden row is in LDS
+  const int P = a.x_all ? 16 : a.p1_cols;
+  const int RB = p1_red_bytes(NW) / 4;   // floats of one slice's reduction buffer
+  float* red = reinterpret_cast<float*>(smem);
+  unsigned char* meta = smem + 2 * S * p1_red_bytes(NW);
+  uint16_t* xs = reinterpret_cast<uint16_t*>(meta + S * 80 * G1);
+  // wave index and slice group are uniform: SGPRs (weight addresses are a
+  // scalar base plus the lane's 16-byte offset)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int sg = wave / NW, wi = wave - sg * NW;
+  const int q = lane >> 4, r = lane & 15;
+  const unsigned lane16 = 16u * (unsigned)lane;
+  if (a.x_all)   // uniform; x is [T][H] contiguous
+    stage_lds(reinterpret_cast<unsigned char*>(xs), c.T * HI, wave, kFusedWaves, lane,
+              [&](int k) { return (const void*)(c.x + 8 * (size_t)k); });
+  // the routing's inputs, read once: lane l holds pair l's expert id
+  const int myid = lane < c.n ? c.ids[lane] : -1;
+  const bool myvalid = lane < c.n && (unsigned)myid < (unsigned)c.E;
+  const float rk = 1.0f / (float)c.K;
+  auto tok_of = [&](int pair) { return div_small(pair, rk); };
+  const unsigned tag = dispatch_tag32();
+  const int g0 = G1 * wi / NW, ng = G1 * (wi + 1) / NW - g0;   // equal for all waves (G1 % NW == 0)
+  const unsigned char* ms = meta + sg * 80 * G1;
+  constexpr float off = W4Consts<ACT>::offset;
+  // the previous unit, whose epilogue is pending
+  bool pend = false;
+  int p_buf = 0, p_ncol = 0, p_j0 = 0, p_cb0 = 0, p_colpair = 0;
+  auto epilogue = [&]() {
+    if (tid < 64 * S) {   // wave s sums slice s: lane ln holds row ln & 15 of columns 4(ln >> 4)..+3
+      const int s = tid >> 6, ln = tid & 63;
+      const float* rs = red + (p_buf * S + s) * RB;
+      f32x4_t gs = *reinterpret_cast<const f32x4_t*>(rs + ((0 * 2 + 0) * 64 + ln) * 4);
+      f32x4_t us = *reinterpret_cast<const f32x4_t*>(rs + ((0 * 2 + 1) * 64 + ln) * 4);
+#pragma unroll
+      for (int w = 1; w < NW; ++w) {
+        gs += *reinterpret_cast<const f32x4_t*>(rs + ((w * 2 + 0) * 64 + ln) * 4);
+        us += *reinterpret_cast<const f32x4_t*>(rs + ((w * 2 + 1) * 64 + ln) * 4);
+      }
+      const float gv[4] = {gs.x, gs.y, gs.z, gs.w}, uv[4] = {us.x, us.y, us.z, us.w};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int col = p_cb0 + 4 * (ln >> 4) + v;
+        const int pr = __shfl(p_colpair, col & 63);
+        // rows r and r^1 are lanes ln and ln^1: one tagged unit per row pair;
+        // the 8 units of a (pair, slice) are one 64-byte line
+        const uint32_t bits = from_f32<ACT>(silu_mul_fast(gv[v], uv[v]));
+        const uint32_t other = (uint32_t)__shfl_xor((int)bits, 1);
+        // only the pass's ncol columns hold its results (the other MFMA
+        // columns repeat its last one): a unit is stored once, final
+        if (4 * (ln >> 4) + v < p_ncol && (ln & 1) == 0)
+          store_agent(a.tact + (size_t)pr * (c.I >> 1) + 8 * (p_j0 + s) + ((ln & 15) >> 1),
+                      ((unsigned long long)tag << 32) | bits | (other << 16));
+      }
+    }
+  };
+  const int n_items = c.n * njs;
+  int unit = 0;
+  for (int item = g; item < n_items; item += NG) {
+    const int pi = item / njs, js = item - pi * njs;   // uniform
+    // routing by ballots (pair pi serves iff it is its expert's first pair);
+    // column j of the expert is its j-th pair in ascending order, the order of
+    // the reference's stable counting sort (moe_common.cpp:146-216)
+    const int e = __shfl(myid, pi);
+    const uint64_t match = __ballot(myvalid && myid == e);
+    if (!((unsigned)e < (unsigned)c.E && (__ffsll((long long)match) - 1) == pi)) continue;   // uniform
+    const int cnt = __builtin_amdgcn_readfirstlane(__popcll(match));
+    const bool inm = (match >> lane) & 1;
+    const uint64_t lt = lanemask_lt(lane);
+    const int dst = inm ? __popcll(match & lt) : cnt + __popcll(~match & lt);
+    const int colpair = __builtin_amdgcn_ds_permute(dst << 2, lane);   // lane l: pair of column l
+    const int eu = __builtin_amdgcn_readfirstlane(e);
+    const int j0 = js * S;
+    const size_t blk = (size_t)eu * NI1 + j0;   // S consecutive slices: contiguous weights and metadata
+    const char* wg = w13 + ((blk + sg) * 2 * G1 + g0) * 1024;     // gate: + g KB, up: + (G1 + g) KB
+    for (int cb0 = 0; cb0 < cnt; cb0 += P, ++unit) {
+      const int ncol = min(P, cnt - cb0);
+      // this unit's LDS operands (the previous unit's readers passed the last barrier)
+      if (cb0 == 0) {
+        const unsigned char* msrc = w13_m + blk * 80 * G1;
+        stage_lds(meta, S * 5 * G1, wave, kFusedWaves, lane, [&](int k) { return (const void*)(msrc + 16 * k); });
+      }
+      int xr;   // LDS row of this lane's column
+      if (a.x_all) {
+        xr = tok_of(__shfl(colpair, (cb0 + min(r, ncol - 1)) & 63));
+      } else {
+        // the pass's hidden rows: row cc at xs + cc * H, in 1 KB chunks (H % 512 == 0)
+        for (int cc = 0; cc < ncol; ++cc) {   // uniform
+          const char* src =
+              reinterpret_cast<const char*>(c.x + (size_t)tok_of(__shfl(colpair, (cb0 + cc) & 63)) * H) + 16 * lane;
+          unsigned char* xd = reinterpret_cast<unsigned char*>(xs + (size_t)cc * H);
+          for (int ch = wave; ch < (HI >> 6); ch += kFusedWaves)
+            __builtin_amdgcn_global_load_lds(src + 1024 * ch, xd + 1024 * ch, 16, 0, 0);
+        }
+        xr = min(r, ncol - 1);
+      }
+      const uint16_t* xrow = xs + xr * H + 32 * q;
+      issue_order_fence();
+      u32x4_t wgv[NB], wuv[NB];
+#pragma unroll
+      for (int gi = 0; gi < NB; ++gi) {
+        const char* p = wg + (size_t)gi * 1024;
+        wgv[gi] = ldg16(p + lane16);
+        wuv[gi] = ldg16(p + (size_t)G1 * 1024 + lane16);
+      }
+      wait_copies_and_sync<2 * NB>();   // metadata and x rows are in LDS
+      if (pend) epilogue();   // the previous unit, while this unit's weights arrive
+      f32x4_t accg = {0, 0, 0, 0}, accu = {0, 0, 0, 0};
+      for (int gb = 0; gb < ng; gb += NB) {
+        if (gb > 0) {
+#pragma unroll
+          for (int gi = 0; gi < NB; ++gi) {
+            const char* p = wg + (size_t)(gb + gi) * 1024;
+            wgv[gi] = ldg16(p + lane16);
+            wuv[gi] = ldg16(p + (size_t)G1 * 1024 + lane16);
+          }
+        }
+#pragma unroll
+        for (int gi = 0; gi < NB; ++gi) {
+          const int gg = g0 + gb + gi;
+          u32x4_t A[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) A[i] = lds16(xrow + 128 * gg + 8 * i);
+          f32x4_t X = {0, 0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) X = mfma16<ACT>(A[i], ones4<ACT>(), X);
+          f32x4_t Gg = {0, 0, 0, 0}, Gu = {0, 0, 0, 0};
+          const uint32_t wgw[4] = {wgv[gi].x, wgv[gi].y, wgv[gi].z, wgv[gi].w};
+          const uint32_t wuw[4] = {wuv[gi].x, wuv[gi].y, wuv[gi].z, wuv[gi].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            Gg = mfma16<ACT>(A[i], deq4<ACT>(wgw[i]), Gg);
+            Gu = mfma16<ACT>(A[i], deq4<ACT>(wuw[i]), Gu);
+          }
+          const uint32_t sc = reinterpret_cast<const uint32_t*>(ms)[r * G1 + gg];
+          const uint32_t zz = ms[64 * G1 + r * G1 + gg];
+          fold(accg, Gg, X, scale_of<SDT>(sc & 0xffffu), off + (float)(zz & 0xfu));
+          fold(accu, Gu, X, scale_of<SDT>(sc >> 16), off + (float)(zz >> 4));
+        }
+      }
+      float* rsw = red + ((unit & 1) * S + sg) * RB;
+      *reinterpret_cast<f32x4_t*>(rsw + ((wi * 2 + 0) * 64 + lane) * 4) = accg;
+      *reinterpret_cast<f32x4_t*>(rsw + ((wi * 2 + 1) * 64 + lane) * 4) = accu;
+      __syncthreads();   // the sums are visible; metadata and x rows are free for the next unit
+      pend = true;
+      p_buf = unit & 1;
+      p_ncol = ncol;
+      p_j0 = j0;
+      p_cb0 = cb0;
+      p_colpair = colpair;
+    }
+  }
+  if (pend) epilogue();
+  else __builtin_amdgcn_s_waitcnt(0);   // served nothing: no hidden-row copy outlives the workgroup
 }
 
 // ---------------------------------------------------------------- down role
@@ -337,9 +515,13 @@ void w4a16_decode_kernel(const int32_t* ids, const uint16_t* x, const char* w13,
   c.ids = ids;
   c.x = x;
   const int b = blockIdx.x;
-  if (b < n1) {   // uniform
-    const int item = b / njs;
-    fused_gate_up<ACT, SDT, NB1, NW, S>(c, a, w13, w13_m, item, b - item * njs, smem);
+  if (b < n1) {   // uniform: n1 gate_up workgroups, then the down items
+    if (n1 == c.n * njs) {   // one workgroup per item
+      const int item = b / njs;
+      fused_gate_up_one<ACT, SDT, NB1, NW, S>(c, a, w13, w13_m, item, b - item * njs, smem);
+    } else {
+      fused_gate_up<ACT, SDT, NB1, NW, S>(c, a, w13, w13_m, b, n1, njs, smem);
+    }
   } else {
     const int nt = (c.H >> 4) / RT, d = b - n1, t = d / nt;
     fused_down<ACT, SDT, NB2, RT>(c, a, w2, w2_m, t, RT * (d - t * nt), smem);
@@ -347,25 +529,26 @@ void w4a16_decode_kernel(const int32_t* ids, const uint16_t* x, const char* w13,
 }
 
 template <int ACT, int SDT, int NB1, int NW, int S, int NB2, int RT>
-static hipError_t launch_fused_t(const W4Args& a, int njs, size_t lds, hipStream_t st) {
+static hipError_t launch_fused_t(const W4Args& a, int njs, int ngu, size_t lds, hipStream_t st) {
   if (lds > kMaxLds)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_decode_kernel<ACT, SDT, NB1, NW, S, NB2, RT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  const int n1 = a.c.n * njs, n2 = a.c.T * (a.c.H >> 4) / RT;
+  const int n1 = ngu, n2 = a.c.T * (a.c.H >> 4) / RT;
   hipLaunchKernelGGL((w4a16_decode_kernel<ACT, SDT, NB1, NW, S, NB2, RT>), dim3(n1 + n2), dim3(kW4FusedWaves * kWave),
                      lds, st, a.c.ids, a.c.x, (const char*)a.w13, a.w13_m, (const char*)a.w2, a.w2_m, n1, njs, a);
   return hipGetLastError();
 }
 
 template <int ACT, int SDT, int NW, int S, int RT>
-static hipError_t dispatch_fused_nb(const W4Args& a, int nb1, int nb2, int njs, size_t lds, hipStream_t st) {
+static hipError_t dispatch_fused_nb(const W4Args& a, int nb1, int nb2, int njs, int ngu, size_t lds,
+                                    hipStream_t st) {
 #define FUSED_NB2(NB1_)                                                                        \
   if (nb1 == NB1_) {                                                                           \
-    if (nb2 == 6) return launch_fused_t<ACT, SDT, NB1_, NW, S, 6, RT>(a, njs, lds, st); \
-    if (nb2 == 4) return launch_fused_t<ACT, SDT, NB1_, NW, S, 4, RT>(a, njs, lds, st); \
-    if (nb2 == 3) return launch_fused_t<ACT, SDT, NB1_, NW, S, 3, RT>(a, njs, lds, st); \
-    if (nb2 == 2) return launch_fused_t<ACT, SDT, NB1_, NW, S, 2, RT>(a, njs, lds, st); \
-    if (nb2 == 1) return launch_fused_t<ACT, SDT, NB1_, NW, S, 1, RT>(a, njs, lds, st); \
+    if (nb2 == 6) return launch_fused_t<ACT, SDT, NB1_, NW, S, 6, RT>(a, njs, ngu, lds, st); \
+    if (nb2 == 4) return launch_fused_t<ACT, SDT, NB1_, NW, S, 4, RT>(a, njs, ngu, lds, st); \
+    if (nb2 == 3) return launch_fused_t<ACT, SDT, NB1_, NW, S, 3, RT>(a, njs, ngu, lds, st); \
+    if (nb2 == 2) return launch_fused_t<ACT, SDT, NB1_, NW, S, 2, RT>(a, njs, ngu, lds, st); \
+    if (nb2 == 1) return launch_fused_t<ACT, SDT, NB1_, NW, S, 1, RT>(a, njs, ngu, lds, st); \
   }
   FUSED_NB2(1) FUSED_NB2(2) FUSED_NB2(3) FUSED_NB2(4)
 #undef FUSED_NB2
@@ -374,9 +557,9 @@ static hipError_t dispatch_fused_nb(const W4Args& a, int nb1, int nb2, int njs, 
 
 template <int ACT, int SDT>
 static hipError_t dispatch_fused(const W4Args& a, const W4FusedPlan& p, hipStream_t st) {
-  if (p.nw == 8) return dispatch_fused_nb<ACT, SDT, 8, 1, 1>(a, p.nb1, p.nb2, p.njs, p.lds, st);
-  if (p.rt == 2) return dispatch_fused_nb<ACT, SDT, 4, 2, 2>(a, p.nb1, p.nb2, p.njs, p.lds, st);
-  return dispatch_fused_nb<ACT, SDT, 4, 2, 1>(a, p.nb1, p.nb2, p.njs, p.lds, st);
+  if (p.nw == 8) return dispatch_fused_nb<ACT, SDT, 8, 1, 1>(a, p.nb1, p.nb2, p.njs, p.ngu, p.lds, st);
+  if (p.rt == 2) return dispatch_fused_nb<ACT, SDT, 4, 2, 2>(a, p.nb1, p.nb2, p.njs, p.ngu, p.lds, st);
+  return dispatch_fused_nb<ACT, SDT, 4, 2, 1>(a, p.nb1, p.nb2, p.njs, p.ngu, p.lds, st);
 }
 
 // largest of {1, 2, 3, 4, 6} (up to cap) that divides need
@@ -400,7 +583,10 @@ W4FusedPlan w4a16_fused_plan(int T, int K, int H, int I, int x_all, int p1_cols,
   p.njs = (I / 16) / S;
   p.nb1 = fused_batch(G1 / p.nw, 4);
   p.nb2 = fused_batch(G2, 6);
-  const long slots = 2L * num_cu, n1 = (long)n * p.njs, tiles = (long)T * (H / 16);
+  const long slots = 2L * num_cu, items = (long)n * p.njs, tiles = (long)T * (H / 16);
+  // gate_up workgroups: one per item, or one per slot taking several items
+  const long n1 = items >= kPipelinedItemsPerSlot * slots ? slots : items;
+  p.ngu = (int)(n1 > 0 ? n1 : 1);
   p.rt = 1;
   if (p.nw == 4 && (H / 16) % 2 == 0 && (tiles > slots || (n1 + tiles > slots && n1 + tiles / 2 <= slots))) p.rt = 2;
   const size_t gate_up = w4_fused_gate_up_lds_bytes(H, x_all ? T : p1_cols, p.nw);
