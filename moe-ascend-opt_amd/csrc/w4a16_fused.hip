@@ -585,15 +585,21 @@ W4FusedPlan w4a16_fused_plan(int T, int K, int H, int I, int x_all, int p1_cols,
   p.nb2 = fused_batch(G2, 6);
   const long slots = 2L * num_cu, items = (long)n * p.njs, tiles = (long)T * (H / 16);
   // gate_up workgroups: one per item, or one per slot taking several items
-  const long n1 = items >= kPipelinedItemsPerSlot * slots ? slots : items;
+  const bool pipelined = items >= kPipelinedItemsPerSlot * slots;
+  const long n1 = pipelined ? slots : items;
   p.ngu = (int)(n1 > 0 ? n1 : 1);
   p.rt = 1;
   if (p.nw == 4 && (H / 16) % 2 == 0 && (tiles > slots || (n1 + tiles > slots && n1 + tiles / 2 <= slots))) p.rt = 2;
   const size_t gate_up = w4_fused_gate_up_lds_bytes(H, x_all ? T : p1_cols, p.nw);
   const size_t down = w4_fused_down_lds_bytes(I, p.rt);
   p.lds = gate_up > down ? gate_up : down;
+  // A down item that needs more than one weight batch (I/128 > 6) sits on the
+  // critical path when no pipelined gate_up work overlaps it: MiniMax-M2 shape
+  // (I = 1536) at bs 1, same-box graph replays, 22.7-22.9 us in one launch
+  // against 19.7-20.1 us in two; at bs 8 (pipelined) one launch is 1.5 us faster.
+  const bool down_chained = G2 > p.nb2 && !pipelined;
   p.ok = K <= kW4FusedWaves && n <= kW4FusedMaxPairs && G1 % p.nw == 0 && (I / 16) % S == 0 && I <= kTagActMaxI &&
-         p.lds <= device_max_lds();
+         !down_chained && p.lds <= device_max_lds();
   return p;
 }
 
