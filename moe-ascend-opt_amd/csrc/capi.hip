@@ -42,6 +42,8 @@ hipError_t launch_w4a16_gemm(const W4Args&, int, int, hipStream_t, hipEvent_t);
 W4FusedPlan w4a16_fused_plan(int, int, int, int, int, int, int);
 hipError_t launch_w4a16_fused(const W4Args&, const W4FusedPlan&, int, hipStream_t);
 hipError_t launch_qint(const QArgs&, int, int, int, int, int, bool, hipStream_t);
+size_t q_fused_lds(int, int, int, int, int);
+hipError_t launch_q_fused(const QArgs&, int, int, int, hipStream_t);
 hipError_t launch_qint_gemm(const QArgs&, int, int, int, hipStream_t);
 hipError_t launch_quant_route(const void*, int, int64_t, int64_t, int8_t*, float*, const int32_t*, int, int, int,
                               const RouteGlobal&, hipStream_t, int);
@@ -420,6 +422,7 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   a.w2 = h->w2.p; a.w2_d = (const uint16_t*)h->w2_s.p;
   a.act_q = (int8_t*)w.act;
   a.act_d = w.act_d;
+  a.tact = w.tact;
   if (gemm) {
     // sorted path: Q8_0 activations once per token, routing with row tiles,
     // the two int8 grouped GEMMs, the combine
@@ -428,6 +431,11 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
     HIPCHK(launch_quant_route(x, act, T, h->H, w.xq, w.xd, ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
     HIPCHK(launch_qint_gemm(a, h->quant, h->scale_dtype, (int)gemm_tiles_max(n, (int)h->E), st));
     HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
+    return MI_MOE_OK;
+  }
+  // the smallest calls in one launch (gate_up hands the intermediate to down inside it)
+  if (token_down && a.tact && q_fused_lds(in, iK, iH, iI, iE)) {
+    HIPCHK(launch_q_fused(a, h->quant, act, h->scale_dtype, st));
     return MI_MOE_OK;
   }
   if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
@@ -523,7 +531,7 @@ MI_API int mi_moe_create(int64_t E, int64_t H, int64_t I, int quant_type, mi_moe
     return fail(MI_MOE_EHIP, "HIP device query / event creation failed");
   }
   // the one-launch decode units (zeroed: no dispatch has tag 0)
-  if (I <= kTagActMaxI && quant_type == MI_MOE_W4A16 &&
+  if (I <= kTagActMaxI &&
       (h->tact.alloc(tagged_act_bytes((int)I)) != hipSuccess ||
        hipMemset(h->tact.p, 0, tagged_act_bytes((int)I)) != hipSuccess)) {
     mi_moe_destroy(h);

@@ -214,6 +214,31 @@ struct QArgs {
   float* act_d;            // [n, I/32] intermediate Q8_0 scales
   const int8_t* xq;        // [T, H] Q8_0 activations (grouped GEMM path)
   const float* xd;         // [T, H/32]
+  unsigned long long* tact;   // tagged intermediate units of the one-launch decode kernel
 };
+
+// One-launch Q8_0 / Q4_0 decode kernel (qint.hip): 8-wave workgroups, gate_up
+// items (pair, 32-row slice of I) for calls of up to kQDecWideMaxPairs routed
+// pairs, down items (token, 16-row tile of H) with a wave per routed expert
+// (top-k <= 8).  The intermediate Q8_0 row of a pair travels as q_tag_units(I)
+// tagged units in the hand-over buffer: I/4 units of 4 bytes, then I/32 units
+// of the blocks' fp32 scales (within tagged_act_bytes(I), whose last unit
+// records a wait that gave up).
+constexpr int kQFusedWaves = 8;
+constexpr int kQFusedMaxPairs = 12;
+__host__ __device__ constexpr int q_tag_units(int I) { return I / 4 + I / 32; }
+// The gate_up workgroups split K in two; the first half's gate and up sums
+// travel as units [pair][I/32 slices][64 rows] after the rows of
+// kQFusedMaxPairs pairs, below the timeout unit (64 * I/2).
+__host__ __device__ constexpr size_t q_part_unit0(int I) { return (size_t)kQFusedMaxPairs * q_tag_units(I); }
+static_assert(q_part_unit0(32) + (size_t)kQFusedMaxPairs * 2 * 32 <= (size_t)32 * 32, "Q units fit the buffer");
+static_assert(q_part_unit0(kTagActMaxI) + (size_t)kQFusedMaxPairs * 2 * kTagActMaxI <= (size_t)32 * kTagActMaxI,
+              "Q units fit the buffer");
+// LDS of a down item: act bytes [8][I] | act d [8][I/32] | act byte sums
+// [8][I/32] | quarter partials [8][64] | outputs [8][16] | state [8] |
+// routing weights [8].
+__host__ __device__ inline size_t q_fused_down_lds_bytes(int I) {
+  return (size_t)kQFusedWaves * (I + (I / 32) * 8 + 64 * 4 + 16 * 4 + 8);
+}
 
 }  // namespace mimoe

@@ -29,6 +29,7 @@
 #include "mi_moe_device.hpp"
 #include "mi_moe_internal.hpp"
 #include "mi_moe_sched.hpp"
+#include "handover.hpp"
 
 namespace mimoe {
 
@@ -101,6 +102,13 @@ __device__ __forceinline__ int block_isum(const int (&wd)[8], const int* xv, int
 // top-10 token is 10 pairs), 4 above (occupancy; 8 waves at 16 pairs measured
 // slower).
 constexpr int kQDecWideMaxPairs = 12;
+// The one-launch decode kernel serves every call of the decode path (up to
+// 64 routed pairs: one wave's ballot routes them), with the gate_up K split
+// over two workgroups up to kQFusedMaxPairs.  Same-box graph replays, config
+// 1 shape (Q8_0, H=2048, I=768, top-8): T = 1 / 2 / 4 / 8 17.05-17.07 /
+// 26.89-26.95 / 40.20-40.28 / 67.34-67.80 us, against 19.90-20.07 /
+// 28.22-28.86 / 40.31-40.54 / 67.76-68.33 us in two launches.
+constexpr int kQFusedPairsLimit = kWave;
 
 // One lane's row weights (whole 4-block layout groups, as 16-byte loads) and
 // the blocks' raw scale bits for up to NG_ groups (Q8_0: 32 VGPRs of weights
@@ -210,49 +218,84 @@ __device__ __forceinline__ QLds carve(unsigned char* smem, int Kmax) {
 }
 
 // ---------------------------------------------------------------- phase 1
-template <int QT, int ACT, int SC, int NW>
-__device__ __forceinline__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int sl, const QLds& L) {
+// TAG: the one-launch kernel's form: the intermediate blocks go to tagged
+// units (q_tag_units per pair row) instead of act_q / act_d.  KS = 2: the
+// workgroups come in pairs kh = 0, 1 per (item, slice), each over half of K
+// (the waves of the pair split K in 16 parts); kh = 0 hands its gate and up
+// sums to kh = 1 as tagged units, and kh = 1 adds them to its own
+// (half 0 + half 1) before the activation.
+template <int QT, int ACT, int SC, int NW, bool TAG = false, int KS = 1>
+__device__ __forceinline__ void q_phase1(const QArgs& a, int e, int cnt, const int* pairs, int sl, const QLds& L,
+                                         int kh = 0) {
   const SchedArgs& c = a.c;
   // wave index uniform (SGPR): the K range and the batch branches below are scalar
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int KB = c.H / 32, S = c.I / 32;
-  const int kb0 = KB * wave / NW, kb1 = KB * (wave + 1) / NW;
+  const int kb0 = KB * (kh * NW + wave) / (KS * NW), kb1 = KB * (kh * NW + wave + 1) / (KS * NW);
+  const int kbs = KB * kh / KS, kbe = KB * (kh + 1) / KS;   // this workgroup's blocks
   const size_t tile = (size_t)e * S + sl;
+  constexpr int kNG = TAG ? (kQBatchGroups<QT, NW> + 1) / 2 : kQBatchGroups<QT, NW>;
   const char* wtile = (const char*)a.w13 + tile * KB * QFmt<QT>::block_bytes;
   const uint16_t* stile = a.w13_d + tile * KB * 64;
   // the first weight batch is in flight while the activations are staged
-  QRowBatch<QT, kQBatchGroups<QT, NW>> B;
-  rows_issue<QT, kQBatchGroups<QT, NW>>(B, wtile, stile, lane, kb0 & ~3, kb1, KB);
+  QRowBatch<QT, kNG> B;
+  rows_issue<QT, kNG>(B, wtile, stile, lane, kb0 & ~3, kb1, KB);
 
   for (int cb0 = 0; cb0 < cnt; cb0 += kQTokPerPass) {
     const int cntp = min(kQTokPerPass, cnt - cb0);
-    // Stage A for the staged tokens (Int8-gemm/q8_gemm.cpp:360-377)
-    const float rkb = 1.0f / (float)KB, rk = 1.0f / (float)c.K;
-    for (int idx = tid; idx < cntp * KB; idx += NW * kWave) {
-      const int cc = div_small(idx, rkb), kb = idx - cc * KB;
+    // Stage A for the staged tokens (Int8-gemm/q8_gemm.cpp:360-377): 8 lanes
+    // per 32-value block, 4 values each, the block's amax and byte sum over
+    // the 8 lanes by shuffles (a max and an integer sum: the same d and bytes
+    // as quant_block_q8_0); every lane runs the same trip count
+    const float rk = 1.0f / (float)c.K;
+    const int p8 = lane & 7, KBw = kbe - kbs, nblk = cntp * KBw;
+    const float rkbw = 1.0f / (float)KBw;
+    for (int b0 = 0; b0 < nblk; b0 += NW * kWave / 8) {
+      const int idx = b0 + (tid >> 3);
+      const bool okb = idx < nblk;
+      const int ix = okb ? idx : 0;
+      const int cc = div_small(ix, rkbw), kb = kbs + ix - cc * KBw;
       const int pr = pairs[cb0 + cc];
       const int t = c.n < (1 << 21) ? div_small(pr, rk) : pr / c.K;   // uniform choice
-      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(c.x + (size_t)t * c.H + kb * 32);
-      float v[32];
+      const u32x2_t w = *reinterpret_cast<const u32x2_t*>(c.x + (size_t)t * c.H + kb * 32 + 4 * p8);
+      const float v[4] = {to_f32<ACT>(w.x & 0xffffu), to_f32<ACT>(w.x >> 16), to_f32<ACT>(w.y & 0xffffu),
+                          to_f32<ACT>(w.y >> 16)};
+      float amax = 0.0f;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const u32x4_t w = src[q4];
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+      for (int j = 0; j < 4; ++j) {
+        const float av = __builtin_fabsf(v[j]);
+        amax = av > amax ? av : amax;
+      }
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          v[8 * q4 + 2 * h] = to_f32<ACT>(ws[h] & 0xffffu);
-          v[8 * q4 + 2 * h + 1] = to_f32<ACT>(ws[h] >> 16);
+      for (int m = 1; m < 8; m <<= 1) {
+        const float o = __shfl_xor(amax, m, 8);
+        amax = o > amax ? o : amax;
+      }
+      float id;
+      const float d = q8_block_scale(amax, &id);
+      int qsum = 0;
+      uint32_t word = 0;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int8_t q = q8_round(v[h] * id);
+        qsum += q;
+        word |= ((uint32_t)(uint8_t)q) << (8 * h);
+      }
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1) qsum += __shfl_xor(qsum, m, 8);
+      if (okb) {
+        *reinterpret_cast<uint32_t*>(L.xq + cc * c.H + kb * 32 + 4 * p8) = word;
+        if (p8 == 0) {
+          L.xd[cc * KB + kb] = d;
+          L.xs[cc * KB + kb] = qsum;
         }
       }
-      int qs;
-      L.xd[cc * KB + kb] = quant_block_q8_0(v, L.xq + cc * c.H + kb * 32, &qs);
-      L.xs[cc * KB + kb] = qs;
     }
     __syncthreads();
     float acc[kQTokPerPass];
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
-    rows_dot<QT, SC, kQBatchGroups<QT, NW>>(B, cb0 == 0, wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.H, KB,
+    rows_dot<QT, SC, kNG>(B, cb0 == 0, wtile, stile, lane, kb0, kb1, L.xq, L.xd, L.xs, c.H, KB,
                                         cntp, acc);
 #pragma unroll
     for (int cc = 0; cc < kQTokPerPass; ++cc)
@@ -269,6 +312,32 @@ __device__ __forceinline__ void q_phase1(const QArgs& a, int e, int cnt, const i
         g = g + L.red[(w * kQTokPerPass + ccl) * 64 + r];
         u = u + L.red[(w * kQTokPerPass + ccl) * 64 + r + 32];
       }
+      if constexpr (KS == 2) {
+        // the K halves: gate and up sums of (column cc, row r) as two units
+        unsigned long long* pu = a.tact + q_part_unit0(c.I) + ((size_t)pairs[cb0 + ccl] * S + sl) * 64;
+        const unsigned tag = dispatch_tag32();
+        if (kh == 0) {
+          if (cc < cntp) {
+            store_agent(pu + r, ((unsigned long long)tag << 32) | __float_as_uint(g));
+            store_agent(pu + 32 + r, ((unsigned long long)tag << 32) | __float_as_uint(u));
+          }
+        } else {
+          unsigned long long vg = 0, vu = 0;
+          for (int polls = 0;; ++polls) {
+            vg = load_agent(pu + r);
+            vu = load_agent(pu + 32 + r);
+            if (__all((unsigned)(vg >> 32) == tag && (unsigned)(vu >> 32) == tag)) break;
+            if (polls > kSpinMax) {   // gave up: the pair's output becomes NaN
+              vg = vu = 0x7fc00000ull;
+              if (tid == 0) store_agent(a.tact + (size_t)64 * (c.I >> 1), 1ull);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          g = __uint_as_float((unsigned)vg) + g;
+          u = __uint_as_float((unsigned)vu) + u;
+        }
+      }
       const float act = silu_mul(g, u);
       // Q8_0 re-quantization of the 32-value intermediate block
       // (pack_A_q8_0, Int8-gemm/gemm_kernels.cpp:394-425)
@@ -281,7 +350,19 @@ __device__ __forceinline__ void q_phase1(const QArgs& a, int e, int cnt, const i
       float id;
       const float d = q8_block_scale(amax, &id);
       const int8_t q = q8_round(act * id);
-      if (cc < cntp) {
+      if constexpr (TAG) {
+        // lane r % 4 == 0 packs bytes r..r+3 of the block into one unit; the
+        // 8 units of a (pair, slice) are one 64-byte line, its scale one unit
+        const uint32_t b = (uint32_t)(uint8_t)q;
+        const uint32_t w = b | ((uint32_t)__shfl_down((int)b, 1, 32) << 8) |
+                           ((uint32_t)__shfl_down((int)b, 2, 32) << 16) | ((uint32_t)__shfl_down((int)b, 3, 32) << 24);
+        if (kh == KS - 1 && cc < cntp) {
+          unsigned long long* row = a.tact + (size_t)pairs[cb0 + cc] * q_tag_units(c.I);
+          const unsigned long long tg = (unsigned long long)dispatch_tag32() << 32;
+          if ((r & 3) == 0) store_agent(row + 8 * sl + (r >> 2), tg | w);
+          if (r == 0) store_agent(row + (c.I >> 2) + sl, tg | __float_as_uint(d));
+        }
+      } else if (cc < cntp) {
         const size_t row = (size_t)pairs[cb0 + cc];
         a.act_q[row * c.I + 32 * sl + r] = q;
         if (r == 0) a.act_d[row * S + sl] = d;
@@ -507,6 +588,160 @@ __global__ __launch_bounds__(kDownMaxK * 64) void q_down_token_kernel(const int3
   }
 }
 
+// ---------------------------------------------------------------- one launch
+// The Q8_0 / Q4_0 decode layer in one launch for the smallest calls (up to
+// kQDecWideMaxPairs routed pairs, top-k <= 8), 8-wave workgroups:
+//  * [0, n1): gate_up items (pair i, 32-row slice sl), the phase-1 routine
+//    above (ballot routing over all ids; the item serves its expert iff i is
+//    the expert's first pair), its intermediate Q8_0 blocks written as tagged
+//    units (handover.hpp);
+//  * [n1, n1 + T * H/16): down items (token t, 16-row tile jt), the
+//    token-major down routine with the combine (Int8-gemm/q8_gemm.cpp:
+//    593-641); wave k < K reads the intermediate row of pair t*K+k from the
+//    units.
+// A down wave issues its weight loads first, polls the row's scale units (one
+// per slice, coherent loads), then reads the whole row, checks every tag and
+// unpacks it into LDS, polling again if a unit is not yet there.  The waits
+// end: workgroups start in index order, so the gate_up items a down item reads
+// from are resident or finished when it starts, and they wait on nothing.
+// The wait is still bounded (kSpinMax polls); a wave that gives up makes its
+// token's tile NaN and sets the buffer's timeout unit.
+template <int QT, int ACT, int SC>
+__device__ __forceinline__ void q_fused_down(const QArgs& a, int t, int jt, unsigned char* smem) {
+  const SchedArgs& c = a.c;
+  const int K = c.K, I = c.I, H = c.H, KB2 = I / 32, HB = H / 64;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int q = lane >> 4, r = lane & 15;
+  int8_t* xq = reinterpret_cast<int8_t*>(smem);
+  float* xd = reinterpret_cast<float*>(smem + (size_t)kQFusedWaves * I);
+  int* xs = reinterpret_cast<int*>(xd + kQFusedWaves * KB2);
+  float* part = reinterpret_cast<float*>(xs + kQFusedWaves * KB2);
+  float* outs = part + kQFusedWaves * 64;
+  int* state = reinterpret_cast<int*>(outs + kQFusedWaves * 16);   // 0 invalid id, 1 valid, 2 wait gave up
+  float* tws = reinterpret_cast<float*>(state + kQFusedWaves);
+  // the combine's routing weights, copied into LDS now (covered by the
+  // barrier's wait below; no registers held)
+  if (tid < K) __builtin_amdgcn_global_load_lds(c.tw + t * K + tid, tws, 4, 0, 0);
+  if (wave < K) {   // uniform: wave k takes routed expert k of token t
+    const int i = t * K + wave;
+    const int e = __builtin_amdgcn_readfirstlane(c.ids[i]);
+    // an invalid id computes on expert 0 and its output is ignored
+    const bool ok = (unsigned)e < (unsigned)c.E;
+    const int row = (jt & 3) * 16 + r;   // this lane's row in the 64-row layout tile
+    const size_t tile = (size_t)(ok ? e : 0) * HB + (jt >> 2);
+    const char* wtile = (const char*)a.w2 + tile * KB2 * QFmt<QT>::block_bytes;
+    const uint16_t* stile = a.w2_d + tile * KB2 * 64;
+    const int kb0 = KB2 * q / 4, kb1 = KB2 * (q + 1) / 4;
+    QRowBatch<QT, 2> B;   // both groups a quarter can touch, in flight during the wait
+    rows_issue<QT, 2>(B, wtile, stile, row, kb0 & ~3, kb1, KB2);
+    int st = ok ? 1 : 0;
+    if (ok) {
+      const unsigned tag = dispatch_tag32();
+      const unsigned long long* units = a.tact + (size_t)i * q_tag_units(I);
+      const int nq = I >> 2, nunits = q_tag_units(I);
+      unsigned* dq = reinterpret_cast<unsigned*>(xq + (size_t)wave * I);
+      float* dd = xd + wave * KB2;
+      auto read_row = [&]() {
+        bool whole = true;
+        for (int u0 = 0; u0 < nunits; u0 += 64 * 4) {
+          unsigned long long v[4];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const int u = u0 + 64 * b + lane;
+            v[b] = u < nunits ? load_agent(units + u) : ((unsigned long long)tag << 32);
+          }
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const int u = u0 + 64 * b + lane;
+            whole = whole && (unsigned)(v[b] >> 32) == tag;
+            if (u < nq) dq[u] = (unsigned)v[b];
+            else if (u < nunits) dd[u - nq] = __uint_as_float((unsigned)v[b]);
+          }
+        }
+        return __all(whole);
+      };
+      for (int polls = 0;;) {
+        bool ready = true;
+        for (int j = lane; j < KB2; j += 64) ready = ready && (unsigned)(load_agent(units + nq + j) >> 32) == tag;
+        if (__all(ready) && read_row()) break;
+        if (++polls > kSpinMax) {
+          st = 2;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (st == 2 && lane == 0) store_agent(a.tact + (size_t)64 * (I >> 1), 1ull);
+      if constexpr (QT == 1) {   // Q4_0: the blocks' byte sums (this wave's own LDS row: in order)
+        for (int kb = lane; kb < KB2; kb += 64) {
+          const int* wq = reinterpret_cast<const int*>(xq + (size_t)wave * I + 32 * kb);
+          int sum = 0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) sum = __builtin_amdgcn_sdot4(wq[j], 0x01010101, sum, false);
+          xs[wave * KB2 + kb] = sum;
+        }
+      }
+    }
+    if (lane == 0) state[wave] = st;
+    float acc[kQTokPerPass];
+#pragma unroll
+    for (int cc = 0; cc < kQTokPerPass; ++cc) acc[cc] = 0.0f;
+    rows_dot<QT, SC, 2>(B, true, wtile, stile, row, kb0, kb1, xq + (size_t)wave * I, xd + wave * KB2,
+                        xs + wave * KB2, I, KB2, 1, acc);
+    part[wave * 64 + lane] = acc[0];
+    if (lane < 16) {   // the quarters in order (this wave's own partials)
+      const float* pw = part + wave * 64;
+      outs[wave * 16 + lane] = ((pw[lane] + pw[16 + lane]) + pw[32 + lane]) + pw[48 + lane];
+    }
+  }
+  __syncthreads();
+  if (tid < 16) {
+    float y = 0.0f;
+    bool gave_up = false;
+#pragma unroll
+    for (int k = 0; k < kQFusedWaves; ++k) {
+      const int sk = k < K ? state[k] : 0;
+      if (sk) {
+        gave_up |= sk == 2;
+        const float prod = tws[k] * outs[16 * k + tid];
+        y = y + prod;
+      }
+    }
+    c.y[(size_t)t * H + 16 * jt + tid] = gave_up ? (uint16_t)0x7fc0u : from_f32<ACT>(y);   // NaN in bf16 and fp16
+  }
+}
+
+// The leading arguments repeat fields of a0 (preloaded into SGPRs; see
+// q_phase1_kernel).
+template <int QT, int ACT, int SC, int KS>
+__global__ __launch_bounds__(kQFusedWaves * kWave) __attribute__((amdgpu_waves_per_eu(4)))
+void q_decode_kernel(const int32_t* ids, const uint16_t* x, const void* w13, const uint16_t* w13_d, const void* w2,
+                     const uint16_t* w2_d, int n1, int I, QArgs a0) {
+  QArgs a = a0;
+  a.c.ids = ids;
+  a.c.x = x;
+  a.w13 = w13;
+  a.w13_d = w13_d;
+  a.w2 = w2;
+  a.w2_d = w2_d;
+  a.c.I = I;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int b = blockIdx.x, S1 = I >> 5;
+  if (b < n1) {   // uniform: gate_up item (pair, slice)
+    const QLds L = carve(smem, a.c.H);
+    const int item = b / (KS * S1), rem = b - item * KS * S1, sl = rem / KS;
+    const int tid = threadIdx.x;
+    const BallotCols cl = ballot_cols(a.c, item, tid & 63);   // every wave: same result
+    if (!cl.serve) return;   // uniform
+    if (tid < kWave) L.route[tid] = cl.colpair;
+    __syncthreads();
+    q_phase1<QT, ACT, SC, kQFusedWaves, true, KS>(a, __builtin_amdgcn_readfirstlane(cl.e),
+                                                 __builtin_amdgcn_readfirstlane(cl.cnt), L.route, sl, L, rem - sl * KS);
+  } else {
+    const int nt = a.c.H >> 4, d = b - n1, t = d / nt;
+    q_fused_down<QT, ACT, SC>(a, t, d - t * nt, smem);
+  }
+}
+
 // Dynamic LDS beyond kMaxLds needs the kernel's opt-in.
 template <class Kern>
 static void lds_opt_in(Kern k, size_t lds) {
@@ -557,6 +792,40 @@ hipError_t launch_qint(const QArgs& a, int qt, int act, int sc, int grid1, int g
   }
   if (act == 1) return sc == 1 ? launch_q_t<1, 1, 1>(a, grid1, grid2, td, st) : launch_q_t<1, 1, 0>(a, grid1, grid2, td, st);
   return sc == 1 ? launch_q_t<1, 0, 1>(a, grid1, grid2, td, st) : launch_q_t<1, 0, 0>(a, grid1, grid2, td, st);
+}
+
+template <int QT, int ACT, int SC, int KS>
+static hipError_t launch_q_fused_ks(const QArgs& a, size_t lds, hipStream_t st) {
+  lds_opt_in(q_decode_kernel<QT, ACT, SC, KS>, lds);
+  const int n1 = a.c.n * (a.c.I / 32) * KS, n2 = a.c.T * (a.c.H / 16);
+  hipLaunchKernelGGL((q_decode_kernel<QT, ACT, SC, KS>), dim3(n1 + n2), dim3(kQFusedWaves * kWave), lds, st,
+                     a.c.ids, a.c.x, a.w13, a.w13_d, a.w2, a.w2_d, n1, a.c.I, a);
+  return hipGetLastError();
+}
+// K split over two workgroups per gate_up item up to kQFusedMaxPairs routed pairs
+template <int QT, int ACT, int SC>
+static hipError_t launch_q_fused_t(const QArgs& a, size_t lds, hipStream_t st) {
+  return a.c.n <= kQFusedMaxPairs ? launch_q_fused_ks<QT, ACT, SC, 2>(a, lds, st)
+                                  : launch_q_fused_ks<QT, ACT, SC, 1>(a, lds, st);
+}
+
+// LDS of the one-launch kernel, or 0 if it does not serve the call.
+size_t q_fused_lds(int n, int K, int H, int I, int E) {
+  if (n > kQFusedPairsLimit || K > kQFusedWaves || I > kTagActMaxI || H % 64 != 0) return 0;
+  const size_t gate_up = q_stage_bytes(H) + q_route_lds_bytes(E, n), down = q_fused_down_lds_bytes(I);
+  const size_t lds = gate_up > down ? gate_up : down;
+  return lds <= device_max_lds() ? lds : 0;
+}
+
+hipError_t launch_q_fused(const QArgs& a, int qt, int act, int sc, hipStream_t st) {
+  const size_t lds = q_fused_lds(a.c.n, a.c.K, a.c.H, a.c.I, a.c.E);
+  if (!lds || !a.tact) return hipErrorInvalidValue;
+  if (qt == 0) {
+    if (act == 1) return sc == 1 ? launch_q_fused_t<0, 1, 1>(a, lds, st) : launch_q_fused_t<0, 1, 0>(a, lds, st);
+    return sc == 1 ? launch_q_fused_t<0, 0, 1>(a, lds, st) : launch_q_fused_t<0, 0, 0>(a, lds, st);
+  }
+  if (act == 1) return sc == 1 ? launch_q_fused_t<1, 1, 1>(a, lds, st) : launch_q_fused_t<1, 1, 0>(a, lds, st);
+  return sc == 1 ? launch_q_fused_t<1, 0, 1>(a, lds, st) : launch_q_fused_t<1, 0, 0>(a, lds, st);
 }
 
 // ---------------------------------------------------------------- grouped GEMMs (int8 MFMA)

@@ -38,11 +38,11 @@
 #include "mi_moe_internal.hpp"
 #include "mi_moe_sched.hpp"
 #include "w4a16_device.hpp"
+#include "handover.hpp"
 
 namespace mimoe {
 
 constexpr int kFusedWaves = kW4FusedWaves;
-constexpr int kSpinMax = 1 << 18;   // polls of one wait (each at least one memory round trip)
 constexpr int kUnitBatch = 6;       // act units per lane loaded together by a down wave (I = 768: all)
 // From this many gate_up items per resident-workgroup slot on, the gate_up
 // workgroups fill the slots and each takes several items (pipelined); below
@@ -50,27 +50,6 @@ constexpr int kUnitBatch = 6;       // act units per lane loaded together by a d
 // (bs 8) the pipelined form is 0.7 us faster per layer, at 1.5 (bs 4) 0.2 us
 // slower, and with half or three quarters of the slots slower at every size.
 constexpr long kPipelinedItemsPerSlot = 2;
-
-__device__ __forceinline__ unsigned long long load_agent(const unsigned long long* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T>
-__device__ __forceinline__ void store_agent(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The AQL packet index of this dispatch (llvm.amdgcn.dispatch.id: SGPRs the
-// command processor fills at launch).
-extern "C" __device__ unsigned long long mimoe_llvm_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
-
-// 32-bit tag of this dispatch: the packet index plus a multiple of the
-// queue's address (odd, so never 0, the value of a cleared unit).  A unit
-// written by an earlier dispatch on the same queue matches only after 2^31
-// more dispatches.
-__device__ __forceinline__ unsigned dispatch_tag32() {
-  const unsigned long long q = (unsigned long long)(uintptr_t)__builtin_amdgcn_queue_ptr();
-  return ((unsigned)mimoe_llvm_dispatch_id() * 2u + (unsigned)(q >> 12) * 0x9E3779B2u) | 1u;
-}
 
 // ---------------------------------------------------------------- gate_up role
 // One item per workgroup (the grid holds every item): item (pair, block js of

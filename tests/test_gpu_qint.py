@@ -122,6 +122,71 @@ def test_forward_dtypes_and_invalid_ids(cuda, qt):
 
 
 @pytest.mark.parametrize("qt", [0, 1])
+def test_one_launch_small_calls(cuda, qt):
+    """The one-launch decode kernel at the sizes whose gate_up K is split over
+    two workgroups (up to 12 routed pairs): one token with a duplicated
+    expert and two out-of-range ids, one token with no valid id (zeros), one
+    top-1 token and 12 top-1 tokens; every call against the oracle, and
+    repeated calls (a new dispatch tag each) bit-identical."""
+    E, H, I = 16, 256, 128
+    w = _weights(qt, E, H, I, seed=70 + qt)
+    h = _handle(qt, E, H, I, w, True, cuda)
+    cases = []
+    ids = torch.tensor([[3, 3, -1, 5, E, 7, 3, 0]], dtype=torch.int32)
+    cases.append(ids)
+    cases.append(torch.full((1, 8), E + 1, dtype=torch.int32))
+    cases.append(torch.tensor([[9]], dtype=torch.int32))
+    cases.append(topk_routing(12, E, 1, seed=71)[0])
+    for i, ids in enumerate(cases):
+        T, K = ids.shape
+        tw = torch.softmax(torch.randn(T, K, generator=torch.Generator().manual_seed(i)), dim=-1)
+        x = torch.randn(T, H, generator=torch.Generator().manual_seed(80 + i)).to(torch.bfloat16)
+        y = _run(h, x, ids, tw, cuda)
+        if bool((ids >= E).all() | (ids < 0).all()):
+            assert torch.all(y == 0)
+        assert max_rel_err(y, _oracle(qt, x, ids, tw, w, E, I)) <= TOL
+        for _ in range(2):
+            assert torch.equal(_run(h, x, ids, tw, cuda), y)
+
+
+@pytest.mark.parametrize("qt", [0, 1])
+def test_one_launch_graph_replay(cuda, qt):
+    """Calls of 8 and 40 routed pairs (both forms of the one-launch kernel)
+    captured in one HIP graph: every replay, with eager calls on the same
+    handle between replays, equals the eager results bit for bit."""
+    E, H, I = 16, 256, 128
+    w = _weights(qt, E, H, I, seed=90 + qt)
+    h = _handle(qt, E, H, I, w, True, cuda)
+    cases = []
+    for T, K, s in ((1, 8, 91), (5, 8, 92)):
+        ids, tw = topk_routing(T, E, K, seed=s)
+        x = torch.randn(T, H, generator=torch.Generator().manual_seed(s)).to(torch.bfloat16)
+        cases.append((x.to(cuda), ids.to(cuda), tw.to(cuda)))
+    outs = [torch.empty(x.shape[0], H, dtype=torch.bfloat16, device=cuda) for x, _, _ in cases]
+    for (x, ids, tw), o in zip(cases, outs):
+        torch.ops.nanovllm.moe_forward_out(x, ids, tw, h, o)
+    torch.cuda.synchronize()
+    eager = [o.cpu() for o in outs]
+    for (x, ids, tw), e in zip(cases, eager):
+        assert max_rel_err(e, _oracle(qt, x.cpu(), ids.cpu(), tw.cpu(), w, E, I)) <= TOL
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for (x, ids, tw), o in zip(cases, outs):
+            torch.ops.nanovllm.moe_forward_out(x, ids, tw, h, o)
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o.cpu(), e), f"replay {rep}"
+        x, ids, tw = cases[rep % 2]
+        y = torch.ops.nanovllm.moe_forward(x, ids, tw, h)
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu(), eager[rep % 2])
+
+
+@pytest.mark.parametrize("qt", [0, 1])
 def test_gemm_path_tiles_and_invalid_ids(cuda, qt):
     """Grouped-GEMM path: an expert with 64 + 64 + 2 rows (two full row tiles
     and a ragged one), one with 65, ids outside [0, E), fp16 activations and
