@@ -29,7 +29,7 @@ constexpr size_t kXAllBytes = 16384; // hidden rows phase 1 copies whole on the 
 constexpr int kDecodeCols = 4;       // phase-1 pass width on the decode path
 
 // kernels / launchers defined in the other translation units
-hipError_t launch_route_global(const int32_t*, int, int, int, const RouteGlobal&, hipStream_t, int);
+hipError_t launch_route_global(const int32_t*, int, int, int, const RouteGlobal&, hipStream_t, int, int);
 hipError_t launch_combine(const float*, const float*, const int32_t*, void*, int, int, int, int, int,
                           hipStream_t);
 hipError_t launch_awq_repack_all(const int32_t*, const int32_t*, const uint16_t*, const int32_t*,
@@ -375,7 +375,7 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
     return MI_MOE_OK;
   }
   // sorted path: routing with row tiles, the two grouped GEMMs, the combine
-  HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
+  HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0, 1));
   HIPCHK(launch_w4a16_gemm(a, act, (int)gemm_tiles_max(n, (int)h->E), st, mid));
   if (!noalloc) h->mid_recorded = mid != nullptr;
   HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
@@ -438,7 +438,7 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
     HIPCHK(launch_q_fused(a, h->quant, act, h->scale_dtype, st));
     return MI_MOE_OK;
   }
-  if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
+  if (a.c.route_global) HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0, 0));
   const int64_t umax = n < h->E ? n : h->E;
   const int64_t grid1 = (n <= kQBallotMaxPairs ? n : umax) * (h->I / 32), grid2 = umax * (h->H / 64);
   HIPCHK(launch_qint(a, h->quant, act, h->scale_dtype, (int)grid1, (int)grid2, token_down, st));
@@ -868,7 +868,7 @@ MI_API int mi_moe_route(const int32_t* ids, int64_t T, int64_t K, int64_t E, int
   unsigned char* base = (unsigned char*)buf.p;
   RouteGlobal rg{counts, starts, (int32_t*)base, token_map, scatter, (int32_t*)(base + a_bytes), nullptr, nullptr,
                  (int32_t*)(base + a_bytes + 256)};
-  HIPCHK(launch_route_global(ids, (int)(T * K), (int)K, (int)E, rg, st, 1));
+  HIPCHK(launch_route_global(ids, (int)(T * K), (int)K, (int)E, rg, st, 1, 0));
   HIPCHK(hipStreamSynchronize(st));
   return MI_MOE_OK;
 }

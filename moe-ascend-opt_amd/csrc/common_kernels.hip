@@ -13,8 +13,8 @@ constexpr int kRouteWaves = kRouteThreads / kWave;
 
 // Routing: the stable counting sort of preprocess_moe_routing
 // (Int8-gemm/moe_common.cpp:146-216) for any number of (t,k) pairs, plus, with
-// tiles_out, the row tiles of the grouped GEMMs: per active expert in
-// ascending order, its sorted rows in chunks of kGemmRows.
+// tiles_out, the row tiles of the grouped GEMMs: each active expert's sorted
+// rows in chunks of kGemmRows, listed heaviest first (route_finish).
 //   n <= kRouteMultiMin: one workgroup (route_global_kernel);
 //   above: route_count_kernel (a histogram per chunk of kRouteChunk ids),
 //   route_scan_kernel (totals, starts, tiles, and per-chunk base offsets),
@@ -33,29 +33,50 @@ __device__ __forceinline__ uint64_t route_match(int e, bool valid, int nbits) {
   return m;
 }
 
+// Row-tile classes by MFMA sub-tiles: class 0 holds 49-64 rows (4 sub-tiles
+// of 16), ..., class 3 holds 1-16 rows.  A W4A16 grouped-GEMM workgroup's time
+// grows with its tile's sub-tiles, so with lpt the tile list is ordered
+// heaviest class first (longest-processing-time first): the heavy tiles start
+// in the first round of workgroups instead of forming the tail of the launch
+// (Zipf-routed T = 512, same box: 138.2-138.7 -> 129.9-130.1 us per layer).
+// The int8 GEMMs keep each expert's tiles together (lpt = 0): there the
+// workgroups of one weight slice and consecutive tiles share an XCD and read
+// the slice through its L2 (with lpt, Q4_0 T = 4096 was 2.7% slower).
+constexpr int kTileClasses = kGemmRows / 16;
+static_assert(kTileClasses == 4, "four 16-row sub-tile classes");
+__device__ __forceinline__ int tile_class(int rows) { return kTileClasses - ((rows + 15) >> 4); }
+
 // Wave 0: per-expert totals counts[E] (LDS) -> counts_out, starts_out, the
-// active list, U and the row tiles; counts[] becomes the starts.
+// active list, U and the row tiles; counts[] becomes the starts.  Tiles are
+// listed by class (lpt: heaviest first; otherwise one class), within a class
+// by expert, then by row.
 __device__ void route_finish(int* counts, int E, int lane, int32_t* counts_out, int32_t* starts_out,
-                             int32_t* active_out, int32_t* U_out, int32_t* tiles_out, int32_t* ntiles_out) {
+                             int32_t* active_out, int32_t* U_out, int32_t* tiles_out, int32_t* ntiles_out,
+                             int lpt) {
   const int per = (E + kWave - 1) / kWave;
   const int base = lane * per;
-  int s = 0, a = 0, tl = 0;   // rows, active experts and row tiles of this lane's experts
+  // rows, active experts and row tiles per class of this lane's experts
+  int s = 0, a = 0, t0 = 0, t1 = 0, t2 = 0, t3 = 0;
   for (int i = 0; i < per; ++i) {
     const int e = base + i;
     if (e < E) {
-      const int c = counts[e];
-      s += c; a += (c > 0); tl += (c + kGemmRows - 1) / kGemmRows;
+      const int c = counts[e], rem = c % kGemmRows, k = lpt ? tile_class(rem) : 0;
+      s += c; a += (c > 0); t0 += c / kGemmRows;
+      if (rem) { t0 += k == 0; t1 += k == 1; t2 += k == 2; t3 += k == 3; }
     }
   }
-  int sinc = s, ainc = a, tinc = tl;
+  int sinc = s, ainc = a, i0 = t0, i1 = t1, i2 = t2, i3 = t3;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
-    const int v = __shfl_up(sinc, off);
-    const int w = __shfl_up(ainc, off);
-    const int u = __shfl_up(tinc, off);
-    if (lane >= off) { sinc += v; ainc += w; tinc += u; }
+    const int v = __shfl_up(sinc, off), w = __shfl_up(ainc, off);
+    const int u0 = __shfl_up(i0, off), u1 = __shfl_up(i1, off), u2 = __shfl_up(i2, off), u3 = __shfl_up(i3, off);
+    if (lane >= off) { sinc += v; ainc += w; i0 += u0; i1 += u1; i2 += u2; i3 += u3; }
   }
-  int sx = sinc - s, ax = ainc - a, tx = tinc - tl;
+  const int n0 = __shfl(i0, kWave - 1), n1 = __shfl(i1, kWave - 1), n2 = __shfl(i2, kWave - 1),
+            n3 = __shfl(i3, kWave - 1);
+  // next free position of each class for this lane's tiles
+  int x0 = i0 - t0, x1 = n0 + i1 - t1, x2 = n0 + n1 + i2 - t2, x3 = n0 + n1 + n2 + i3 - t3;
+  int sx = sinc - s, ax = ainc - a;
   for (int i = 0; i < per; ++i) {
     const int e = base + i;
     if (e < E) {
@@ -65,10 +86,12 @@ __device__ void route_finish(int* counts, int E, int lane, int32_t* counts_out, 
       counts[e] = sx;
       if (c > 0) active_out[ax++] = e;
       if (tiles_out)
-        for (int r0 = 0; r0 < c; r0 += kGemmRows, ++tx) {
+        for (int r0 = 0; r0 < c; r0 += kGemmRows) {
+          const int rows = min(kGemmRows, c - r0), k = lpt ? tile_class(rows) : 0;
+          const int tx = k == 0 ? x0++ : k == 1 ? x1++ : k == 2 ? x2++ : x3++;
           tiles_out[4 * tx + 0] = e;
           tiles_out[4 * tx + 1] = sx + r0;
-          tiles_out[4 * tx + 2] = min(kGemmRows, c - r0);
+          tiles_out[4 * tx + 2] = rows;
           tiles_out[4 * tx + 3] = 0;
         }
       sx += c;
@@ -77,7 +100,7 @@ __device__ void route_finish(int* counts, int E, int lane, int32_t* counts_out, 
   if (lane == kWave - 1) {
     starts_out[E] = sinc;
     *U_out = ainc;
-    if (ntiles_out) *ntiles_out = tinc;
+    if (ntiles_out) *ntiles_out = n0 + n1 + n2 + n3;
   }
 }
 
@@ -159,7 +182,7 @@ static_assert(kRouteMultiMin <= kRouteThreads * kRouteSegIter, "a wave segment f
 __device__ __forceinline__ void route_global_body(const int32_t* __restrict__ ids, int n, int K, int E,
                                                   int32_t* counts_out, int32_t* starts_out, int32_t* active_out,
                                                   int32_t* tok, int32_t* scat, int32_t* U_out, int tok_div,
-                                                  int32_t* tiles_out, int32_t* ntiles_out, int* lds) {
+                                                  int32_t* tiles_out, int32_t* ntiles_out, int* lds, int lpt) {
   int* counts = lds;            // [E]: totals, then the starts
   int* cw = lds + E;            // [kRouteWaves][E]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -182,7 +205,8 @@ __device__ __forceinline__ void route_global_body(const int32_t* __restrict__ id
     counts[e] = run;
   }
   __syncthreads();
-  if (tid < kWave) route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out);
+  if (tid < kWave)
+    route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out, lpt);
   __syncthreads();
   route_seg_rank(lo, hi, K, counts, lane, mine, seg, tok, scat, tok_div);
 }
@@ -190,10 +214,10 @@ __device__ __forceinline__ void route_global_body(const int32_t* __restrict__ id
 __global__ __launch_bounds__(kRouteThreads) void route_global_kernel(
     const int32_t* __restrict__ ids, int n, int K, int E, int32_t* counts_out,
     int32_t* starts_out, int32_t* active_out, int32_t* tok, int32_t* scat, int32_t* U_out,
-    int tok_div, int32_t* tiles_out, int32_t* ntiles_out) {
+    int tok_div, int32_t* tiles_out, int32_t* ntiles_out, int lpt) {
   extern __shared__ int lds[];
   route_global_body(ids, n, K, E, counts_out, starts_out, active_out, tok, scat, U_out, tok_div, tiles_out,
-                    ntiles_out, lds);
+                    ntiles_out, lds, lpt);
 }
 
 // Multi-workgroup routing, step 1: the expert histogram of one chunk of ids.
@@ -226,7 +250,8 @@ __global__ __launch_bounds__(kRouteCountThreads) void route_count_kernel(const i
 __global__ __launch_bounds__(kRouteThreads) void route_scan_kernel(int32_t* chunk_counts, int C, int E,
                                                                    int32_t* counts_out, int32_t* starts_out,
                                                                    int32_t* active_out, int32_t* U_out,
-                                                                   int32_t* tiles_out, int32_t* ntiles_out) {
+                                                                   int32_t* tiles_out, int32_t* ntiles_out,
+                                                                   int lpt) {
   extern __shared__ int counts[];   // [E]
   const int tid = threadIdx.x, lane = tid & 63;
   // chunk counts in batches of 8 loads issued together (one round trip per batch)
@@ -243,7 +268,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_scan_kernel(int32_t* chun
     counts[e] = s;
   }
   __syncthreads();
-  if (tid < kWave) route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out);
+  if (tid < kWave)
+    route_finish(counts, E, lane, counts_out, starts_out, active_out, U_out, tiles_out, ntiles_out, lpt);
   __syncthreads();
   for (int e = tid; e < E; e += kRouteThreads) {
     int run = counts[e];
@@ -291,8 +317,9 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(const int3
 }
 
 // tok_div = 0: tok[] holds pair indices t*K+k (fused kernels); 1: token ids.
+// lpt: row tiles heaviest first (route_finish).
 hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const RouteGlobal& rg,
-                               hipStream_t st, int tok_div) {
+                               hipStream_t st, int tok_div, int lpt) {
   if (n > kRouteMultiMin) {
     if (!rg.chunk) return hipErrorInvalidValue;   // the chunked routing needs its scratch
     const int C = (n + kRouteChunk - 1) / kRouteChunk;
@@ -301,7 +328,7 @@ hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const Ro
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kRouteThreads), (size_t)E * sizeof(int), st, rg.chunk,
-                       C, E, rg.counts, rg.starts, rg.active, rg.U, rg.tiles, rg.ntiles);
+                       C, E, rg.counts, rg.starts, rg.active, rg.U, rg.tiles, rg.ntiles, lpt);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(route_scatter_kernel, dim3(C), dim3(kRouteThreads), (size_t)kRouteWaves * E * sizeof(int),
@@ -311,7 +338,7 @@ hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const Ro
   const size_t lds = (size_t)(kRouteWaves + 1) * E * sizeof(int);
   hipLaunchKernelGGL(route_global_kernel, dim3(1), dim3(kRouteThreads), lds, st, ids, n, K, E,
                      rg.counts, rg.starts, rg.active, rg.tok, rg.scat, rg.U, tok_div, rg.tiles,
-                     rg.ntiles);
+                     rg.ntiles, lpt);
   return hipGetLastError();
 }
 
@@ -418,7 +445,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_quant_kernel(
   extern __shared__ int lds[];
   if (blockIdx.x == 0) {   // uniform
     route_global_body(ids, n, K, E, counts_out, starts_out, active_out, tok, scat, U_out, tok_div, tiles_out,
-                      ntiles_out, lds);
+                      ntiles_out, lds, 0);
     return;
   }
   quant_act_blocks<ACT>(x, (int64_t)(blockIdx.x - 1) * kRouteThreads + threadIdx.x,
@@ -450,7 +477,7 @@ hipError_t launch_quant_route(const void* x, int act, int64_t T, int64_t H, int8
   if (n > kRouteMultiMin || nblk == 0) {
     hipError_t err = launch_quant_act(x, act, T, H, qs, d, st);
     if (err != hipSuccess) return err;
-    return launch_route_global(ids, n, K, E, rg, st, tok_div);
+    return launch_route_global(ids, n, K, E, rg, st, tok_div, 0);
   }
   const int64_t gq = std::min<int64_t>((nblk + kRouteThreads - 1) / kRouteThreads, 1024);
   const size_t lds = (size_t)(kRouteWaves + 1) * E * sizeof(int);
