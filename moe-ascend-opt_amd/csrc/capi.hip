@@ -31,7 +31,7 @@ constexpr int kDecodeCols = 4;       // phase-1 pass width on the decode path
 // kernels / launchers defined in the other translation units
 hipError_t launch_route_global(const int32_t*, int, int, int, const RouteGlobal&, hipStream_t, int, int);
 hipError_t launch_combine(const float*, const float*, const int32_t*, void*, int, int, int, int, int,
-                          hipStream_t);
+                          hipStream_t, bool);
 hipError_t launch_awq_repack_all(const int32_t*, const int32_t*, const uint16_t*, const int32_t*,
                                  const int32_t*, const uint16_t*, void*, unsigned char*, void*,
                                  unsigned char*, int, int, int, hipStream_t);
@@ -378,7 +378,7 @@ int forward_w4a16(mi_moe_handle* h, const void* x, void* y, const float* tw, con
   HIPCHK(launch_route_global(ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0, 1));
   HIPCHK(launch_w4a16_gemm(a, act, (int)gemm_tiles_max(n, (int)h->E), st, mid));
   if (!noalloc) h->mid_recorded = mid != nullptr;
-  HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
+  HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st, true));
   return MI_MOE_OK;
 }
 
@@ -430,7 +430,7 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
     a.xd = w.xd;
     HIPCHK(launch_quant_route(x, act, T, h->H, w.xq, w.xd, ids, (int)n, (int)K, (int)h->E, a.c.rg, st, 0));
     HIPCHK(launch_qint_gemm(a, h->quant, h->scale_dtype, (int)gemm_tiles_max(n, (int)h->E), st));
-    HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
+    HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st, false));
     return MI_MOE_OK;
   }
   // the smallest calls in one launch (gate_up hands the intermediate to down inside it)
@@ -442,7 +442,7 @@ int forward_q(mi_moe_handle* h, const void* x, void* y, const float* tw, const i
   const int64_t umax = n < h->E ? n : h->E;
   const int64_t grid1 = (n <= kQBallotMaxPairs ? n : umax) * (h->I / 32), grid2 = umax * (h->H / 64);
   HIPCHK(launch_qint(a, h->quant, act, h->scale_dtype, (int)grid1, (int)grid2, token_down, st));
-  if (!token_down) HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st));
+  if (!token_down) HIPCHK(launch_combine(a.c.eout, tw, ids, y, (int)T, (int)K, (int)h->E, (int)h->H, act, st, false));
   return MI_MOE_OK;
 }
 

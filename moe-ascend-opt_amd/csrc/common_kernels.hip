@@ -344,17 +344,22 @@ hipError_t launch_route_global(const int32_t* ids, int n, int K, int E, const Ro
 
 // Stage C1 + C2 of Int8-gemm/q8_gemm.cpp:593-641 (tp = 1): y[t,h] =
 // cast(sum_k w[t,k] * eout[t*K+k, h]) over the valid ids in k order; a token
-// without a valid id gets 0.  One thread per (t, 4 consecutive h).
-template <int ACT>
+// without a valid id gets 0.  E16: the rows hold activation-dtype values (the
+// W4A16 sorted path; one thread per (t, 8 consecutive h)), else fp32 (one
+// thread per (t, 4 consecutive h)): 16-byte row loads either way.
+template <int ACT, bool E16>
 __global__ void combine_kernel(const float* __restrict__ eout, const float* __restrict__ tw,
                                const int32_t* __restrict__ ids, uint16_t* __restrict__ y, int T,
                                int K, int E, int H) {
-  const int H4 = H >> 2;
-  const int64_t total = (int64_t)T * H4;
+  constexpr int V = E16 ? 8 : 4;
+  const int HV = H / V;
+  const int64_t total = (int64_t)T * HV;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
-    const int t = (int)(idx / H4), h = (int)(idx - (int64_t)t * H4) * 4;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int t = (int)(idx / HV), h = (int)(idx - (int64_t)t * HV) * V;
+    float acc[V];
+#pragma unroll
+    for (int q = 0; q < V; ++q) acc[q] = 0.0f;
     // 8 pairs at a time: their ids, weights and rows are loaded together (the
     // row of a pair with an invalid id is read but not used), then added in k
     // order
@@ -362,43 +367,58 @@ __global__ void combine_kernel(const float* __restrict__ eout, const float* __re
     for (int k0 = 0; k0 < K; k0 += kB) {
       int ev[kB];
       float wv[kB];
-      f32x4_t rv[kB];
+      u32x4_t rv[kB];
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
         const int i = t * K + min(k0 + j, K - 1);
         ev[j] = k0 + j < K ? ids[i] : -1;
         wv[j] = tw[i];
-        rv[j] = *reinterpret_cast<const f32x4_t*>(eout + (size_t)i * H + h);
+        const size_t off = (size_t)i * H + h;
+        rv[j] = E16 ? *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(eout) + off)
+                    : *reinterpret_cast<const u32x4_t*>(eout + off);
       }
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
         if ((unsigned)ev[j] >= (unsigned)E) continue;
-        const float vv[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+        const uint32_t u[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+        float vv[V];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+          if constexpr (E16) {
+            vv[2 * q] = to_f32<ACT>(u[q]);
+            vv[2 * q + 1] = to_f32<ACT>(u[q] >> 16);
+          } else {
+            vv[q] = __uint_as_float(u[q]);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < V; ++q) {
           const float prod = wv[j] * vv[q];
           acc[q] = acc[q] + prod;
         }
       }
     }
-    const uint32_t lo = from_f32<ACT>(acc[0]) | ((uint32_t)from_f32<ACT>(acc[1]) << 16);
-    const uint32_t hi = from_f32<ACT>(acc[2]) | ((uint32_t)from_f32<ACT>(acc[3]) << 16);
-    *reinterpret_cast<u32x2_t*>(y + (size_t)t * H + h) = u32x2_t{lo, hi};
+    uint32_t o[V / 2];
+#pragma unroll
+    for (int q = 0; q < V / 2; ++q)
+      o[q] = from_f32<ACT>(acc[2 * q]) | ((uint32_t)from_f32<ACT>(acc[2 * q + 1]) << 16);
+    if constexpr (E16)
+      *reinterpret_cast<u32x4_t*>(y + (size_t)t * H + h) = u32x4_t{o[0], o[1], o[2], o[3]};
+    else
+      *reinterpret_cast<u32x2_t*>(y + (size_t)t * H + h) = u32x2_t{o[0], o[1]};
   }
 }
 
+// eout16 requires H % 8 == 0 (the W4A16 layouts have H % 128 == 0).
 hipError_t launch_combine(const float* eout, const float* tw, const int32_t* ids, void* y, int T,
-                          int K, int E, int H, int act, hipStream_t st) {
-  const int64_t total = (int64_t)T * (H / 4);
+                          int K, int E, int H, int act, hipStream_t st, bool eout16) {
+  const int64_t total = (int64_t)T * (H / (eout16 ? 8 : 4));
   if (total == 0) return hipSuccess;
   int64_t grid = (total + 255) / 256;
   if (grid > 65536) grid = 65536;
-  if (act == 1)
-    hipLaunchKernelGGL(combine_kernel<1>, dim3((unsigned)grid), dim3(256), 0, st, eout, tw, ids,
-                       (uint16_t*)y, T, K, E, H);
-  else
-    hipLaunchKernelGGL(combine_kernel<0>, dim3((unsigned)grid), dim3(256), 0, st, eout, tw, ids,
-                       (uint16_t*)y, T, K, E, H);
+  auto kern = act == 1 ? (eout16 ? combine_kernel<1, true> : combine_kernel<1, false>)
+                       : (eout16 ? combine_kernel<0, true> : combine_kernel<0, false>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, st, eout, tw, ids, (uint16_t*)y, T, K, E, H);
   return hipGetLastError();
 }
 

@@ -528,7 +528,9 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm13_kernel(const int32_t* nti
 // 64 rows); wave w owns the 16-row tile 64m + 16w of each quad, so a staged
 // activation row serves kGemm2Quads weight tiles (the rows are re-staged by
 // every workgroup of the tile: 2 quads halve that traffic).  eout[pair] gets
-// the tiles' fp32 values; the combine kernel sums over k.
+// the tiles' values rounded to the activation dtype (the precision of the
+// act rows they come from; half the fp32 bytes written here and read by the
+// combine kernel, which sums over k in fp32).
 template <int ACT, int SDT>
 __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(const int32_t* ntiles, const int32_t* tiles,
                                                             const int32_t* tok, const uint16_t* act, const void* w2,
@@ -614,6 +616,7 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(const int32_t* ntil
     for (int p = 0; p < kGemm2Quads; ++p) wc[p] = wn[p];
     __syncthreads();
   }
+  uint16_t* eout = reinterpret_cast<uint16_t*>(c.eout);
 #pragma unroll
   for (int p = 0; p < kGemm2Quads; ++p)
 #pragma unroll
@@ -623,7 +626,7 @@ __global__ __launch_bounds__(kBlock) void w4a16_gemm2_kernel(const int32_t* ntil
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int row = 16 * s + 4 * q + v;
-          if (row < rows) c.eout[(size_t)pairs[row] * H + 64 * (m0 + p) + 16 * wave + r] = vv[v];
+          if (row < rows) eout[(size_t)pairs[row] * H + 64 * (m0 + p) + 16 * wave + r] = from_f32<ACT>(vv[v]);
         }
       }
     }
