@@ -89,10 +89,7 @@ __device__ void route_finish(int* counts, int E, int lane, int32_t* counts_out, 
         for (int r0 = 0; r0 < c; r0 += kGemmRows) {
           const int rows = min(kGemmRows, c - r0), k = lpt ? tile_class(rows) : 0;
           const int tx = k == 0 ? x0++ : k == 1 ? x1++ : k == 2 ? x2++ : x3++;
-          tiles_out[4 * tx + 0] = e;
-          tiles_out[4 * tx + 1] = sx + r0;
-          tiles_out[4 * tx + 2] = rows;
-          tiles_out[4 * tx + 3] = 0;
+          *reinterpret_cast<int4*>(tiles_out + 4 * tx) = int4{e, sx + r0, rows, 0};
         }
       sx += c;
     }
